@@ -1,0 +1,212 @@
+// GEMM entry points: catopt_hip_linear and catopt_hip_matmul.
+//
+// bf16 with K-contiguous, 16-byte aligned operands goes to the 256x256
+// bf16 MFMA kernel (gemm_bf16.hip).  Everything else — fp32 (the weight
+// chain of the linear-bias association form and its construction-time
+// fold), transposed operands, unaligned views — runs here on a 64x64-tile
+// kernel using the 32x32x2 fp32 MFMA, with operands staged through LDS in
+// k-contiguous order whatever their global layout.  bf16 operands are
+// widened to fp32 in LDS (the products are exact), so both paths
+// accumulate in fp32.
+#include "common.hpp"
+
+namespace catopt {
+bool gemm_bf16_nt_fast_ok(int64_t M, int64_t N, int64_t K, const void* x, int64_t ldx,
+                          const void* w, int64_t ldw, const void* y, int64_t ldy);
+int32_t gemm_bf16_nt_launch(int32_t epi, int64_t M, int64_t N, int64_t K, const void* x,
+                            int64_t ldx, const void* w, int64_t ldw, const void* bias,
+                            const void* bias2, void* y, int64_t ldy, int64_t batch,
+                            int64_t strideA, int64_t strideB, int64_t strideC, hipStream_t s);
+
+namespace {
+
+constexpr int TM = 64, TN = 64, TK = 32, NTH = 256;
+
+__device__ __forceinline__ f32x16 mfma32x32x2f32(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// C[b] = epi(op(A[b]) op(B[b])).  TA: A stored K x M.  TB: B stored N x K
+// (the linear-weight layout) — TB=false means B stored K x N.
+// Paired epilogues read B rows n and n + N (TB must be true).
+template <typename T, bool TA, bool TB, int EPI>
+__global__ __launch_bounds__(NTH) void gemm_generic(
+    const T* __restrict__ A, int64_t lda, int64_t sA, const T* __restrict__ B, int64_t ldb,
+    int64_t sB, const T* __restrict__ bias, const T* __restrict__ bias2, T* __restrict__ C,
+    int64_t ldc, int64_t sC, int M, int N, int K) {
+  constexpr bool PAIRED = (EPI == CATOPT_EPI_SILU_MUL || EPI == CATOPT_EPI_GLU);
+  constexpr int BROWS = PAIRED ? 2 * TN : TN;
+  __shared__ float As[TM][TK + 1];
+  __shared__ float Bs[BROWS][TK + 1];
+  const int64_t bz = blockIdx.z;
+  A += bz * sA;
+  B += bz * sB;
+  C += bz * sC;
+  const int m0 = blockIdx.y * TM, n0 = blockIdx.x * TN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l32 = lane & 31, g = lane >> 5;
+
+  f32x16 acc0, acc1;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc0[r] = acc1[r] = 0.f;
+
+  for (int k0 = 0; k0 < K; k0 += TK) {
+    // A tile -> As[m][k]
+    for (int e = tid; e < TM * TK; e += NTH) {
+      int m, k;
+      if (TA) { k = e / TM; m = e % TM; } else { m = e / TK; k = e % TK; }
+      const int gm = m0 + m, gk = k0 + k;
+      float v = 0.f;
+      if (gm < M && gk < K) v = load_f32(A, TA ? (int64_t)gk * lda + gm : (int64_t)gm * lda + gk);
+      As[m][k] = v;
+    }
+    // B tile -> Bs[n][k]
+    for (int e = tid; e < BROWS * TK; e += NTH) {
+      int n, k;
+      if (TB) { n = e / TK; k = e % TK; } else { k = e / BROWS; n = e % BROWS; }
+      int gn;
+      bool ok;
+      if (PAIRED) {
+        const int half = n / TN, nn = n % TN;
+        ok = n0 + nn < N;
+        gn = n0 + nn + half * N;
+      } else {
+        gn = n0 + n;
+        ok = gn < N;
+      }
+      const int gk = k0 + k;
+      float v = 0.f;
+      if (ok && gk < K) v = load_f32(B, TB ? (int64_t)gn * ldb + gk : (int64_t)gk * ldb + gn);
+      Bs[n][k] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < TK; kk += 2) {
+      const float a = As[wm * 32 + l32][kk + g];
+      const float b0 = Bs[wn * 32 + l32][kk + g];
+      acc0 = mfma32x32x2f32(a, b0, acc0);
+      if (PAIRED) {
+        const float b1 = Bs[TN + wn * 32 + l32][kk + g];
+        acc1 = mfma32x32x2f32(a, b1, acc1);
+      }
+    }
+    __syncthreads();
+  }
+
+  const int n = n0 + wn * 32 + l32;
+  if (n >= N) return;
+  float badd = 0.f, badd2 = 0.f;
+  if (EPI == CATOPT_EPI_BIAS || EPI == CATOPT_EPI_BIAS_ADD2) badd = load_f32(bias, n);
+  if (EPI == CATOPT_EPI_BIAS_ADD2) badd2 = load_f32(bias2, n);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int m = m0 + wm * 32 + acc_row(r, g);
+    if (m >= M) continue;
+    float o;
+    if (EPI == CATOPT_EPI_SILU_MUL) o = silu_f(acc0[r]) * acc1[r];
+    else if (EPI == CATOPT_EPI_GLU) o = acc0[r] * sigmoid_f(acc1[r]);
+    else o = (acc0[r] + badd) + badd2;
+    store_f32(C, (int64_t)m * ldc + n, o);
+  }
+}
+
+template <typename T, bool TA, bool TB, int EPI>
+int32_t launch_generic(const void* A, int64_t lda, int64_t sA, const void* B, int64_t ldb,
+                       int64_t sB, const void* bias, const void* bias2, void* C, int64_t ldc,
+                       int64_t sC, int64_t batch, int64_t M, int64_t N, int64_t K, hipStream_t s) {
+  const int64_t gx = (N + TN - 1) / TN, gy = (M + TM - 1) / TM;
+  if (gx > 0x7fffffff || gy > 65535 || batch > 65535) return CATOPT_E_UNSUPPORTED;
+  gemm_generic<T, TA, TB, EPI><<<dim3((uint32_t)gx, (uint32_t)gy, (uint32_t)batch), dim3(NTH), 0, s>>>(
+      static_cast<const T*>(A), lda, sA, static_cast<const T*>(B), ldb, sB,
+      static_cast<const T*>(bias), static_cast<const T*>(bias2), static_cast<T*>(C), ldc, sC,
+      (int)M, (int)N, (int)K);
+  CATOPT_LAUNCH_CHECK();
+  return CATOPT_OK;
+}
+
+template <typename T, bool TA, bool TB>
+int32_t dispatch_epi(int32_t epi, const void* A, int64_t lda, int64_t sA, const void* B,
+                     int64_t ldb, int64_t sB, const void* bias, const void* bias2, void* C,
+                     int64_t ldc, int64_t sC, int64_t batch, int64_t M, int64_t N, int64_t K,
+                     hipStream_t s) {
+  switch (epi) {
+    case CATOPT_EPI_NONE:
+      return launch_generic<T, TA, TB, CATOPT_EPI_NONE>(A, lda, sA, B, ldb, sB, bias, bias2, C, ldc, sC, batch, M, N, K, s);
+    case CATOPT_EPI_BIAS:
+      return launch_generic<T, TA, TB, CATOPT_EPI_BIAS>(A, lda, sA, B, ldb, sB, bias, bias2, C, ldc, sC, batch, M, N, K, s);
+    case CATOPT_EPI_BIAS_ADD2:
+      return launch_generic<T, TA, TB, CATOPT_EPI_BIAS_ADD2>(A, lda, sA, B, ldb, sB, bias, bias2, C, ldc, sC, batch, M, N, K, s);
+    default:
+      return CATOPT_E_INVAL;
+  }
+}
+
+template <typename T>
+int32_t dispatch_paired(int32_t epi, const void* A, int64_t lda, const void* B, int64_t ldb,
+                        void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, hipStream_t s) {
+  if (epi == CATOPT_EPI_SILU_MUL)
+    return launch_generic<T, false, true, CATOPT_EPI_SILU_MUL>(A, lda, 0, B, ldb, 0, nullptr, nullptr, C, ldc, 0, 1, M, N, K, s);
+  return launch_generic<T, false, true, CATOPT_EPI_GLU>(A, lda, 0, B, ldb, 0, nullptr, nullptr, C, ldc, 0, 1, M, N, K, s);
+}
+
+}  // namespace
+}  // namespace catopt
+
+using namespace catopt;
+
+extern "C" int32_t catopt_hip_linear(int32_t dtype, int64_t M, int64_t N, int64_t K,
+                                     const void* x, int64_t ldx, const void* w, int64_t ldw,
+                                     const void* bias, const void* bias2, int32_t epilogue,
+                                     void* y, int64_t ldy, void* stream) {
+  if (M < 0 || N < 0 || K < 0) return CATOPT_E_INVAL;
+  if (epilogue < CATOPT_EPI_NONE || epilogue > CATOPT_EPI_GLU) return CATOPT_E_INVAL;
+  if (dtype != CATOPT_F32 && dtype != CATOPT_BF16) return CATOPT_E_UNSUPPORTED;
+  if (M == 0 || N == 0) return CATOPT_OK;
+  if (K == 0) return CATOPT_E_UNSUPPORTED;  // an empty contraction: leave to the caller
+  if (!x || !w || !y || ldx < K || ldw < K || ldy < N) return CATOPT_E_INVAL;
+  const bool paired = epilogue == CATOPT_EPI_SILU_MUL || epilogue == CATOPT_EPI_GLU;
+  if ((epilogue == CATOPT_EPI_BIAS || epilogue == CATOPT_EPI_BIAS_ADD2) && !bias) return CATOPT_E_INVAL;
+  if (epilogue == CATOPT_EPI_BIAS_ADD2 && !bias2) return CATOPT_E_INVAL;
+  if (M > 0x7fffffffLL || N > 0x3fffffffLL || K > 0x7fffffffLL) return CATOPT_E_UNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == CATOPT_BF16 && gemm_bf16_nt_fast_ok(M, N, K, x, ldx, w, ldw, y, ldy))
+    return gemm_bf16_nt_launch(epilogue, M, N, K, x, ldx, w, ldw, bias, bias2, y, ldy, 1, 0, 0, 0, s);
+  if (paired) {
+    return dtype == CATOPT_BF16 ? dispatch_paired<uint16_t>(epilogue, x, ldx, w, ldw, y, ldy, M, N, K, s)
+                                : dispatch_paired<float>(epilogue, x, ldx, w, ldw, y, ldy, M, N, K, s);
+  }
+  return dtype == CATOPT_BF16
+             ? dispatch_epi<uint16_t, false, true>(epilogue, x, ldx, 0, w, ldw, 0, bias, bias2, y, ldy, 0, 1, M, N, K, s)
+             : dispatch_epi<float, false, true>(epilogue, x, ldx, 0, w, ldw, 0, bias, bias2, y, ldy, 0, 1, M, N, K, s);
+}
+
+extern "C" int32_t catopt_hip_matmul(int32_t dtype, int64_t batch, int64_t M, int64_t N,
+                                     int64_t K, const void* A, int64_t lda, int64_t strideA,
+                                     int32_t transA, const void* B, int64_t ldb, int64_t strideB,
+                                     int32_t transB, void* C, int64_t ldc, int64_t strideC,
+                                     void* stream) {
+  if (batch < 0 || M < 0 || N < 0 || K < 0) return CATOPT_E_INVAL;
+  if (dtype != CATOPT_F32 && dtype != CATOPT_BF16) return CATOPT_E_UNSUPPORTED;
+  if (batch == 0 || M == 0 || N == 0) return CATOPT_OK;
+  if (K == 0) return CATOPT_E_UNSUPPORTED;
+  if (!A || !B || !C || ldc < N) return CATOPT_E_INVAL;
+  if ((transA ? lda < M : lda < K) || (transB ? ldb < K : ldb < N)) return CATOPT_E_INVAL;
+  if (M > 0x7fffffffLL || N > 0x3fffffffLL || K > 0x7fffffffLL) return CATOPT_E_UNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool strides_ok = strideA % 8 == 0 && strideB % 8 == 0;
+  if (dtype == CATOPT_BF16 && !transA && transB && strides_ok &&
+      gemm_bf16_nt_fast_ok(M, N, K, A, lda, B, ldb, C, ldc))
+    return gemm_bf16_nt_launch(CATOPT_EPI_NONE, M, N, K, A, lda, B, ldb, nullptr, nullptr, C, ldc,
+                               batch, strideA, strideB, strideC, s);
+#define CATOPT_MM(T)                                                                                          \
+  if (!transA && !transB) return dispatch_epi<T, false, false>(0, A, lda, strideA, B, ldb, strideB, nullptr, nullptr, C, ldc, strideC, batch, M, N, K, s); \
+  if (!transA && transB) return dispatch_epi<T, false, true>(0, A, lda, strideA, B, ldb, strideB, nullptr, nullptr, C, ldc, strideC, batch, M, N, K, s);   \
+  if (transA && !transB) return dispatch_epi<T, true, false>(0, A, lda, strideA, B, ldb, strideB, nullptr, nullptr, C, ldc, strideC, batch, M, N, K, s);   \
+  return dispatch_epi<T, true, true>(0, A, lda, strideA, B, ldb, strideB, nullptr, nullptr, C, ldc, strideC, batch, M, N, K, s);
+  if (dtype == CATOPT_BF16) {
+    CATOPT_MM(uint16_t)
+  }
+  CATOPT_MM(float)
+#undef CATOPT_MM
+}

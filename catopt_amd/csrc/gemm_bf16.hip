@@ -1,0 +1,269 @@
+// bf16 "NT" GEMM on gfx950 MFMA with fused epilogues.
+//
+//   C[m, n] = epi( sum_k A[m, k] * B[n, k] )
+//
+// A is the activation (rows of length K, K contiguous), B the weight in
+// nn.Linear layout (out_features x in_features, K contiguous): both operands
+// are K-contiguous, which is the layout the 32x32x16 MFMA consumes directly
+// (each lane supplies 8 consecutive k of one row/column).
+//
+// Tiling: 256x256 block tile, BK = 64, 4 waves in a 2x2 grid, each wave a
+// 128x128 sub-tile = 4x4 MFMA blocks (256 fp32 accumulators per lane).  The
+// K loop is double buffered: global loads for tile k+1 are issued into
+// registers before the MFMAs of tile k, then stored to the other LDS stage,
+// one barrier per K tile.  LDS rows are 128 B (64 bf16) with the 16-byte
+// chunk index XOR-swizzled by (row & 7) so that both the row-wise stores and
+// the MFMA fragment reads are bank-conflict free.
+//
+// Paired epilogues (SILU_MUL / GLU): the B tile holds 128 rows of the first
+// projection and the 128 matching rows of the second (row n and row n + N of
+// the concatenated weight), so every wave owns both halves of its output
+// columns and the gate is applied in registers — the chunk/silu/mul of the
+// SWIGLU_FUSE form never touch HBM.
+//
+// Block-to-tile mapping is XCD-aware: the hardware deals workgroups round
+// robin over 8 XCDs, so consecutive logical tiles (grouped 8 M-tiles at a
+// time) are gathered onto the same XCD to share its L2.
+#include "common.hpp"
+
+namespace catopt {
+namespace {
+
+constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int NT = 256;
+constexpr int STAGE_ELEMS = (BM + BN) * BK;              // bf16 elements per stage
+constexpr int LDS_BYTES = 2 * STAGE_ELEMS * 2;           // two stages
+
+__device__ __forceinline__ int swz(int row, int chunk) {  // element offset of chunk in LDS
+  return row * BK + ((chunk ^ (row & 7)) << 3);
+}
+
+struct TileMap {
+  int tm, tn;
+};
+
+__device__ __forceinline__ TileMap map_tile(int tiles_m, int tiles_n) {
+  int bid = blockIdx.x;
+  const int nb = gridDim.x;
+  if ((nb & 7) == 0) {
+    const int xcd = bid & 7, loc = bid >> 3;
+    bid = xcd * (nb >> 3) + loc;
+  }
+  constexpr int GM = 8;
+  const int per_group = GM * tiles_n;
+  const int group = bid / per_group;
+  const int first_m = group * GM;
+  const int gsize = min(tiles_m - first_m, GM);
+  const int in_group = bid - group * per_group;
+  TileMap t;
+  t.tm = first_m + in_group % gsize;
+  t.tn = in_group / gsize;
+  return t;
+}
+
+template <int EPI>
+__global__ __launch_bounds__(NT) void gemm_bf16_nt(
+    const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb,
+    const uint16_t* __restrict__ bias, const uint16_t* __restrict__ bias2,
+    uint16_t* __restrict__ C, int64_t ldc, int M, int N, int K, int tiles_m, int tiles_n,
+    int64_t sA, int64_t sB, int64_t sC) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  A += (int64_t)blockIdx.y * sA;
+  B += (int64_t)blockIdx.y * sB;
+  C += (int64_t)blockIdx.y * sC;
+  constexpr bool PAIRED = (EPI == CATOPT_EPI_SILU_MUL || EPI == CATOPT_EPI_GLU);
+  const TileMap tile = map_tile(tiles_m, tiles_n);
+  const int m0 = tile.tm * BM;
+  // n0: first output column of this tile; B rows for the tile start at n0
+  // (and at N + n0 for the second projection of a paired epilogue).
+  const int n0 = tile.tn * (PAIRED ? BN / 2 : BN);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l32 = lane & 31, g = lane >> 5;
+
+  // Global load assignment: 8 threads per 128-byte row slice, 32 rows per pass.
+  const int ld_row = tid >> 3, ld_chunk = tid & 7;
+  const uint16_t* a_src[8];
+  bool a_ok[8];
+  const uint16_t* b_src[8];
+  bool b_ok[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = ld_row + 32 * i;
+    const int am = m0 + r;
+    a_ok[i] = am < M;
+    a_src[i] = A + (int64_t)(a_ok[i] ? am : 0) * lda + ld_chunk * 8;
+    int bn;
+    bool ok;
+    if (PAIRED) {
+      const int half = r >> 7, rr = r & 127;
+      ok = n0 + rr < N;
+      bn = (ok ? n0 + rr : 0) + half * N;
+    } else {
+      bn = n0 + r;
+      ok = bn < N;
+      if (!ok) bn = 0;
+    }
+    b_ok[i] = ok;
+    b_src[i] = B + (int64_t)bn * ldb + ld_chunk * 8;
+  }
+
+  u32x4 ra[8], rb[8];
+  auto gload = [&](int k0) {
+    const bool kin = k0 + ld_chunk * 8 < K;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      ra[i] = (a_ok[i] && kin) ? *reinterpret_cast<const u32x4*>(a_src[i] + k0) : u32x4{0, 0, 0, 0};
+      rb[i] = (b_ok[i] && kin) ? *reinterpret_cast<const u32x4*>(b_src[i] + k0) : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto sstore = [&](int stage) {
+    uint16_t* As = lds + stage * STAGE_ELEMS;
+    uint16_t* Bs = As + BM * BK;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = ld_row + 32 * i;
+      *reinterpret_cast<u32x4*>(As + swz(r, ld_chunk)) = ra[i];
+      *reinterpret_cast<u32x4*>(Bs + swz(r, ld_chunk)) = rb[i];
+    }
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  // B-tile row of the wave's column block j.
+  auto brow = [&](int j) {
+    return PAIRED ? (j >> 1) * 128 + wn * 64 + (j & 1) * 32 : wn * 128 + j * 32;
+  };
+
+  const int ktiles = (K + BK - 1) / BK;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < ktiles) gload((kt + 1) * BK);
+    const uint16_t* As = lds + cur * STAGE_ELEMS;
+    const uint16_t* Bs = As + BM * BK;
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      bf16x8 af[4], bfr[4];
+      const int chunk = 2 * ks + g;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        af[i] = *reinterpret_cast<const bf16x8*>(As + swz(wm * 128 + i * 32 + l32, chunk));
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        bfr[j] = *reinterpret_cast<const bf16x8*>(Bs + swz(brow(j) + l32, chunk));
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma32x32x16(af[i], bfr[j], acc[i][j]);
+    }
+    if (kt + 1 < ktiles) sstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: lane owns output column (l32) of each 32-wide block and 16 rows.
+  if (PAIRED) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + wn * 64 + j * 32 + l32;
+      if (n >= N) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm * 128 + i * 32 + acc_row(r, g);
+          if (m >= M) continue;
+          const float a = acc[i][j][r], b = acc[i][j + 2][r];
+          const float o = (EPI == CATOPT_EPI_SILU_MUL) ? silu_f(a) * b : a * sigmoid_f(b);
+          C[(int64_t)m * ldc + n] = f32_to_bf16(o);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + wn * 128 + j * 32 + l32;
+      if (n >= N) continue;
+      float badd = 0.f;
+      if (EPI == CATOPT_EPI_BIAS || EPI == CATOPT_EPI_BIAS_ADD2) badd = bf16_to_f32(bias[n]);
+      float badd2 = 0.f;
+      if (EPI == CATOPT_EPI_BIAS_ADD2) badd2 = bf16_to_f32(bias2[n]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm * 128 + i * 32 + acc_row(r, g);
+          if (m >= M) continue;
+          float o = acc[i][j][r];
+          if (EPI == CATOPT_EPI_BIAS || EPI == CATOPT_EPI_BIAS_ADD2) o += badd;
+          if (EPI == CATOPT_EPI_BIAS_ADD2) o += badd2;
+          C[(int64_t)m * ldc + n] = f32_to_bf16(o);
+        }
+      }
+    }
+  }
+}
+
+template <int EPI>
+int32_t launch(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb,
+               const uint16_t* bias, const uint16_t* bias2, uint16_t* C, int64_t ldc, int M,
+               int N, int K, int64_t batch, int64_t sA, int64_t sB, int64_t sC, hipStream_t s) {
+  constexpr bool PAIRED = (EPI == CATOPT_EPI_SILU_MUL || EPI == CATOPT_EPI_GLU);
+  static bool attr_done = false;  // idempotent; benign race (same value written)
+  if (!attr_done) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_bf16_nt<EPI>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
+    if (e != hipSuccess) return set_hip_error(e);
+    attr_done = true;
+  }
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = (N + (PAIRED ? BN / 2 : BN) - 1) / (PAIRED ? BN / 2 : BN);
+  const int64_t nblocks = (int64_t)tiles_m * tiles_n;
+  if (nblocks > 0x7fffffff || batch > 65535) return CATOPT_E_UNSUPPORTED;
+  gemm_bf16_nt<EPI><<<dim3((uint32_t)nblocks, (uint32_t)batch), dim3(NT), LDS_BYTES, s>>>(
+      A, lda, B, ldb, bias, bias2, C, ldc, M, N, K, tiles_m, tiles_n, sA, sB, sC);
+  CATOPT_LAUNCH_CHECK();
+  return CATOPT_OK;
+}
+
+}  // namespace
+
+// Fast-path predicate shared with the dispatcher in gemm.hip.
+bool gemm_bf16_nt_fast_ok(int64_t M, int64_t N, int64_t K, const void* x, int64_t ldx,
+                          const void* w, int64_t ldw, const void* y, int64_t ldy) {
+  return M > 0 && N > 0 && K > 0 && M < (1LL << 31) && N < (1LL << 30) && K < (1LL << 31) &&
+         K % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0 && aligned16(x) && aligned16(w) &&
+         ldy >= 1 && y != nullptr;
+}
+
+int32_t gemm_bf16_nt_launch(int32_t epi, int64_t M, int64_t N, int64_t K, const void* x,
+                            int64_t ldx, const void* w, int64_t ldw, const void* bias,
+                            const void* bias2, void* y, int64_t ldy, int64_t batch,
+                            int64_t sA, int64_t sB, int64_t sC, hipStream_t s) {
+  auto A = static_cast<const uint16_t*>(x);
+  auto B = static_cast<const uint16_t*>(w);
+  auto b1 = static_cast<const uint16_t*>(bias);
+  auto b2 = static_cast<const uint16_t*>(bias2);
+  auto C = static_cast<uint16_t*>(y);
+  switch (epi) {
+    case CATOPT_EPI_NONE: return launch<CATOPT_EPI_NONE>(A, ldx, B, ldw, b1, b2, C, ldy, (int)M, (int)N, (int)K, batch, sA, sB, sC, s);
+    case CATOPT_EPI_BIAS: return launch<CATOPT_EPI_BIAS>(A, ldx, B, ldw, b1, b2, C, ldy, (int)M, (int)N, (int)K, batch, sA, sB, sC, s);
+    case CATOPT_EPI_BIAS_ADD2: return launch<CATOPT_EPI_BIAS_ADD2>(A, ldx, B, ldw, b1, b2, C, ldy, (int)M, (int)N, (int)K, batch, sA, sB, sC, s);
+    case CATOPT_EPI_SILU_MUL: return launch<CATOPT_EPI_SILU_MUL>(A, ldx, B, ldw, b1, b2, C, ldy, (int)M, (int)N, (int)K, batch, sA, sB, sC, s);
+    case CATOPT_EPI_GLU: return launch<CATOPT_EPI_GLU>(A, ldx, B, ldw, b1, b2, C, ldy, (int)M, (int)N, (int)K, batch, sA, sB, sC, s);
+    default: return CATOPT_E_INVAL;
+  }
+}
+
+}  // namespace catopt

@@ -1,0 +1,389 @@
+// Diagonal affine scans on gfx950 (fp32).
+//
+// Both kernels are HBM-streaming: every lane owns state elements and walks
+// the time axis.  The loads of a block of U steps are issued one block ahead
+// of the arithmetic (register double buffering), so each wave keeps
+// U x 16 B x 64 lanes of reads in flight while it computes.
+//
+// Schedules (the int64 chunk table chunk_starts[0..n] cuts [0, T)):
+//   STREAM  — one pass; a lane walks the chunks in table order.  HBM-optimal
+//             (a is read once) and used whenever the lanes fill the GPU.
+//   CHUNKED — three launches: (1) every chunk composes its own map
+//             (P = prod a, H = local state from 0), chunk-parallel;
+//             (2) per lane, fold the carries over chunks in table order,
+//             leaving the carry-in of each chunk in the workspace;
+//             (3) every chunk re-runs from its carry-in and emits outputs.
+//             This is the two-level blocked scan of the reference's
+//             all-prefix path; it trades a second read of the inputs for
+//             chunk-level parallelism when B*D*N alone cannot fill the GPU.
+#include "common.hpp"
+
+namespace catopt {
+namespace {
+
+constexpr int kThreads = 256;
+
+// Chunk bounds clamped to [0, T]: a malformed table can only shorten the
+// walk, never index outside the inputs (the host validates the table too).
+__device__ __forceinline__ int64_t cclamp(int64_t v, int64_t T) { return v < 0 ? 0 : (v > T ? T : v); }
+
+// ---------------------------------------------------------------- affd scan
+// h_t = a_t * h_{t-1} + u_t over [t0, t1) for lane s.
+__device__ __forceinline__ float affd_run(const float* __restrict__ a, int64_t lda,
+                                          const float* __restrict__ u, int64_t ldu,
+                                          float* __restrict__ states, int64_t S, int64_t s,
+                                          int64_t t0, int64_t t1, float h, float* prod) {
+  constexpr int U = 8;
+  float p = 1.f;
+  int64_t t = t0;
+  for (; t + U <= t1; t += U) {
+    float av[U], uv[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      av[i] = a[(t + i) * lda + s];
+      uv[i] = u[(t + i) * ldu + s];
+    }
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      h = av[i] * h + uv[i];
+      p *= av[i];
+      if (states) states[(t + i) * S + s] = h;
+    }
+  }
+  for (; t < t1; ++t) {
+    const float av = a[t * lda + s];
+    h = av * h + u[t * ldu + s];
+    p *= av;
+    if (states) states[t * S + s] = h;
+  }
+  if (prod) *prod = p;
+  return h;
+}
+
+__global__ __launch_bounds__(kThreads) void affd_stream(
+    const float* __restrict__ a, int64_t lda, const float* __restrict__ u, int64_t ldu,
+    const float* __restrict__ h0, const int64_t* __restrict__ cs, int64_t nc, int64_t T, int64_t S,
+    float* __restrict__ states, float* __restrict__ hf) {
+  const int64_t s = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (s >= S) return;
+  float h = h0 ? h0[s] : 0.f;
+  for (int64_t c = 0; c < nc; ++c)
+    h = affd_run(a, lda, u, ldu, states, S, s, cclamp(cs[c], T), cclamp(cs[c + 1], T), h, nullptr);
+  if (hf) hf[s] = h;
+}
+
+// Phase 1: ws_p[c, s] = prod of a over chunk c; ws_h[c, s] = chunk-local state.
+__global__ __launch_bounds__(kThreads) void affd_chunk_local(
+    const float* __restrict__ a, int64_t lda, const float* __restrict__ u, int64_t ldu,
+    const int64_t* __restrict__ cs, int64_t T, int64_t S, float* __restrict__ ws_p,
+    float* __restrict__ ws_h) {
+  const int64_t s = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const int64_t c = blockIdx.y;
+  if (s >= S) return;
+  float p;
+  const float h = affd_run(a, lda, u, ldu, nullptr, S, s, cclamp(cs[c], T), cclamp(cs[c + 1], T), 0.f, &p);
+  ws_p[c * S + s] = p;
+  ws_h[c * S + s] = h;
+}
+
+// Phase 2: carry fold; ws_h[c, s] becomes the state entering chunk c.
+__global__ __launch_bounds__(kThreads) void scan_carry(const float* __restrict__ h0, int64_t nc,
+                                                       int64_t S, const float* __restrict__ ws_p,
+                                                       float* __restrict__ ws_h,
+                                                       float* __restrict__ hf) {
+  const int64_t s = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (s >= S) return;
+  float cin = h0 ? h0[s] : 0.f;
+  for (int64_t c = 0; c < nc; ++c) {
+    const float p = ws_p[c * S + s], h = ws_h[c * S + s];
+    ws_h[c * S + s] = cin;
+    cin = p * cin + h;
+  }
+  if (hf) hf[s] = cin;
+}
+
+// Phase 3: re-run each chunk from its carry-in, writing the prefix states.
+__global__ __launch_bounds__(kThreads) void affd_chunk_apply(
+    const float* __restrict__ a, int64_t lda, const float* __restrict__ u, int64_t ldu,
+    const int64_t* __restrict__ cs, int64_t T, int64_t S, const float* __restrict__ ws_h,
+    float* __restrict__ states) {
+  const int64_t s = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const int64_t c = blockIdx.y;
+  if (s >= S) return;
+  affd_run(a, lda, u, ldu, states, S, s, cclamp(cs[c], T), cclamp(cs[c + 1], T), ws_h[c * S + s], nullptr);
+}
+
+// ---------------------------------------------------------------- SSM scan
+// Thread layout: TPD = N/4 threads per channel d, each owning 4 consecutive
+// state elements n (one 16-byte load of a per step); DPW = 256/TPD channels
+// per workgroup; grid.y = batch.  y[b,t,d] is reduced across the TPD lanes
+// of a channel with xor shuffles (DPP quad-perm / ds_swizzle patterns).
+template <int N>
+struct SsmLayout {
+  static constexpr int TPD = N / 4;
+  static constexpr int DPW = kThreads / TPD;
+};
+
+template <int N, bool APS>
+struct SsmStep {
+  f32x4 a;
+  f32x4 bx;
+  f32x4 c;
+  float x;
+};
+
+template <int N, bool APS>
+__device__ __forceinline__ void ssm_load(SsmStep<N, APS>& st, const float* __restrict__ a,
+                                         const float* __restrict__ bx,
+                                         const float* __restrict__ c,
+                                         const float* __restrict__ x, int64_t b, int64_t t,
+                                         int64_t T, int64_t D, int64_t d, int n0) {
+  const int64_t bt = b * T + t;
+  if (APS) {
+    st.a = *reinterpret_cast<const f32x4*>(a + (bt * D + d) * N + n0);
+  } else {
+    const float av = a[bt * D + d];
+    st.a = f32x4{av, av, av, av};
+  }
+  st.bx = *reinterpret_cast<const f32x4*>(bx + bt * N + n0);
+  st.c = *reinterpret_cast<const f32x4*>(c + bt * N + n0);
+  st.x = x[bt * D + d];
+}
+
+template <int N>
+__device__ __forceinline__ float lane_reduce(float p) {
+#pragma unroll
+  for (int o = 1; o < SsmLayout<N>::TPD; o <<= 1) p += __shfl_xor(p, o, 64);
+  return p;
+}
+
+// Run steps [t0, t1) from state h; optionally emit y and the product of a.
+template <int N, bool APS, bool EMIT>
+__device__ __forceinline__ f32x4 ssm_run(const float* __restrict__ a,
+                                         const float* __restrict__ bx,
+                                         const float* __restrict__ c,
+                                         const float* __restrict__ x, float* __restrict__ y,
+                                         int64_t b, int64_t T, int64_t D, int64_t d, bool dok,
+                                         int n0, int64_t t0, int64_t t1, f32x4 h, f32x4* prod) {
+  constexpr int U = 8;
+  const int64_t dd = dok ? d : 0;  // out-of-range channels shadow channel 0, never store
+  f32x4 p = f32x4{1.f, 1.f, 1.f, 1.f};
+  SsmStep<N, APS> cur[U], nxt[U];
+  int64_t t = t0;
+  if (t + U <= t1) {
+#pragma unroll
+    for (int i = 0; i < U; ++i) ssm_load(cur[i], a, bx, c, x, b, t + i, T, D, dd, n0);
+  }
+  for (; t + U <= t1; t += U) {
+    const bool more = t + 2 * U <= t1;
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < U; ++i) ssm_load(nxt[i], a, bx, c, x, b, t + U + i, T, D, dd, n0);
+    }
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      h = cur[i].a * h + cur[i].bx * cur[i].x;
+      if (!EMIT) p *= cur[i].a;
+      if (EMIT) {
+        const f32x4 ch = cur[i].c * h;
+        const float r = lane_reduce<N>(ch[0] + ch[1] + ch[2] + ch[3]);
+        if (dok && n0 == 0) y[(b * T + t + i) * D + d] = r;
+      }
+    }
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < U; ++i) cur[i] = nxt[i];
+    }
+  }
+  for (; t < t1; ++t) {
+    SsmStep<N, APS> st;
+    ssm_load(st, a, bx, c, x, b, t, T, D, dd, n0);
+    h = st.a * h + st.bx * st.x;
+    if (!EMIT) p *= st.a;
+    if (EMIT) {
+      const f32x4 ch = st.c * h;
+      const float r = lane_reduce<N>(ch[0] + ch[1] + ch[2] + ch[3]);
+      if (dok && n0 == 0) y[(b * T + t) * D + d] = r;
+    }
+  }
+  if (prod) *prod = p;
+  return h;
+}
+
+template <int N>
+struct SsmIdx {
+  int64_t d;
+  bool dok;
+  int n0;
+};
+
+template <int N>
+__device__ __forceinline__ SsmIdx<N> ssm_idx(int64_t D) {
+  SsmIdx<N> r;
+  const int tl = threadIdx.x;
+  r.d = (int64_t)blockIdx.x * SsmLayout<N>::DPW + tl / SsmLayout<N>::TPD;
+  r.dok = r.d < D;
+  r.n0 = (tl % SsmLayout<N>::TPD) * 4;
+  return r;
+}
+
+template <int N, bool APS>
+__global__ __launch_bounds__(kThreads) void ssm_stream(
+    const float* __restrict__ a, const float* __restrict__ bx, const float* __restrict__ c,
+    const float* __restrict__ x, const float* __restrict__ h0, const int64_t* __restrict__ cs,
+    int64_t nc, int64_t T, int64_t D, float* __restrict__ y, float* __restrict__ hf) {
+  const SsmIdx<N> ix = ssm_idx<N>(D);
+  const int64_t b = blockIdx.y;
+  f32x4 h = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int64_t sidx = (b * D + ix.d) * N + ix.n0;
+  if (h0 && ix.dok) h = *reinterpret_cast<const f32x4*>(h0 + sidx);
+  for (int64_t k = 0; k < nc; ++k)
+    h = ssm_run<N, APS, true>(a, bx, c, x, y, b, T, D, ix.d, ix.dok, ix.n0, cclamp(cs[k], T),
+                              cclamp(cs[k + 1], T), h, nullptr);
+  if (hf && ix.dok) *reinterpret_cast<f32x4*>(hf + sidx) = h;
+}
+
+template <int N, bool APS>
+__global__ __launch_bounds__(kThreads) void ssm_chunk_local(
+    const float* __restrict__ a, const float* __restrict__ bx, const float* __restrict__ c,
+    const float* __restrict__ x, const int64_t* __restrict__ cs, int64_t T, int64_t D,
+    int64_t S, float* __restrict__ ws_p, float* __restrict__ ws_h) {
+  const SsmIdx<N> ix = ssm_idx<N>(D);
+  const int64_t b = blockIdx.y, k = blockIdx.z;
+  f32x4 p;
+  const f32x4 h = ssm_run<N, APS, false>(a, bx, c, x, nullptr, b, T, D, ix.d, ix.dok, ix.n0,
+                                         cclamp(cs[k], T), cclamp(cs[k + 1], T),
+                                         f32x4{0.f, 0.f, 0.f, 0.f}, &p);
+  if (!ix.dok) return;
+  const int64_t sidx = (b * D + ix.d) * N + ix.n0;
+  *reinterpret_cast<f32x4*>(ws_p + k * S + sidx) = p;
+  *reinterpret_cast<f32x4*>(ws_h + k * S + sidx) = h;
+}
+
+template <int N, bool APS>
+__global__ __launch_bounds__(kThreads) void ssm_chunk_apply(
+    const float* __restrict__ a, const float* __restrict__ bx, const float* __restrict__ c,
+    const float* __restrict__ x, const int64_t* __restrict__ cs, int64_t T, int64_t D,
+    int64_t S, const float* __restrict__ ws_h, float* __restrict__ y) {
+  const SsmIdx<N> ix = ssm_idx<N>(D);
+  const int64_t b = blockIdx.y, k = blockIdx.z;
+  const int64_t sidx = (b * D + (ix.dok ? ix.d : 0)) * N + ix.n0;
+  const f32x4 h = *reinterpret_cast<const f32x4*>(ws_h + k * S + sidx);
+  ssm_run<N, APS, true>(a, bx, c, x, y, b, T, D, ix.d, ix.dok, ix.n0, cclamp(cs[k], T),
+                        cclamp(cs[k + 1], T), h, nullptr);
+}
+
+// Lanes that fill the GPU: 256 CUs x 8 waves x 64 lanes.
+constexpr int64_t kFillThreads = 256LL * 8 * 64;
+
+template <int N, bool APS>
+int32_t ssm_launch(int64_t B, int64_t T, int64_t D, const float* a, const float* bx,
+                   const float* c, const float* x, const float* h0, const int64_t* cs,
+                   int64_t nc, int32_t schedule, float* y, float* hf, void* ws, int64_t wsb,
+                   hipStream_t s) {
+  const int64_t gx = (D + SsmLayout<N>::DPW - 1) / SsmLayout<N>::DPW;
+  const int64_t S = B * D * N;
+  const int64_t threads = gx * kThreads * B;
+  bool chunked = schedule == CATOPT_SCAN_CHUNKED;
+  if (schedule == CATOPT_SCAN_AUTO) chunked = nc > 1 && threads < kFillThreads;
+  if (gx > 0x7fffffff || B > 65535 || nc > 65535) return CATOPT_E_UNSUPPORTED;
+  if (!chunked) {
+    ssm_stream<N, APS><<<dim3((uint32_t)gx, (uint32_t)B), dim3(kThreads), 0, s>>>(
+        a, bx, c, x, h0, cs, nc, T, D, y, hf);
+    CATOPT_LAUNCH_CHECK();
+    return CATOPT_OK;
+  }
+  if (!ws || wsb < catopt_hip_scan_workspace_bytes(S, nc)) return CATOPT_E_WORKSPACE;
+  float* ws_p = static_cast<float*>(ws);
+  float* ws_h = ws_p + nc * S;
+  ssm_chunk_local<N, APS><<<dim3((uint32_t)gx, (uint32_t)B, (uint32_t)nc), dim3(kThreads), 0, s>>>(
+      a, bx, c, x, cs, T, D, S, ws_p, ws_h);
+  CATOPT_LAUNCH_CHECK();
+  scan_carry<<<dim3((uint32_t)((S + kThreads - 1) / kThreads)), dim3(kThreads), 0, s>>>(
+      h0, nc, S, ws_p, ws_h, hf);
+  CATOPT_LAUNCH_CHECK();
+  ssm_chunk_apply<N, APS><<<dim3((uint32_t)gx, (uint32_t)B, (uint32_t)nc), dim3(kThreads), 0, s>>>(
+      a, bx, c, x, cs, T, D, S, ws_h, y);
+  CATOPT_LAUNCH_CHECK();
+  return CATOPT_OK;
+}
+
+}  // namespace
+}  // namespace catopt
+
+using namespace catopt;
+
+extern "C" int64_t catopt_hip_scan_workspace_bytes(int64_t S, int64_t n_chunks) {
+  if (S < 0 || n_chunks < 0) return -1;
+  return 2 * S * n_chunks * (int64_t)sizeof(float);
+}
+
+extern "C" int32_t catopt_hip_affd_scan(int64_t T, int64_t S, const float* a, int64_t lda,
+                                        const float* u, int64_t ldu, const float* h0,
+                                        const int64_t* chunk_starts, int64_t n_chunks,
+                                        int32_t schedule, float* states, float* h_final,
+                                        void* workspace, int64_t workspace_bytes, void* stream) {
+  if (T < 0 || S < 0 || n_chunks < 1 || lda < 0 || ldu < S) return CATOPT_E_INVAL;
+  if (lda != 0 && lda < S) return CATOPT_E_INVAL;
+  if (schedule < CATOPT_SCAN_AUTO || schedule > CATOPT_SCAN_CHUNKED) return CATOPT_E_INVAL;
+  if (S == 0) return CATOPT_OK;
+  if (!chunk_starts || (T > 0 && (!a || !u))) return CATOPT_E_INVAL;
+  if (S > 0x7fffffffLL * kThreads || n_chunks > 65535) return CATOPT_E_UNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t gx = (S + kThreads - 1) / kThreads;
+  bool chunked = schedule == CATOPT_SCAN_CHUNKED;
+  if (schedule == CATOPT_SCAN_AUTO) chunked = n_chunks > 1 && S < kFillThreads;
+  if (!chunked) {
+    affd_stream<<<dim3((uint32_t)gx), dim3(kThreads), 0, s>>>(a, lda, u, ldu, h0, chunk_starts,
+                                                              n_chunks, T, S, states, h_final);
+    CATOPT_LAUNCH_CHECK();
+    return CATOPT_OK;
+  }
+  if (!workspace || workspace_bytes < catopt_hip_scan_workspace_bytes(S, n_chunks))
+    return CATOPT_E_WORKSPACE;
+  float* ws_p = static_cast<float*>(workspace);
+  float* ws_h = ws_p + n_chunks * S;
+  affd_chunk_local<<<dim3((uint32_t)gx, (uint32_t)n_chunks), dim3(kThreads), 0, s>>>(
+      a, lda, u, ldu, chunk_starts, T, S, ws_p, ws_h);
+  CATOPT_LAUNCH_CHECK();
+  scan_carry<<<dim3((uint32_t)gx), dim3(kThreads), 0, s>>>(h0, n_chunks, S, ws_p, ws_h, h_final);
+  CATOPT_LAUNCH_CHECK();
+  if (states) {
+    affd_chunk_apply<<<dim3((uint32_t)gx, (uint32_t)n_chunks), dim3(kThreads), 0, s>>>(
+        a, lda, u, ldu, chunk_starts, T, S, ws_h, states);
+    CATOPT_LAUNCH_CHECK();
+  }
+  return CATOPT_OK;
+}
+
+extern "C" int32_t catopt_hip_ssm_scan(int64_t B, int64_t T, int64_t D, int64_t N,
+                                       const float* a, int32_t a_per_state, const float* bx,
+                                       const float* c, const float* x, const float* h0,
+                                       const int64_t* chunk_starts, int64_t n_chunks,
+                                       int32_t schedule, float* y, float* h_final,
+                                       void* workspace, int64_t workspace_bytes, void* stream) {
+  if (B < 0 || T < 0 || D < 0 || n_chunks < 1) return CATOPT_E_INVAL;
+  if (schedule < CATOPT_SCAN_AUTO || schedule > CATOPT_SCAN_CHUNKED) return CATOPT_E_INVAL;
+  if (B == 0 || D == 0) return CATOPT_OK;
+  if (!chunk_starts || (T > 0 && (!a || !bx || !c || !x || !y))) return CATOPT_E_INVAL;
+  if (!aligned16(a) && a_per_state) return CATOPT_E_INVAL;
+  if (!aligned16(bx) || !aligned16(c) || (h0 && !aligned16(h0)) || (h_final && !aligned16(h_final)))
+    return CATOPT_E_INVAL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define CATOPT_SSM(NN)                                                                                \
+  case NN:                                                                                            \
+    return a_per_state ? ssm_launch<NN, true>(B, T, D, a, bx, c, x, h0, chunk_starts, n_chunks,     \
+                                              schedule, y, h_final, workspace, workspace_bytes, s)  \
+                       : ssm_launch<NN, false>(B, T, D, a, bx, c, x, h0, chunk_starts, n_chunks,    \
+                                               schedule, y, h_final, workspace, workspace_bytes, s);
+  switch (N) {
+    CATOPT_SSM(4)
+    CATOPT_SSM(8)
+    CATOPT_SSM(16)
+    CATOPT_SSM(32)
+    CATOPT_SSM(64)
+    default:
+      return CATOPT_E_UNSUPPORTED;
+  }
+#undef CATOPT_SSM
+}

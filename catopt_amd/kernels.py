@@ -1,0 +1,448 @@
+"""Torch-facing wrappers over the C ABI: device memory and streams in, kernels out.
+
+Every function here takes ``torch.Tensor`` operands that already live on a
+ROCm device, allocates its outputs (and any workspace) with torch's caching
+allocator, and enqueues the kernel on torch's current stream.  Shapes,
+dtypes and layouts are checked on the host before any launch, so a kernel
+only ever sees operands that match what its grid assumes.  There is no CPU
+path: a host tensor or a missing library raises.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Sequence
+
+import torch
+
+from . import _lib as L
+
+_DT = {torch.float32: L.F32, torch.bfloat16: L.BF16}
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _need_device(*ts: torch.Tensor | None) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"expected a tensor, got {type(t).__name__}")
+        if t.device.type != "cuda":
+            raise ValueError(
+                "catopt_amd kernels run on a ROCm device only; got a tensor on "
+                f"{t.device} (there is no CPU fallback)"
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"operands on different devices: {dev} vs {t.device}")
+    if dev is None:
+        raise ValueError("no tensor operands")
+    return dev
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise NotImplementedError(
+            f"dtype {t.dtype} is not supported by the HIP kernels (fp32, bf16)"
+        ) from None
+
+
+def _rows_view(x: torch.Tensor) -> tuple[torch.Tensor, int]:
+    """(M, K) view with a contiguous last axis and a uniform row stride."""
+    if x.dim() == 0:
+        raise ValueError("expected at least a vector")
+    x2 = x.reshape(-1, x.shape[-1]) if x.dim() != 2 else x
+    if x2.stride(-1) != 1 or (x2.shape[0] > 1 and x2.stride(0) < x2.shape[1]):
+        x2 = x2.contiguous()
+    ld = x2.stride(0) if x2.shape[0] > 1 else x2.shape[1]
+    return x2, max(ld, x2.shape[1])
+
+
+# --------------------------------------------------------------------- norms
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor | None, eps: float) -> torch.Tensor:
+    """``x * rsqrt(mean(x², -1) + eps) * weight`` over the last axis."""
+    _need_device(x, weight)
+    lib = L.load()
+    dt = _dtype_code(x)
+    if weight is not None:
+        if weight.dtype != x.dtype or weight.numel() != x.shape[-1]:
+            raise ValueError("rms_norm weight must match x's last axis and dtype")
+        weight = weight.contiguous()
+    x2, ldx = _rows_view(x)
+    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    rows, cols = x2.shape
+    st = lib.catopt_hip_rmsnorm(dt, rows, cols, _ptr(x2), ldx, _ptr(weight), float(eps),
+                                _ptr(y), cols, _stream(x))
+    L.check("catopt_hip_rmsnorm", st)
+    return y
+
+
+# ---------------------------------------------------------------------- GEMM
+
+
+def linear(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None = None,
+    bias2: torch.Tensor | None = None,
+    epilogue: int | None = None,
+) -> torch.Tensor:
+    """``epi(x @ weightᵀ)`` with nn.Linear weight layout ``(out, in)``.
+
+    ``epilogue`` defaults to NONE / BIAS / BIAS_ADD2 by which biases are
+    given.  For ``EPI_SILU_MUL`` / ``EPI_GLU`` the weight holds both
+    projections stacked along its rows and the output width is half of them.
+    """
+    _need_device(x, weight, bias, bias2)
+    lib = L.load()
+    dt = _dtype_code(x)
+    if weight.dtype != x.dtype or weight.dim() != 2:
+        raise ValueError("linear weight must be 2-D and share x's dtype")
+    if epilogue is None:
+        epilogue = L.EPI_NONE if bias is None else (L.EPI_BIAS if bias2 is None else L.EPI_BIAS_ADD2)
+    K = x.shape[-1]
+    if weight.shape[1] != K:
+        raise ValueError(f"linear: x has {K} features, weight expects {weight.shape[1]}")
+    paired = epilogue in (L.EPI_SILU_MUL, L.EPI_GLU)
+    n_rows = weight.shape[0]
+    if paired and n_rows % 2:
+        raise ValueError("paired epilogue needs an even number of weight rows")
+    N = n_rows // 2 if paired else n_rows
+    for b in (bias, bias2):
+        if b is not None and (b.numel() != N or b.dtype != x.dtype):
+            raise ValueError("bias must be an [N] vector of x's dtype")
+    bias = bias.contiguous() if bias is not None else None
+    bias2 = bias2.contiguous() if bias2 is not None else None
+    if weight.stride(1) != 1:
+        weight = weight.contiguous()
+    x2, ldx = _rows_view(x)
+    M = x2.shape[0]
+    y = torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
+    if M == 0 or N == 0:
+        return y
+    if K == 0:
+        y.zero_()
+        if bias is not None:
+            y += bias
+        if bias2 is not None:
+            y += bias2
+        if paired:
+            raise NotImplementedError("paired epilogue over an empty contraction")
+        return y
+    st = lib.catopt_hip_linear(dt, M, N, K, _ptr(x2), ldx, _ptr(weight), weight.stride(0),
+                               _ptr(bias), _ptr(bias2), int(epilogue), _ptr(y), N, _stream(x))
+    L.check("catopt_hip_linear", st)
+    return y
+
+
+def _mat_layout(t: torch.Tensor) -> tuple[torch.Tensor, bool, int, int]:
+    """(tensor, transposed, ld, batch_stride) for a (batch, r, c) operand."""
+    s_b, s_r, s_c = t.stride()
+    r, c = t.shape[1], t.shape[2]
+    if s_c == 1 and (r == 1 or s_r >= c):
+        return t, False, max(s_r, c), s_b
+    if s_r == 1 and (c == 1 or s_c >= r):
+        return t, True, max(s_c, r), s_b
+    t = t.contiguous()
+    return t, False, c, t.stride(0)
+
+
+def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """``torch.matmul`` semantics for 2-D and batched 3-D+ operands (fp32/bf16)."""
+    _need_device(a, b)
+    lib = L.load()
+    dt = _dtype_code(a)
+    if a.dtype != b.dtype:
+        raise ValueError(f"matmul operands must share a dtype: {a.dtype} vs {b.dtype}")
+    if a.dim() < 2 or b.dim() < 2:
+        if a.dim() == 1 and b.dim() >= 2:
+            return matmul(a.unsqueeze(0), b).squeeze(-2)
+        if b.dim() == 1 and a.dim() >= 2:
+            return matmul(a, b.unsqueeze(-1)).squeeze(-1)
+        raise NotImplementedError("matmul of two vectors")
+    M, K = a.shape[-2], a.shape[-1]
+    K2, N = b.shape[-2], b.shape[-1]
+    if K != K2:
+        raise ValueError(f"matmul shape mismatch {tuple(a.shape)} @ {tuple(b.shape)}")
+    batch_shape = torch.broadcast_shapes(a.shape[:-2], b.shape[:-2])
+    nb = math.prod(batch_shape) if batch_shape else 1
+    # A single matrix broadcast over the batch keeps batch stride 0 (no copy).
+    a3 = a.unsqueeze(0).expand(nb, M, K) if a.dim() == 2 else a.expand(*batch_shape, M, K).reshape(nb, M, K)
+    b3 = b.unsqueeze(0).expand(nb, K, N) if b.dim() == 2 else b.expand(*batch_shape, K, N).reshape(nb, K, N)
+    a3, ta, lda, sa = _mat_layout(a3)
+    b3, tb, ldb, sb = _mat_layout(b3)
+    out = torch.empty((nb, M, N), dtype=a.dtype, device=a.device)
+    if nb and M and N:
+        if K == 0:
+            out.zero_()
+        else:
+            st = lib.catopt_hip_matmul(dt, nb, M, N, K, _ptr(a3), lda, sa, int(ta), _ptr(b3), ldb,
+                                       sb, int(tb), _ptr(out), N, M * N, _stream(a))
+            L.check("catopt_hip_matmul", st)
+    return out.reshape(*batch_shape, M, N)
+
+
+# ----------------------------------------------------------------- attention
+
+
+def _bhtd(t: torch.Tensor) -> tuple[torch.Tensor, list[int]]:
+    if t.dim() != 4:
+        raise ValueError("attention operands are (B, H, T, d)")
+    if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:3]) or t.data_ptr() % 16:
+        t = t.contiguous()
+    return t, [t.stride(0), t.stride(1), t.stride(2)]
+
+
+def attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    scale: float,
+    *,
+    causal: bool = False,
+    causal_off: int = 0,
+    mask: torch.Tensor | None = None,
+    normalize: bool = True,
+    return_ml: bool = False,
+):
+    """Online-softmax attention ``(B,H,T,d)`` bf16.
+
+    ``causal`` keeps key ``j`` for query ``i`` iff ``j <= i + causal_off``;
+    ``mask`` is a bool keep-mask ``(Tq, Tk)`` shared over (B, H).  With
+    ``normalize=False`` the raw numerator ``a`` is returned; ``return_ml``
+    adds the fp32 ``(m, l)`` om carriers, shaped ``(B, H, Tq, 1)``.
+    """
+    _need_device(q, k, v, mask)
+    lib = L.load()
+    if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise NotImplementedError("HIP attention runs on bf16 operands")
+    B, H, Tq, d = q.shape
+    Bk, Hk, Tk, dk = k.shape
+    if (Bk, Hk, dk) != (B, H, d) or v.shape[:3] != k.shape[:3]:
+        raise ValueError(f"attention shape mismatch q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)}")
+    dv = v.shape[3]
+    if d != dv or d not in (64, 128):
+        raise NotImplementedError(f"HIP attention supports d = dv in (64, 128), got {d}, {dv}")
+    q, qs = _bhtd(q)
+    k, ks = _bhtd(k)
+    v, vs = _bhtd(v)
+    o = torch.empty((B, H, Tq, dv), dtype=q.dtype, device=q.device)
+    m = l = None
+    if return_ml:
+        m = torch.empty((B, H, Tq), dtype=torch.float32, device=q.device)
+        l = torch.empty((B, H, Tq), dtype=torch.float32, device=q.device)
+    mode = L.MASK_NONE
+    mask_u8 = None
+    mask_ld = 0
+    if mask is not None:
+        if causal:
+            raise ValueError("pass either causal=True or a mask, not both")
+        if mask.shape[-2:] != (Tq, Tk) or mask.numel() != Tq * Tk:
+            raise NotImplementedError("mask must be a (Tq, Tk) keep-mask shared over (B, H)")
+        mask_u8 = mask.reshape(Tq, Tk).to(torch.uint8).contiguous()
+        mask_ld = Tk
+        mode = L.MASK_BOOL
+    elif causal:
+        mode = L.MASK_CAUSAL
+    st = lib.catopt_hip_attn_fwd(
+        L.BF16, B, H, Tq, Tk, d, dv, _ptr(q), L.i64_array(qs), _ptr(k), L.i64_array(ks),
+        _ptr(v), L.i64_array(vs), float(scale), mode, int(causal_off), _ptr(mask_u8), mask_ld,
+        int(bool(normalize)), _ptr(o), L.i64_array([o.stride(0), o.stride(1), o.stride(2)]),
+        _ptr(m), _ptr(l), _stream(q))
+    L.check("catopt_hip_attn_fwd", st)
+    if return_ml:
+        return o, m.unsqueeze(-1), l.unsqueeze(-1)
+    return o
+
+
+def om_compose(f, g):
+    """FlashAttention combine of two fp32 om carriers ``(m, l, a)``."""
+    m1, l1, a1 = f
+    m2, l2, a2 = g
+    _need_device(m1, l1, a1, m2, l2, a2)
+    lib = L.load()
+    ts = [t.float().contiguous() for t in (m1, l1, a1, m2, l2, a2)]
+    m1, l1, a1, m2, l2, a2 = ts
+    rows = m1.numel()
+    if l1.numel() != rows or m2.numel() != rows or l2.numel() != rows:
+        raise ValueError("om carriers disagree on their row count")
+    dv = a1.numel() // max(rows, 1)
+    if a1.shape != a2.shape or dv * rows != a1.numel():
+        raise ValueError("om numerators disagree")
+    m, l, a = torch.empty_like(m1), torch.empty_like(l1), torch.empty_like(a1)
+    st = lib.catopt_hip_om_compose(rows, dv, _ptr(m1), _ptr(l1), _ptr(a1), _ptr(m2), _ptr(l2),
+                                   _ptr(a2), _ptr(m), _ptr(l), _ptr(a), _stream(m1))
+    L.check("catopt_hip_om_compose", st)
+    return m, l, a
+
+
+# ----------------------------------------------------------------- retention
+
+RETENTION_CHUNK = 64
+
+
+def retention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma: torch.Tensor,
+              scale: float = 1.0) -> torch.Tensor:
+    """``scale * Σ_{s<=t} γ_h^(t-s) (q_t·k_s) v_s`` for ``(B,H,T,128)`` bf16."""
+    _need_device(q, k, v, gamma)
+    lib = L.load()
+    if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise NotImplementedError("HIP retention runs on bf16 operands")
+    if q.dim() != 4 or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("retention operands must share a (B, H, T, d) shape")
+    B, H, T, d = q.shape
+    if d != 128 or T % RETENTION_CHUNK:
+        raise NotImplementedError(f"HIP retention needs d = 128 and T % {RETENTION_CHUNK} == 0")
+    g = gamma.to(torch.float32).reshape(-1).contiguous()
+    if g.numel() != H:
+        raise ValueError("gamma must hold one rate per head")
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    o = torch.empty_like(q)
+    wsb = lib.catopt_hip_retention_workspace_bytes(B, H, T, d, RETENTION_CHUNK)
+    if wsb < 0:
+        raise ValueError("retention workspace query rejected the shape")
+    ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=q.device)
+    st = lib.catopt_hip_retention_fwd(L.BF16, B, H, T, d, RETENTION_CHUNK, _ptr(q), _ptr(k),
+                                      _ptr(v), _ptr(g), float(scale), _ptr(o), _ptr(ws), wsb,
+                                      _stream(q))
+    L.check("catopt_hip_retention_fwd", st)
+    return o
+
+
+def decay(gamma: torch.Tensor, t: int) -> torch.Tensor:
+    """``decay(γ, t)`` on device, fp32, shape ``(*γ.shape, t, t)``."""
+    _need_device(gamma)
+    lib = L.load()
+    g = gamma.to(torch.float32).reshape(-1).contiguous()
+    out = torch.empty((g.numel(), t, t), dtype=torch.float32, device=g.device)
+    L.check("catopt_hip_decay", lib.catopt_hip_decay(g.numel(), t, _ptr(g), _ptr(out), _stream(g)))
+    return out.reshape(*gamma.shape, t, t)
+
+
+def decay_vec(gamma: torch.Tensor, t: int, offset: int = 0, sign: int = 1) -> torch.Tensor:
+    """``decay_vec(γ, t, offset, sign)`` on device, fp32, shape ``(*γ.shape, t)``."""
+    _need_device(gamma)
+    lib = L.load()
+    g = gamma.to(torch.float32).reshape(-1).contiguous()
+    out = torch.empty((g.numel(), t), dtype=torch.float32, device=g.device)
+    L.check("catopt_hip_decay_vec",
+            lib.catopt_hip_decay_vec(g.numel(), t, int(offset), int(sign), _ptr(g), _ptr(out), _stream(g)))
+    return out.reshape(*gamma.shape, t)
+
+
+# ---------------------------------------------------------------------- scans
+
+
+def _chunk_table(chunk_starts: Sequence[int] | torch.Tensor, T: int, device) -> tuple[torch.Tensor, int]:
+    cs = torch.as_tensor(chunk_starts, dtype=torch.int64).cpu()
+    if cs.dim() != 1 or cs.numel() < 2:
+        raise ValueError("chunk table needs at least [0, T]")
+    if int(cs[0]) != 0 or int(cs[-1]) != T or bool((cs[1:] <= cs[:-1]).any()) and T > 0:
+        raise ValueError(f"chunk table must rise strictly from 0 to T={T}")
+    return cs.to(device), cs.numel() - 1
+
+
+def affd_scan(a: torch.Tensor, u: torch.Tensor, h0: torch.Tensor | None,
+              chunk_starts, *, schedule: int = L.SCAN_AUTO, states: bool = True):
+    """Diagonal affine scan over the leading axis: ``h_t = a_t h_{t-1} + u_t``.
+
+    ``a`` is ``(T, *S)`` or ``(*S)`` (shared over steps), ``u`` is ``(T, *S)``.
+    Returns ``(states (T, *S) or None, h_final (*S))`` in fp32.
+    """
+    _need_device(a, u, h0)
+    lib = L.load()
+    T = u.shape[0]
+    sshape = u.shape[1:]
+    S = math.prod(sshape)
+    u2 = u.to(torch.float32).reshape(T, S).contiguous()
+    if a.shape == sshape:
+        a2, lda = a.to(torch.float32).reshape(1, S).contiguous(), 0
+    elif a.shape == u.shape:
+        a2, lda = a.to(torch.float32).reshape(T, S).contiguous(), S
+    else:
+        raise ValueError(f"scan a{tuple(a.shape)} does not fit u{tuple(u.shape)}")
+    h = h0.to(torch.float32).reshape(S).contiguous() if h0 is not None else None
+    cs, nc = _chunk_table(chunk_starts, T, u.device)
+    out = torch.empty((T, S), dtype=torch.float32, device=u.device) if states else None
+    hf = torch.empty((S,), dtype=torch.float32, device=u.device)
+    wsb = lib.catopt_hip_scan_workspace_bytes(S, nc)
+    ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=u.device)
+    st = lib.catopt_hip_affd_scan(T, S, _ptr(a2), lda, _ptr(u2), S, _ptr(h), _ptr(cs), nc,
+                                  int(schedule), _ptr(out), _ptr(hf), _ptr(ws), wsb, _stream(u))
+    L.check("catopt_hip_affd_scan", st)
+    return (out.reshape(T, *sshape) if out is not None else None), hf.reshape(sshape)
+
+
+def ssm_scan(a: torch.Tensor, bx: torch.Tensor, c: torch.Tensor, x: torch.Tensor,
+             h0: torch.Tensor | None, chunk_starts, *, schedule: int = L.SCAN_AUTO,
+             return_state: bool = False):
+    """Selective diagonal SSM with fused input/readout, fp32.
+
+    ``a`` (B,T,D,N) or (B,T,D); ``bx``, ``c`` (B,T,N); ``x`` (B,T,D);
+    ``h0`` (B,D,N) or None.  Returns ``y`` (B,T,D) [and ``h_T`` (B,D,N)].
+    """
+    _need_device(a, bx, c, x, h0)
+    lib = L.load()
+    B, T, D = x.shape
+    N = bx.shape[-1]
+    if bx.shape != (B, T, N) or c.shape != (B, T, N):
+        raise ValueError("bx and c must be (B, T, N)")
+    if a.shape == (B, T, D, N):
+        aps = 1
+    elif a.shape == (B, T, D):
+        aps = 0
+    else:
+        raise ValueError(f"a must be (B,T,D,N) or (B,T,D), got {tuple(a.shape)}")
+    if N not in (4, 8, 16, 32, 64):
+        raise NotImplementedError(f"HIP SSM scan supports N in (4, 8, 16, 32, 64), got {N}")
+    f = lambda t: None if t is None else t.to(torch.float32).contiguous()  # noqa: E731
+    a, bx, c, x, h0 = f(a), f(bx), f(c), f(x), f(h0)
+    if h0 is not None and h0.shape != (B, D, N):
+        raise ValueError("h0 must be (B, D, N)")
+    cs, nc = _chunk_table(chunk_starts, T, x.device)
+    y = torch.empty((B, T, D), dtype=torch.float32, device=x.device)
+    hf = torch.empty((B, D, N), dtype=torch.float32, device=x.device) if return_state else None
+    wsb = lib.catopt_hip_scan_workspace_bytes(B * D * N, nc)
+    ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=x.device)
+    st = lib.catopt_hip_ssm_scan(B, T, D, N, _ptr(a), aps, _ptr(bx), _ptr(c), _ptr(x), _ptr(h0),
+                                 _ptr(cs), nc, int(schedule), _ptr(y), _ptr(hf), _ptr(ws), wsb,
+                                 _stream(x))
+    L.check("catopt_hip_ssm_scan", st)
+    return (y, hf) if return_state else y
+
+
+# --------------------------------------------------------------- elementwise
+
+
+def silu(x: torch.Tensor) -> torch.Tensor:
+    _need_device(x)
+    lib = L.load()
+    xc = x.contiguous()
+    y = torch.empty_like(xc)
+    L.check("catopt_hip_silu", lib.catopt_hip_silu(_dtype_code(x), xc.numel(), _ptr(xc), _ptr(y), _stream(x)))
+    return y
+
+
+def silu_mul(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+    _need_device(g, u)
+    lib = L.load()
+    if g.shape != u.shape or g.dtype != u.dtype:
+        g, u = torch.broadcast_tensors(g, u)
+    gc, uc = g.contiguous(), u.contiguous()
+    y = torch.empty_like(gc)
+    L.check("catopt_hip_silu_mul",
+            lib.catopt_hip_silu_mul(_dtype_code(gc), gc.numel(), _ptr(gc), _ptr(uc), _ptr(y), _stream(g)))
+    return y

@@ -1,0 +1,289 @@
+"""GPU parity of every C-ABI kernel against the numpy oracle.
+
+Inputs are seeded on the host, rounded to the kernel dtype, and the oracle
+runs on exactly those values in float64.  Gates (the north star's, as the
+reference's verify metric ``max|Δ| / (max|ref| + 1e-8)``):
+  fp32  ≤ 1e-5,   bf16  ≤ 2e-2,   integer tables bit-exact.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from catopt_amd import _lib as L
+from catopt_amd import kernels as K
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-5
+TOL_BF16 = 2e-2
+
+
+def _np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().double().numpy()
+
+
+def _gate(ref, out, tol):
+    rep = oracle.verify_equiv(ref, _np(out) if isinstance(out, torch.Tensor) else out, rtol=tol)
+    assert rep["passed"], rep
+    return rep
+
+
+def _rand(shape, dtype, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g, dtype=torch.float32) * scale).to(dtype)
+
+
+# ------------------------------------------------------------------ rmsnorm
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 4096), (33, 1000), (7, 4097), (5, 8192)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rmsnorm(dev, rows, cols, dtype):
+    x = _rand((rows, cols), dtype, 1)
+    w = (1 + 0.02 * _rand((cols,), torch.float32, 2)).to(dtype)
+    y = K.rmsnorm(x.to(dev), w.to(dev), 1e-6)
+    ref = oracle.rms_norm(_np(x), _np(w), 1e-6)
+    _gate(ref, y, TOL_BF16 if dtype == torch.bfloat16 else TOL_F32)
+
+
+def test_rmsnorm_strided_rows_no_weight(dev):
+    x = _rand((16, 2 * 512), torch.bfloat16, 3)[:, :512]
+    y = K.rmsnorm(x.to(dev), None, 1e-5)
+    _gate(oracle.rms_norm(_np(x), None, 1e-5), y, TOL_BF16)
+
+
+# ------------------------------------------------------------------ linear
+
+
+@pytest.mark.parametrize("M,N,Kd", [(512, 512, 512), (300, 520, 264), (17, 1000, 64), (1, 256, 4096)])
+@pytest.mark.parametrize("with_bias", [0, 1, 2])
+def test_linear_bf16(dev, M, N, Kd, with_bias):
+    x = _rand((M, Kd), torch.bfloat16, 10)
+    w = _rand((N, Kd), torch.bfloat16, 11, 0.05)
+    b = _rand((N,), torch.bfloat16, 12) if with_bias else None
+    b2 = _rand((N,), torch.bfloat16, 13) if with_bias == 2 else None
+    y = K.linear(x.to(dev), w.to(dev), None if b is None else b.to(dev), None if b2 is None else b2.to(dev))
+    ref = oracle.linear(_np(x), _np(w), None if b is None else _np(b))
+    if b2 is not None:
+        ref = ref + _np(b2)
+    _gate(ref, y, TOL_BF16)
+
+
+@pytest.mark.parametrize("M,N,Kd", [(256, 384, 512), (100, 200, 128), (513, 128, 4096)])
+@pytest.mark.parametrize("epi", [L.EPI_SILU_MUL, L.EPI_GLU])
+def test_linear_paired_epilogue(dev, M, N, Kd, epi):
+    x = _rand((M, Kd), torch.bfloat16, 20)
+    wg = _rand((N, Kd), torch.bfloat16, 21, 0.05)
+    wu = _rand((N, Kd), torch.bfloat16, 22, 0.05)
+    wcat = torch.cat([wg, wu], 0)
+    y = K.linear(x.to(dev), wcat.to(dev), epilogue=epi)
+    g = oracle.linear(_np(x), _np(wg))
+    u = oracle.linear(_np(x), _np(wu))
+    ref = oracle.silu(g) * u if epi == L.EPI_SILU_MUL else g * (1 / (1 + np.exp(-u)))
+    _gate(ref, y, TOL_BF16)
+
+
+def test_linear_paired_unaligned_falls_to_generic(dev):
+    # K % 8 != 0 takes the generic kernel; the result must not change.
+    x = _rand((40, 60), torch.bfloat16, 23)
+    w = _rand((2 * 72, 60), torch.bfloat16, 24, 0.1)
+    y = K.linear(x.to(dev), w.to(dev), epilogue=L.EPI_SILU_MUL)
+    g, u = oracle.linear(_np(x), _np(w[:72])), oracle.linear(_np(x), _np(w[72:]))
+    _gate(oracle.silu(g) * u, y, TOL_BF16)
+
+
+@pytest.mark.parametrize("M,N,Kd", [(64, 512, 512), (7, 33, 129)])
+def test_linear_fp32(dev, M, N, Kd):
+    x = _rand((M, Kd), torch.float32, 30)
+    w = _rand((N, Kd), torch.float32, 31, 1 / math.sqrt(Kd))
+    b = _rand((N,), torch.float32, 32)
+    y = K.linear(x.to(dev), w.to(dev), b.to(dev))
+    _gate(oracle.linear(_np(x), _np(w), _np(b)), y, TOL_F32)
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_matmul_layouts(dev, ta, tb, dtype):
+    A = _rand((3, 70, 90), dtype, 40)
+    B = _rand((3, 90, 50), dtype, 41)
+    a = A.transpose(1, 2).contiguous().transpose(1, 2) if ta else A
+    b = B.transpose(1, 2).contiguous().transpose(1, 2) if tb else B
+    y = K.matmul(a.to(dev), b.to(dev))
+    _gate(_np(A) @ _np(B), y, TOL_BF16 if dtype == torch.bfloat16 else TOL_F32)
+
+
+def test_matmul_fold_chain_fp32(dev):
+    Ws = [_rand((512, 512), torch.float32, 50 + i, 1 / math.sqrt(512)) for i in range(3)]
+    y = K.matmul(K.matmul(Ws[2].to(dev), Ws[1].to(dev)), Ws[0].to(dev))
+    _gate(_np(Ws[2]) @ _np(Ws[1]) @ _np(Ws[0]), y, TOL_F32)
+
+
+def test_matmul_broadcast_batch(dev):
+    A = _rand((4, 2, 64, 96), torch.bfloat16, 60)
+    B = _rand((96, 128), torch.bfloat16, 61)
+    y = K.matmul(A.to(dev), B.to(dev))
+    _gate(_np(A) @ _np(B), y, TOL_BF16)
+
+
+# ------------------------------------------------------------------ attention
+
+
+def _qkv(B, H, T, d, seed, Tk=None):
+    Tk = Tk or T
+    return (_rand((B, H, T, d), torch.bfloat16, seed), _rand((B, H, Tk, d), torch.bfloat16, seed + 1),
+            _rand((B, H, Tk, d), torch.bfloat16, seed + 2))
+
+
+@pytest.mark.parametrize("T,d", [(256, 128), (200, 128), (384, 64), (64, 128)])
+def test_attention_causal(dev, T, d):
+    q, k, v = _qkv(1, 3, T, d, 70)
+    scale = 1 / math.sqrt(d)
+    o = K.attention(q.to(dev), k.to(dev), v.to(dev), scale, causal=True)
+    ref = oracle.attention_om(_np(q), _np(k), _np(v), scale, causal=True, block=64)
+    _gate(ref, o, TOL_BF16)
+    assert not torch.isnan(o).any()
+
+
+def test_attention_ml_carriers_and_unnormalised(dev):
+    q, k, v = _qkv(2, 2, 128, 128, 80)
+    scale = 0.1
+    a, m, l = K.attention(q.to(dev), k.to(dev), v.to(dev), scale, causal=True, normalize=False, return_ml=True)
+    out, mr, lr = oracle.attention_om(_np(q), _np(k), _np(v), scale, causal=True, block=32, return_ml=True)
+    _gate(mr, m, 1e-5)
+    _gate(lr, l, TOL_BF16)
+    _gate(out * lr, a, TOL_BF16)
+
+
+def test_attention_bool_mask_nan_rows(dev):
+    T = 96
+    q, k, v = _qkv(1, 2, T, 128, 90)
+    rng = np.random.default_rng(0)
+    keep = rng.random((T, T)) < 0.3
+    keep[5, :] = False  # a fully masked row: om_apply gives NaN there
+    o = K.attention(q.to(dev), k.to(dev), v.to(dev), 0.125, mask=torch.from_numpy(keep).to(dev))
+    ref = oracle.attention_om(_np(q), _np(k), _np(v), 0.125, causal=False, mask=keep, block=32)
+    on = _np(o)
+    assert np.array_equal(np.isnan(on), np.isnan(ref))
+    fin = ~np.isnan(ref)
+    _gate(np.where(fin, ref, 0), np.where(fin, on, 0), TOL_BF16)
+
+
+def test_attention_causal_offset_and_cross_lengths(dev):
+    q, k, v = _qkv(1, 2, 100, 128, 95, Tk=300)
+    o = K.attention(q.to(dev), k.to(dev), v.to(dev), 0.08, causal=True, causal_off=200)
+    ref = oracle.attention_om(_np(q), _np(k), _np(v), 0.08, causal=True, causal_off=200)
+    _gate(ref, o, TOL_BF16)
+
+
+def test_om_compose_kernel(dev):
+    rng = np.random.default_rng(1)
+    m1 = rng.standard_normal((40, 1))
+    m2 = rng.standard_normal((40, 1))
+    m1[3] = -np.inf
+    m2[7] = -np.inf
+    m1[9] = m2[9] = -np.inf
+    l1, l2 = rng.random((40, 1)), rng.random((40, 1))
+    a1, a2 = rng.standard_normal((40, 16)), rng.standard_normal((40, 16))
+    l1[m1 == -np.inf] = 0
+    l2[m2 == -np.inf] = 0
+    f = [torch.tensor(t, dtype=torch.float32, device=dev) for t in (m1, l1, a1)]
+    g = [torch.tensor(t, dtype=torch.float32, device=dev) for t in (m2, l2, a2)]
+    m, l, a = K.om_compose(f, g)
+    rm, rl, ra = oracle.om_compose((m1, l1, a1), (m2, l2, a2))
+    assert np.array_equal(np.isinf(_np(m)), np.isinf(rm))
+    _gate(rl, l, TOL_F32)
+    _gate(ra, a, TOL_F32)
+
+
+# ------------------------------------------------------------------ retention
+
+
+def _gammas(H):
+    return np.array([1 - 2.0 ** (-5 - h / 2) for h in range(H)], dtype=np.float32)
+
+
+@pytest.mark.parametrize("B,H,T", [(1, 2, 512), (2, 3, 1024), (1, 1, 64)])
+def test_retention_vs_kway_form(dev, B, H, T):
+    scale = 1.0
+    q = _rand((B, H, T, 128), torch.bfloat16, 100, 1 / math.sqrt(128))
+    k = _rand((B, H, T, 128), torch.bfloat16, 101, 1 / math.sqrt(128))
+    v = _rand((B, H, T, 128), torch.bfloat16, 102, 1 / math.sqrt(128))
+    gam = _gammas(H)
+    o = K.retention(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(gam).to(dev), scale)
+    g64 = gam.astype(np.float64)
+    if T >= 128:  # the K-way delivered form with 64-row chunks
+        ref = oracle.retention_kway(_np(q), _np(k), _np(v), g64, T // 64, scale)
+    else:  # a single chunk is the quadratic form itself
+        ref = oracle.retention_quadratic(_np(q), _np(k), _np(v), g64, scale)
+    _gate(ref, o, TOL_BF16)
+
+
+def test_retention_long_many_segments(dev):
+    # 64 chunks over one (b,h): exercises the segment carry pass.
+    B, H, T = 1, 2, 4096
+    q = _rand((B, H, T, 128), torch.bfloat16, 110, 1 / math.sqrt(128))
+    k = _rand((B, H, T, 128), torch.bfloat16, 111, 1 / math.sqrt(128))
+    v = _rand((B, H, T, 128), torch.bfloat16, 112, 1 / math.sqrt(128))
+    gam = _gammas(H)
+    o = K.retention(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(gam).to(dev), 0.5)
+    ref = oracle.retention_quadratic(_np(q), _np(k), _np(v), gam.astype(np.float64), 0.5)
+    _gate(ref, o, TOL_BF16)
+
+
+def test_decay_generators(dev):
+    gam = _gammas(4)
+    g = torch.from_numpy(gam).to(dev)
+    _gate(oracle.decay(gam.astype(np.float64), 64), K.decay(g, 64), TOL_F32)
+    for off, sign in [(0, -1), (128, 1), (64, 0)]:
+        _gate(oracle.decay_vec(gam.astype(np.float64), 64, off, sign), K.decay_vec(g, 64, off, sign), TOL_F32)
+
+
+# ------------------------------------------------------------------ scans
+
+
+@pytest.mark.parametrize("schedule", [L.SCAN_STREAM, L.SCAN_CHUNKED])
+@pytest.mark.parametrize("lti", [False, True])
+def test_affd_scan(dev, schedule, lti):
+    rng = np.random.default_rng(5)
+    T, S = 300, 1000
+    a = rng.uniform(0.5, 1.0, (S,) if lti else (T, S)).astype(np.float32)
+    u = rng.standard_normal((T, S)).astype(np.float32)
+    h0 = rng.standard_normal(S).astype(np.float32)
+    table = oracle.prefix_chunk_table(T)
+    st, hf = K.affd_scan(torch.from_numpy(a).to(dev), torch.from_numpy(u).to(dev),
+                         torch.from_numpy(h0).to(dev), table, schedule=schedule)
+    ref = oracle.serial_affd_scan(a.astype(np.float64), u.astype(np.float64), h0.astype(np.float64))
+    _gate(ref, st, TOL_F32)
+    _gate(ref[-1], hf, TOL_F32)
+
+
+@pytest.mark.parametrize("schedule", [L.SCAN_STREAM, L.SCAN_CHUNKED])
+@pytest.mark.parametrize("N,D,aps", [(16, 64, True), (16, 70, True), (4, 40, False), (64, 16, True)])
+def test_ssm_scan(dev, schedule, N, D, aps):
+    rng = np.random.default_rng(6)
+    B, T = 2, 257
+    z = rng.standard_normal((B, T, D, N) if aps else (B, T, D))
+    a = np.exp(-np.log1p(np.exp(z))).astype(np.float32)  # exp(-softplus(z)) in (0, 1)
+    bx = rng.standard_normal((B, T, N)).astype(np.float32)
+    c = rng.standard_normal((B, T, N)).astype(np.float32)
+    x = rng.standard_normal((B, T, D)).astype(np.float32)
+    h0 = rng.standard_normal((B, D, N)).astype(np.float32)
+    table = oracle.prefix_chunk_table(T)
+    t = lambda z_: torch.from_numpy(z_).to(dev)  # noqa: E731
+    y, hf = K.ssm_scan(t(a), t(bx), t(c), t(x), t(h0), table, schedule=schedule, return_state=True)
+    ry, rh = oracle.ssm_serial(*(z_.astype(np.float64) for z_ in (a, bx, c, x, h0)))
+    _gate(ry, y, TOL_F32)
+    _gate(rh, hf, TOL_F32)
+
+
+def test_silu_kernels(dev):
+    x = _rand((1000,), torch.bfloat16, 7)
+    u = _rand((1000,), torch.bfloat16, 8)
+    _gate(oracle.silu(_np(x)), K.silu(x.to(dev)), TOL_BF16)
+    _gate(oracle.silu(_np(x)) * _np(u), K.silu_mul(x.to(dev), u.to(dev)), TOL_BF16)
