@@ -1,0 +1,501 @@
+"""Delivered-form throughput of the HIP executor on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--forms c1,c2,c3,c4,c5]
+                    [--cpu-budget SECONDS] [--no-cpu]
+
+One "step" is one forward of a delivered form over one batch of synthetic
+input that is already resident in HBM (BASELINE.json's five configs, seeded
+with ``torch.manual_seed(0)``).  The headline workload is config 2 (the
+SwiGLU MLP block with RMSNorm: rms_norm -> gate/up GEMM with the silu*mul
+epilogue -> down GEMM); its whole-step TFLOP/s is ``value``.  Every other
+config is measured the same way and reported under ``forms``.
+
+Per form:
+  * ``ms_per_step``  — HIP events on torch's current stream (the stream the
+    kernels are launched on) around K back-to-back steps, after W warmup
+    steps, bracketed by ``torch.cuda.synchronize()``;
+  * ``roofline``     — the form's dominant kernel timed alone the same way:
+    algorithmic flops (MFMA-bound) or bytes (HBM-bound) per launch divided by
+    its average launch duration, against MI355X's published peak;
+  * ``cpu_baseline`` — the numpy oracle (``oracle/``, the CPU restatement of
+    the reference's delivered-module arithmetic) timed on a bounded sample of
+    the same inputs on this host; its outputs double as a parity check of
+    the GPU outputs on that sample (``parity_max_rel``).
+
+Only rank 0 of one process prints, one JSON line on stdout.  ``--gpus`` above
+1 exits with a message: this build measures one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "delivered-kernel TFLOP/s & HBM GB/s (% of MI355X peak) per lowered form"
+PEAK = {"bf16_tflops": 2500.0, "fp32_tflops": 157.3, "hbm_gbs": 8000.0}
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# --------------------------------------------------------------------- timing
+
+
+def time_events(fn, steps: int, warmup: int) -> float:
+    """Average ms per call of ``fn`` over ``steps`` calls (HIP events)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        fn()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps
+
+
+def cpu_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+
+        n = [int(i.get("num_threads", 1)) for i in threadpool_info() if i.get("user_api") == "blas"]
+        return max(n) if n else 1
+    except Exception:  # pragma: no cover - threadpoolctl missing
+        return 1
+
+
+def time_cpu(fn, budget_s: float, min_reps: int = 2) -> tuple[float, int, object]:
+    """Median seconds per call of ``fn`` (≥ ``min_reps`` calls, ~``budget_s`` total)."""
+    times, out = [], None
+    t_start = time.perf_counter()
+    while len(times) < min_reps or time.perf_counter() - t_start < budget_s:
+        t0 = time.perf_counter()
+        out = fn()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 50:
+            break
+    times.sort()
+    return times[len(times) // 2], len(times), out
+
+
+# ---------------------------------------------------------------------- forms
+
+
+class Form:
+    """One BASELINE config: inputs, one delivered step, its dominant kernel."""
+
+    name = ""
+    workload = ""
+    dtype = ""
+    unit = ""          # the form's headline unit: "TFLOP/s" or "GB/s"
+    bound = ""         # "mfma" | "hbm" for the dominant kernel
+    peak = 0.0
+    work = 0.0         # algorithmic flops or bytes per step
+    dom_name = ""
+    dom_work = 0.0     # algorithmic flops or bytes per dominant-kernel launch
+
+    def setup(self, dev) -> None: ...
+    def step(self) -> None: ...
+    def dominant(self) -> None: ...
+    def cpu(self, budget: float) -> dict | None: return None
+    def free(self) -> None:
+        for k in list(vars(self)):
+            if not k.startswith("_"):
+                delattr(self, k)
+
+    def throughput(self, ms: float) -> float:
+        scale = 1e12 if self.unit == "TFLOP/s" else 1e9
+        return self.work / (ms * 1e-3) / scale
+
+
+def _gen(seed=0):
+    import torch
+
+    return torch.Generator(device="cuda").manual_seed(seed)
+
+
+class C1WeightChain(Form):
+    name, dtype, unit, bound = "c1", "f32", "TFLOP/s", "mfma"
+    workload = "C1 deep linear weight chain: 8x nn.Linear(512,512)+bias folded to one GEMM+bias, x[64,512] fp32"
+    peak = PEAK["fp32_tflops"]
+    work = dom_work = 2.0 * 64 * 512 * 512
+    dom_name = "gemm_generic<float,NT,BIAS>"
+
+    def setup(self, dev):
+        import torch
+
+        from catopt_amd import kernels as K
+
+        torch.manual_seed(0)
+        layers = [torch.nn.Linear(512, 512) for _ in range(8)]
+        self.x_cpu = torch.randn(64, 512)
+        self.Ws = [l.weight.detach().to(dev) for l in layers]
+        self.bs = [l.bias.detach().to(dev) for l in layers]
+        self.Ws_cpu = [l.weight.detach().numpy() for l in layers]
+        self.bs_cpu = [l.bias.detach().numpy() for l in layers]
+        self.x = self.x_cpu.to(dev)
+        # construction-time fold on the device (7 GEMMs + bias mat-vecs)
+        W = self.Ws[0]
+        c = self.bs[0]
+        for Wl, bl in zip(self.Ws[1:], self.bs[1:]):
+            W = K.matmul(Wl, W)
+            c = K.matmul(Wl, c.unsqueeze(-1)).squeeze(-1) + bl
+        self.W_eff, self.c = W.contiguous(), c.contiguous()
+        self.K = K
+
+    def step(self):
+        self.y = self.K.linear(self.x, self.W_eff, self.c)
+
+    dominant = step
+
+    def cpu(self, budget):
+        import numpy as np
+
+        import oracle
+
+        x = self.x_cpu.numpy()
+        W, adds = oracle.fold_linear_chain(self.Ws_cpu, self.bs_cpu)
+        sec, reps, out = time_cpu(lambda: oracle.folded_chain_forward(x, W, adds), budget, 20)
+        ref = oracle.linear_chain(x.astype(np.float64), [w.astype(np.float64) for w in self.Ws_cpu],
+                                  [b.astype(np.float64) for b in self.bs_cpu])
+        self.step()
+        rel = oracle.verify_equiv(ref, self.y.cpu().double().numpy())["max_rel"]
+        return {"value": self.work / sec / 1e12, "unit": "TFLOP/s", "cores": cpu_threads(),
+                "kind": "port", "sample": f"full C1 forward (folded form, numpy fp32), {reps} reps",
+                "parity_max_rel": rel}
+
+
+class C2SwiGLU(Form):
+    name, dtype, unit, bound = "c2", "bf16", "TFLOP/s", "mfma"
+    workload = ("C2 SwiGLU MLP block with RMSNorm: x[8,2048,4096] bf16, rms_norm(eps=1e-6) -> "
+                "gate/up GEMM [4096->2x11008] with fused silu*mul -> down GEMM [11008->4096]")
+    peak = PEAK["bf16_tflops"]
+    M, D, F = 8 * 2048, 4096, 11008
+    work = 2.0 * M * D * 2 * F + 2.0 * M * F * D
+    dom_name = "gemm_bf16_nt<SILU_MUL>"
+    dom_work = 2.0 * M * D * 2 * F
+
+    def setup(self, dev):
+        import torch
+
+        from catopt_amd import _lib as L
+        from catopt_amd import kernels as K
+
+        g = _gen(0)
+        bf = torch.bfloat16
+        self.L = L
+        self.x = torch.randn(8, 2048, self.D, device=dev, generator=g).to(bf)
+        self.gamma = (1 + 0.02 * torch.randn(self.D, device=dev, generator=g)).to(bf)
+        wg = (0.02 * torch.randn(self.F, self.D, device=dev, generator=g)).to(bf)
+        wu = (0.02 * torch.randn(self.F, self.D, device=dev, generator=g)).to(bf)
+        self.w_cat = torch.cat([wg, wu], 0).contiguous()  # the folded concat(W_gate, W_up)
+        del wg, wu
+        self.w_down = (0.02 * torch.randn(self.D, self.F, device=dev, generator=g)).to(bf)
+        self.K = K
+        self.h = K.rmsnorm(self.x, self.gamma, 1e-6)
+
+    def step(self):
+        K = self.K
+        h = K.rmsnorm(self.x, self.gamma, 1e-6)
+        a = K.linear(h, self.w_cat, epilogue=self.L.EPI_SILU_MUL)
+        self.y = K.linear(a, self.w_down)
+
+    def dominant(self):
+        self.K.linear(self.h, self.w_cat, epilogue=self.L.EPI_SILU_MUL)
+
+    def cpu(self, budget):
+        import numpy as np
+
+        import oracle
+
+        rows = 256
+        x = self.x.reshape(-1, self.D)[:rows].float().cpu().numpy()
+        gam = self.gamma.float().cpu().numpy()
+        wcat = self.w_cat.float().cpu().numpy()
+        wg, wu = wcat[: self.F], wcat[self.F:]
+        wd = self.w_down.float().cpu().numpy()
+
+        def run():
+            return oracle.swiglu_fused(oracle.rms_norm(x, gam, 1e-6), wg, wu, wd)
+
+        sec, reps, out = time_cpu(run, budget)
+        self.step()
+        y = self.y.reshape(-1, self.D)[:rows].float().cpu().numpy()
+        rel = oracle.verify_equiv(out, y)["max_rel"]
+        flops = self.work * rows / self.M
+        return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": cpu_threads(),
+                "kind": "port",
+                "sample": f"first {rows} of {self.M} rows through rms_norm+swiglu (numpy fp32), {reps} reps",
+                "parity_max_rel": rel}
+
+
+class C3Attention(Form):
+    name, dtype, unit, bound = "c3", "bf16", "TFLOP/s", "mfma"
+    B, H, T, Dh = 4, 32, 4096, 128
+    workload = "C3 causal MHA (om_apply(om_elem) online softmax): q,k,v[4,32,4096,128] bf16, scale 1/sqrt(128)"
+    peak = PEAK["bf16_tflops"]
+    work = dom_work = 4.0 * B * H * T * T * Dh / 2  # causal half of the square
+    dom_name = "attn_fwd_kernel<128,CAUSAL>"
+
+    def setup(self, dev):
+        import torch
+
+        from catopt_amd import kernels as K
+
+        g = _gen(0)
+        shp = (self.B, self.H, self.T, self.Dh)
+        self.q = torch.randn(shp, device=dev, generator=g).to(torch.bfloat16)
+        self.k = torch.randn(shp, device=dev, generator=g).to(torch.bfloat16)
+        self.v = torch.randn(shp, device=dev, generator=g).to(torch.bfloat16)
+        self.scale = 1.0 / math.sqrt(self.Dh)
+        self.K = K
+
+    def step(self):
+        self.o = self.K.attention(self.q, self.k, self.v, self.scale, causal=True)
+
+    dominant = step
+
+    def cpu(self, budget):
+        import oracle
+
+        q, k, v = (t[0, 0].float().cpu().numpy() for t in (self.q, self.k, self.v))
+        sec, reps, out = time_cpu(lambda: oracle.attention_om(q, k, v, self.scale, causal=True), budget)
+        self.step()
+        rel = oracle.verify_equiv(out, self.o[0, 0].float().cpu().numpy())["max_rel"]
+        flops = self.work / (self.B * self.H)
+        return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": cpu_threads(),
+                "kind": "port",
+                "sample": f"one (b,h) of {self.B * self.H}: T=4096 single-leaf om form (numpy fp32), {reps} reps",
+                "parity_max_rel": rel}
+
+
+class C4Retention(Form):
+    name, dtype, unit, bound = "c4", "bf16", "GB/s", "hbm"
+    B, H, T, Dh, C = 4, 16, 8192, 128, 64
+    workload = ("C4 chunked decayed retention (om_decayed K-way, C=64): q,k,v[4,16,8192,128] bf16 "
+                "~N(0,1)/sqrt(128), gamma_h = 1-2^(-5-h/2) fp32")
+    peak = PEAK["hbm_gbs"]
+    work = dom_work = 4.0 * B * H * T * Dh * 2  # q, k, v read + o written, bf16
+    flops = B * H * (T / C) * (4 * C * C * Dh + 4 * C * Dh * Dh)
+    dom_name = "ret_seg_out"
+
+    def setup(self, dev):
+        import torch
+
+        from catopt_amd import kernels as K
+
+        g = _gen(0)
+        shp = (self.B, self.H, self.T, self.Dh)
+        s = 1.0 / math.sqrt(self.Dh)
+        self.q = (torch.randn(shp, device=dev, generator=g) * s).to(torch.bfloat16)
+        self.k = (torch.randn(shp, device=dev, generator=g) * s).to(torch.bfloat16)
+        self.v = (torch.randn(shp, device=dev, generator=g) * s).to(torch.bfloat16)
+        self.gamma = torch.tensor([1 - 2.0 ** (-5 - h / 2) for h in range(self.H)],
+                                  dtype=torch.float32, device=dev)
+        self.K = K
+
+    def step(self):
+        self.o = self.K.retention(self.q, self.k, self.v, self.gamma, 1.0)
+
+    dominant = step
+
+    def cpu(self, budget):
+        import numpy as np
+
+        import oracle
+
+        Ts = 1024  # the first 1024 steps of one (b,h): causal, so a prefix is exact
+        q, k, v = (t[0, :1, :Ts].float().cpu().numpy() for t in (self.q, self.k, self.v))
+        g = self.gamma[:1].cpu().numpy().astype(np.float32)
+        sec, reps, out = time_cpu(lambda: oracle.retention_kway(q, k, v, g, Ts // self.C, 1.0), budget)
+        self.step()
+        rel = oracle.verify_equiv(out, self.o[0, :1, :Ts].float().cpu().numpy())["max_rel"]
+        nbytes = 4.0 * Ts * self.Dh * 2
+        return {"value": nbytes / sec / 1e9, "unit": "GB/s", "cores": cpu_threads(), "kind": "port",
+                "sample": f"(b=0,h=0), first {Ts} of {self.T} steps, K-way form C=64 (numpy fp32), {reps} reps",
+                "parity_max_rel": rel}
+
+
+class C5SSM(Form):
+    name, dtype, unit, bound = "c5", "f32", "GB/s", "hbm"
+    B, D, N, T = 16, 2048, 16, 16384
+    workload = ("C5 diagonal selective SSM scan, all y_t: B=16 D=2048 N=16 T=16384 fp32, "
+                "a_t (B,T,D,N) = exp(-softplus(N(0,1))), b_t,c_t (B,T,N), x_t (B,T,D)")
+    peak = PEAK["hbm_gbs"]
+    work = dom_work = 4.0 * (B * T * D * N + 2 * B * T * N + 2 * B * T * D)
+    dom_name = "ssm_stream<16,per-state a>"
+
+    def setup(self, dev):
+        import torch
+
+        import oracle  # noqa: F401  (chunk table only; see below)
+
+        from catopt_amd import kernels as K
+
+        g = _gen(0)
+        B, D, N, T = self.B, self.D, self.N, self.T
+        a = torch.randn((B, T, D, N), device=dev, generator=g)
+        self.a = a.neg_().sigmoid_()  # exp(-softplus(z)) == sigmoid(-z), in place
+        self.bx = torch.randn((B, T, N), device=dev, generator=g)
+        self.c = torch.randn((B, T, N), device=dev, generator=g)
+        self.x = torch.randn((B, T, D), device=dev, generator=g)
+        blk = math.ceil(math.sqrt(T))
+        nc = (T + blk - 1) // blk
+        self.table = [i * blk for i in range(nc)] + [T]  # the blocked-prefix chunk plan
+        self.K = K
+
+    def step(self):
+        self.y = self.K.ssm_scan(self.a, self.bx, self.c, self.x, None, self.table)
+
+    dominant = step
+
+    def cpu(self, budget):
+        import numpy as np
+
+        import oracle
+
+        Dn, Ts = 32, 4096  # 32 channels of batch 0, first 4096 steps (causal: a prefix is exact)
+        a = self.a[:1, :Ts, :Dn].cpu().numpy()
+        bx = self.bx[:1, :Ts].cpu().numpy()
+        c = self.c[:1, :Ts].cpu().numpy()
+        x = self.x[:1, :Ts, :Dn].cpu().numpy()
+        sec, reps, (yr, _) = time_cpu(lambda: oracle.ssm_serial(a, bx, c, x), budget)
+        self.step()
+        rel = oracle.verify_equiv(yr, self.y[:1, :Ts, :Dn].cpu().numpy())["max_rel"]
+        nbytes = 4.0 * (Ts * Dn * self.N + 2 * Ts * self.N + 2 * Ts * Dn)
+        return {"value": nbytes / sec / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"b=0, {Dn} of {self.D} channels, first {Ts} of {self.T} steps, serial recurrence (numpy fp32), {reps} reps",
+                "parity_max_rel": rel}
+
+
+FORMS = {f.name: f for f in (C1WeightChain, C2SwiGLU, C3Attention, C4Retention, C5SSM)}
+HEADLINE = "c2"
+
+
+def measure(form: Form, dev, steps: int, warmup: int, cpu_budget: float | None) -> dict:
+    import torch
+
+    log(f"{form.name}: setup")
+    form.setup(dev)
+    torch.cuda.synchronize()
+    log(f"{form.name}: timing {steps} steps after {warmup} warmup")
+    w0 = time.perf_counter()
+    ms = time_events(form.step, steps, warmup)
+    wall_ms = (time.perf_counter() - w0) * 1e3
+    dom_steps = max(steps, 10)
+    dom_ms = time_events(form.dominant, dom_steps, 2)
+    achieved = form.dom_work / (dom_ms * 1e-3) / (1e12 if form.bound == "mfma" else 1e9)
+    rec = {
+        "workload": form.workload,
+        "dtype": form.dtype,
+        "ms_per_step": round(ms, 5),
+        "value": round(form.throughput(ms), 3),
+        "unit": form.unit,
+        "work_per_step": form.work,
+        "roofline": {
+            "kernel": form.dom_name,
+            "bound": form.bound,
+            "achieved": round(achieved, 3),
+            "peak": form.peak,
+            "unit": "TFLOP/s" if form.bound == "mfma" else "GB/s",
+            "frac": round(achieved / form.peak, 4),
+            "traffic": None,
+            "avg_launch_us": round(dom_ms * 1e3, 3),
+            "work_per_launch": form.dom_work,
+        },
+        "wall_ms_incl_warmup": round(wall_ms, 2),
+    }
+    if isinstance(form, C4Retention):
+        rec["tflops_chunked_form"] = round(form.flops / (ms * 1e-3) / 1e12, 3)
+    if cpu_budget:
+        log(f"{form.name}: cpu baseline (~{cpu_budget:.0f}s)")
+        try:
+            rec["cpu_baseline"] = form.cpu(cpu_budget)
+        except MemoryError as exc:  # pragma: no cover
+            rec["cpu_baseline"] = {"error": str(exc)}
+    form.free()
+    torch.cuda.empty_cache()
+    return rec
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--forms", default="c1,c2,c3,c4,c5")
+    ap.add_argument("--cpu-budget", type=float, default=10.0,
+                    help="seconds of CPU oracle work for the headline form (others get a third)")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args(argv)
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} (WORLD_SIZE={world}) is not "
+              "supported; every config runs on one MI355X and reports that GPU's throughput.",
+              file=sys.stderr)
+        return 2
+    if int(os.environ.get("RANK", "0")) != 0:
+        return 0
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    from catopt_amd import _lib
+
+    _lib.load()  # loud if the HIP library is missing
+    dev = torch.device("cuda", 0)
+    names = [n.strip() for n in args.forms.split(",") if n.strip()]
+    for n in names:
+        if n not in FORMS:
+            print(f"unknown form {n!r}; choose from {sorted(FORMS)}", file=sys.stderr)
+            return 2
+    forms = {}
+    for n in names:
+        budget = None if args.no_cpu else (args.cpu_budget if n == HEADLINE else args.cpu_budget / 3)
+        forms[n] = measure(FORMS[n](), dev, args.steps, args.warmup, budget)
+        log(f"{n}: {forms[n]['value']} {forms[n]['unit']} ({forms[n]['ms_per_step']} ms/step, "
+            f"roofline frac {forms[n]['roofline']['frac']})")
+
+    head = forms.get(HEADLINE) or forms[names[0]]
+    head_name = HEADLINE if HEADLINE in forms else names[0]
+    line = {
+        "metric": METRIC,
+        "value": head["value"],
+        "unit": head["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": head["dtype"],
+        "data": "synthetic (seeded N(0,1) inputs and random-init weights of the config shapes)",
+        "config": {"workload": head["workload"], "form": head_name,
+                   "device": torch.cuda.get_device_name(0)},
+        "roofline": head["roofline"],
+        "cpu_baseline": head.get("cpu_baseline"),
+        "forms": forms,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
