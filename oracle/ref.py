@@ -497,15 +497,15 @@ def ssm_chunked(a, bx, c, x, h0, table):
         locs.append((P, H))
     # phase 2: carries in table order
     carries = []
-    cin = h
+    h_final = h
     for P, H in locs:
-        carries.append(cin)
-        cin = P * cin + H
+        carries.append(h_final)
+        h_final = P * h_final + H
     # phase 3: re-run each chunk from its carry
     y = np.empty((B, T, D), dtype=x.dtype)
-    for (s, e), cin in zip(zip(table[:-1], table[1:]), carries):
-        hh = cin
+    for (s, e), carry in zip(zip(table[:-1], table[1:]), carries):
+        hh = carry
         for t in range(s, e):
             hh = A[:, t] * hh + U[:, t]
             y[:, t] = np.einsum("bn,bdn->bd", c[:, t], hh)
-    return y, cin
+    return y, h_final

@@ -1,0 +1,89 @@
+"""The C ABI library loads and exports what ``include/catopt_hip.h`` declares (CPU only).
+
+No compute call is made here: only the version/strerror/workspace queries
+and argument checks that every entry point performs on the host before it
+touches the HIP runtime.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from catopt_amd import _lib as L
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+
+
+def _declared() -> set[str]:
+    names: set[str] = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(catopt_hip_\w+)\s*\(", text))
+    return names
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not L.LIB_PATH.exists():  # built by __graft_entry__.build(); build here only if absent
+        from catopt_amd import build
+
+        build.build()
+    return L.load()
+
+
+def test_header_and_binding_agree():
+    declared = _declared()
+    assert declared, "no catopt_hip_* declarations found"
+    assert declared == set(L.SIGNATURES), declared ^ set(L.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(L.LIB_PATH)], capture_output=True, text=True)
+    assert out.returncode == 0, out.stderr
+    exported = set(re.findall(r"\b(catopt_hip_\w+)$", out.stdout, flags=re.M))
+    missing = _declared() - exported
+    assert not missing, missing
+    for name in _declared():
+        assert getattr(lib, name) is not None
+
+
+def test_version_and_status_text(lib):
+    assert lib.catopt_hip_abi_version() == L.ABI_VERSION
+    assert lib.catopt_hip_strerror(L.OK) == b"ok"
+    assert lib.catopt_hip_strerror(L.E_WORKSPACE) == b"workspace too small"
+    assert lib.catopt_hip_strerror(99) == b"unknown status"
+    assert lib.catopt_hip_last_hip_error() == 0
+
+
+def test_workspace_queries(lib):
+    # retention: one d x d fp32 state per (b, h, segment); rejects other d / chunk
+    assert lib.catopt_hip_retention_workspace_bytes(1, 1, 64, 128, 64) >= 128 * 128 * 4
+    assert lib.catopt_hip_retention_workspace_bytes(1, 1, 64, 96, 64) == -1
+    assert lib.catopt_hip_retention_workspace_bytes(1, 1, 64, 128, 32) == -1
+    assert lib.catopt_hip_scan_workspace_bytes(10, 3) == 2 * 10 * 3 * 4
+    assert lib.catopt_hip_scan_workspace_bytes(-1, 3) == -1
+
+
+def test_host_argument_checks(lib):
+    # Each of these is rejected before any HIP call (bad sizes or enums).
+    assert lib.catopt_hip_rmsnorm(L.BF16, -1, 8, None, 8, None, 1e-6, None, 8, None) == L.E_INVAL
+    assert lib.catopt_hip_rmsnorm(L.BF16, 4, 8, None, 4, None, 1e-6, None, 8, None) == L.E_INVAL
+    assert lib.catopt_hip_rmsnorm(L.BF16, 0, 8, None, 8, None, 1e-6, None, 8, None) == L.OK
+    assert lib.catopt_hip_linear(L.BF16, 4, 4, 4, None, 4, None, 4, None, None, 9, None, 4, None) == L.E_INVAL
+    assert lib.catopt_hip_linear(7, 4, 4, 4, None, 4, None, 4, None, None, 0, None, 4, None) == L.E_UNSUPPORTED
+    assert lib.catopt_hip_linear(L.F32, 0, 4, 4, None, 4, None, 4, None, None, 0, None, 4, None) == L.OK
+    assert lib.catopt_hip_retention_fwd(L.BF16, 1, 1, 100, 128, 64, None, None, None, None, 1.0,
+                                        None, None, 0, None) == L.E_UNSUPPORTED
+    zeros = (C.c_int64 * 3)(0, 0, 0)
+    assert lib.catopt_hip_attn_fwd(L.BF16, 1, 1, 8, 8, 96, 96, None, zeros, None, zeros, None, zeros,
+                                   1.0, L.MASK_CAUSAL, 0, None, 0, 1, None, zeros, None, None,
+                                   None) in (L.E_UNSUPPORTED, L.E_INVAL)
+    table = (C.c_int64 * 2)(0, 4)
+    assert lib.catopt_hip_affd_scan(4, 8, None, 8, None, 8, None, table, 1, 7, None, None, None, 0,
+                                    None) == L.E_INVAL
