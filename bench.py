@@ -381,7 +381,31 @@ class C5SSM(Form):
                 "parity_max_rel": rel}
 
 
-FORMS = {f.name: f for f in (C1WeightChain, C2SwiGLU, C3Attention, C4Retention, C5SSM)}
+class CopyStream(Form):
+    """STREAM-style device copy of 2 GiB fp32: the measured-achievable HBM
+    figure reported beside the vendor peak, and the known-size kernel the
+    ``FETCH_SIZE`` / ``WRITE_SIZE`` counters are calibrated against."""
+
+    name, dtype, unit, bound = "copy", "f32", "GB/s", "hbm"
+    NBYTES = 2 << 30
+    workload = "device-to-device copy of 2 GiB fp32 (torch copy_ kernel), read + write"
+    peak = PEAK["hbm_gbs"]
+    work = dom_work = 2.0 * NBYTES
+    dom_name = "torch copy kernel"
+
+    def setup(self, dev):
+        import torch
+
+        self.src = torch.ones(self.NBYTES // 4, dtype=torch.float32, device=dev)
+        self.dst = torch.empty_like(self.src)
+
+    def step(self):
+        self.dst.copy_(self.src)
+
+    dominant = step
+
+
+FORMS = {f.name: f for f in (C1WeightChain, C2SwiGLU, C3Attention, C4Retention, C5SSM, CopyStream)}
 HEADLINE = "c2"
 
 
@@ -436,7 +460,7 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--forms", default="c1,c2,c3,c4,c5")
+    ap.add_argument("--forms", default="c1,c2,c3,c4,c5,copy")
     ap.add_argument("--cpu-budget", type=float, default=10.0,
                     help="seconds of CPU oracle work for the headline form (others get a third)")
     ap.add_argument("--no-cpu", action="store_true")

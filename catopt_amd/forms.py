@@ -1,0 +1,174 @@
+"""Constructors of the delivered terms for the five benchmark configurations.
+
+catopt's search extracts these terms on the CPU; the constructors spell them
+from the law right-hand sides that produce them, so tests and the benchmark
+can feed this package's sink exactly what the orchestrator would route:
+
+* :func:`weight_chain_form` — ``L`` stacked ``linear`` layers folded by
+  repeated ``ASSOC_LINEAR_BIAS`` (luisfuturist/catopt
+  ``packages/catopt-core/src/catopt_core/laws/tensor.py:1374-1394``):
+  ``linear(linear(x,A,b1),B,b2) → add(linear(x, matmul(B,A), matmul(B,b1)), b2)``,
+  applied from the innermost pair out;
+* :func:`swiglu_block_form` — ``RMS_NORM_FOLD`` (``tensor.py:712-741``) then
+  the ``SWIGLU_FUSE`` RHS (``tensor.py:1485-1519``) and the down projection;
+* :func:`causal_attention_form` — the ``OM_LIFT`` RHS (``om.py:153-193``)
+  over ``masked_fill(q kᵀ / √d, ¬mask, -inf)`` with a bool lower-triangular
+  mask Param (or the ``cmask`` generator);
+* :func:`retention_kway_form` — ``om_decayed_kway_blocks(K)``
+  (``om.py:3040-3210``), built arm by arm as ``_kway_rhs`` spells it;
+* :func:`scan_final_form` / :func:`scan_prefix_form` — the diagonal-affine
+  chain ``applyd(affd_compose(…), h)`` and its stacked all-prefix form
+  (``xcarrier.py:2252-2273``), with leaves reading step ``t`` of shared
+  ``a`` / ``u`` arrays.
+
+Each returns ``(IR, param_shapes)``; parameter values come from the caller.
+"""
+
+from __future__ import annotations
+
+import math
+
+from .ir import IR, Const, Op, Param, TensorType, Var
+
+__all__ = [
+    "weight_chain_form",
+    "swiglu_block_form",
+    "causal_attention_form",
+    "retention_kway_form",
+    "retention_block_form",
+    "scan_final_form",
+    "scan_prefix_form",
+]
+
+mk = Op.make
+
+
+def weight_chain_form(L: int = 8, d: int = 512, rows: int = 64) -> tuple[IR, dict]:
+    """``add(…add(linear(x, W_eff, c_0), c_1)…, c_{L-1})`` with ``W_eff`` and
+    every ``c_i`` spelled as ``matmul`` chains of the layer Params."""
+    x = Var("x", TensorType((rows, d)))
+    Ws = [Param(f"W{i + 1}", TensorType((d, d))) for i in range(L)]
+    bs = [Param(f"b{i + 1}", TensorType((d,))) for i in range(L)]
+    W = Ws[0]
+    adds: list = [bs[0]]
+    for Wl, bl in zip(Ws[1:], bs[1:]):
+        W = mk("matmul", Wl, W)
+        adds = [mk("matmul", Wl, c) for c in adds] + [bl]
+    y = mk("linear", x, W, adds[0])
+    for c in adds[1:]:
+        y = mk("add", y, c)
+    shapes = {p.name: p.typ.shape for p in Ws + bs}
+    return IR(y, [x]), shapes
+
+
+def swiglu_block_form(rows_shape=(8, 2048), D: int = 4096, F: int = 11008,
+                      eps: float = 1e-6) -> tuple[IR, dict]:
+    """``linear(mul(silu(chunk(Y, 2, -1, 0)), chunk(Y, 2, -1, 1)), W_down)``,
+    ``Y = linear(rms_norm(x, γ), concat(W_gate, W_up, dim=0))``."""
+    x = Var("x", TensorType((*rows_shape, D)))
+    g = Param("gamma", TensorType((D,)))
+    wg, wu = Param("W_gate", TensorType((F, D))), Param("W_up", TensorType((F, D)))
+    wd = Param("W_down", TensorType((D, F)))
+    h = mk("rms_norm", x, g, dim=(D,), eps=eps)
+    y = mk("linear", h, mk("concat", wg, wu, dim=0))
+    gate = mk("chunk", y, chunks=2, dim=-1, index=0)
+    up = mk("chunk", y, chunks=2, dim=-1, index=1)
+    out = mk("linear", mk("mul", mk("silu", gate), up), wd)
+    return IR(out, [x]), {"gamma": (D,), "W_gate": (F, D), "W_up": (F, D), "W_down": (D, F)}
+
+
+def causal_attention_form(B: int = 4, H: int = 32, T: int = 4096, d: int = 128,
+                          mask: str = "param") -> tuple[IR, dict]:
+    """``om_apply(om_elem(masked_fill(q kᵀ / √d, ¬mask, -inf), v))``.
+
+    ``mask="param"``: a bool keep-mask Param ``mask (T, T)`` (lower
+    triangle); ``mask="cmask"``: the causal generator ``cmask(s, off=0)``."""
+    q, k, v = (Var(n, TensorType((B, H, T, d))) for n in "qkv")
+    s = mk("div", mk("matmul", q, mk("transpose", k, dim0=-2, dim1=-1)), Const(math.sqrt(d)))
+    shapes = {}
+    if mask == "param":
+        m = Param("mask", TensorType((T, T)))
+        masked = mk("logical_not", m)
+        shapes["mask"] = (T, T)
+    elif mask == "cmask":
+        masked = mk("cmask", s, off=0)
+    else:
+        raise ValueError(mask)
+    sm = mk("masked_fill", s, masked, Const(float("-inf")))
+    return IR(mk("om_apply", mk("om_elem", sm, v)), [q, k, v]), shapes
+
+
+def _kway_rhs(s, v, g, K: int, C: int):
+    SZ = (C,) * K
+
+    def score(i, j):
+        return mk("split", mk("split", s, sizes=SZ, dim=-2, index=i), sizes=SZ, dim=-1, index=j)
+
+    def value(j):
+        return mk("split", v, sizes=SZ, dim=-2, index=j)
+
+    blocks = []
+    for i in range(K):
+        acc = mk("om_decayed", score(i, i), mk("decay", g, t=C), value(i))
+        for j in range(i):
+            row = mk("unsqueeze", mk("decay_vec", g, t=C, offset=(i - j) * C), dim=-1)
+            col = mk("unsqueeze", mk("decay_vec", g, t=C, sign=-1), dim=-2)
+            acc = mk("add", acc, mk("mul", row, mk("matmul", mk("mul", score(i, j), col), value(j))))
+        blocks.append(acc)
+    out = blocks[-1]
+    for blk in reversed(blocks[:-1]):
+        out = mk("concat", blk, out, dim=-2)
+    return out
+
+
+def retention_kway_form(B: int = 4, H: int = 16, T: int = 8192, d: int = 128, C: int = 64,
+                        scale: float | None = None) -> tuple[IR, dict]:
+    """The K-way chunked form (``K = T / C``) of
+    ``om_decayed(s, decay(γ, T), v)`` with ``s = q kᵀ`` (``/ 1/scale`` when
+    ``scale`` is given, spelled as a ``div`` by the constant)."""
+    if T % C:
+        raise ValueError("T must be a multiple of C")
+    q, k, v = (Var(n, TensorType((B, H, T, d))) for n in "qkv")
+    g = Param("gamma", TensorType((H,)))
+    s = mk("matmul", q, mk("transpose", k, dim0=-2, dim1=-1))
+    if scale is not None:
+        s = mk("div", s, Const(1.0 / scale))
+    return IR(_kway_rhs(s, v, g, T // C, C), [q, k, v]), {"gamma": (H,)}
+
+
+def retention_block_form(B: int, H: int, T: int, d: int = 128) -> tuple[IR, dict]:
+    """The un-chunked source ``om_decayed(q kᵀ, decay(γ, T), v)``."""
+    q, k, v = (Var(n, TensorType((B, H, T, d))) for n in "qkv")
+    g = Param("gamma", TensorType((H,)))
+    s = mk("matmul", q, mk("transpose", k, dim0=-2, dim1=-1))
+    return IR(mk("om_decayed", s, mk("decay", g, t=T), v), [q, k, v]), {"gamma": (H,)}
+
+
+def _leaf(a, u, t: int):
+    return mk("aff_diag", mk("select", a, dim=0, index=t), mk("select", u, dim=0, index=t))
+
+
+def scan_final_form(T: int, state_shape: tuple) -> tuple[IR, dict]:
+    """``applyd(f_{T-1} ∘ … ∘ f_0, h)``, ``f_t = aff_diag(a[t], u[t])``, as a
+    left-leaning compose chain (leaf 0 of the product is the last step)."""
+    a = Var("a", TensorType((T, *state_shape)))
+    u = Var("u", TensorType((T, *state_shape)))
+    h = Var("h", TensorType(tuple(state_shape)))
+    F = _leaf(a, u, 0)
+    for t in range(1, T):
+        F = mk("affd_compose", _leaf(a, u, t), F)
+    return IR(mk("applyd", F, h), [a, u, h]), {}
+
+
+def scan_prefix_form(T: int, state_shape: tuple) -> tuple[IR, dict]:
+    """``applyd(aff_diag(stack(affd_a f_t), stack(affd_b f_t)), h)`` over the
+    prefixes ``f_t = f_{t-1} ∘ leaf_t``: every state ``h_0 … h_{T-1}``."""
+    a = Var("a", TensorType((T, *state_shape)))
+    u = Var("u", TensorType((T, *state_shape)))
+    h = Var("h", TensorType(tuple(state_shape)))
+    fs = [_leaf(a, u, 0)]
+    for t in range(1, T):
+        fs.append(mk("affd_compose", _leaf(a, u, t), fs[-1]))
+    A = mk("stack", *[mk("affd_a", f) for f in fs], dim=0)
+    Bm = mk("stack", *[mk("affd_b", f) for f in fs], dim=0)
+    return IR(mk("applyd", mk("aff_diag", A, Bm), h), [a, u, h]), {}

@@ -292,6 +292,7 @@ def om_compose(f, g):
 # ----------------------------------------------------------------- retention
 
 RETENTION_CHUNK = 64
+RETENTION_HEAD_DIM = 128
 
 
 def retention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma: torch.Tensor,

@@ -1,0 +1,342 @@
+"""Host logic of the HIP sink on the CPU: term model, weight fold, epilogue
+fusion, the three executor plans, routing, verify and the fallback contract.
+
+The HIP-backed ops are swapped for torch functions through the op-table seam
+(``tests/cpu_table.py``); every numeric check compares against the numpy
+oracle in float64.  Planted mistakes (a wrong offset, a missing cross block,
+a flipped sign, a shifted mask) must make the plan decline.
+"""
+
+from __future__ import annotations
+
+import json
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from catopt_amd import forms
+from catopt_amd.evaluator import HipIRModule
+from catopt_amd.executors import (
+    HipChunkedDecayModule,
+    HipOMModule,
+    HipScanModule,
+    build_decayed_plan,
+    build_scan_plan,
+    prefix_chunk_table,
+)
+from catopt_amd.executors.om import _triangle_offset, parse_score
+from catopt_amd.ir import IR, Const, Op, Param, TensorType, Var, postorder, term_from_data, term_to_data
+from catopt_amd.sink import HipSink, route_spec, verify_equiv
+from tests.cpu_table import cpu_table
+
+mk = Op.make
+
+
+def _np(t):
+    return t.detach().double().numpy()
+
+
+# ------------------------------------------------------------------ term model
+
+
+def test_op_interning_and_spelling_strict_identity():
+    x = Var("x", TensorType((2, 3)))
+    a = mk("mul", x, Const(2))
+    assert mk("mul", x, Const(2)) is a
+    assert mk("mul", x, Const(2.0)) is not a  # Const(2) != Const(2.0)
+    assert mk("sum", x, dim=0) is not mk("sum", x, dim=0.0)
+    assert hash(mk("add", a, a)) == hash(mk("add", a, a))
+
+
+def test_wire_format_round_trip():
+    ir, _ = forms.retention_kway_form(1, 2, 256, 128, 64, scale=0.5)
+    data = term_to_data(ir.root)
+    back = term_from_data(json.loads(json.dumps(data)))
+    assert back is ir.root  # interning gives back the very same object
+    ir3, _ = forms.causal_attention_form(1, 1, 64, 64, mask="cmask")
+    assert term_from_data(json.loads(json.dumps(term_to_data(ir3.root)))) is ir3.root
+
+
+def test_postorder_deep_chain_has_no_recursion_limit():
+    ir, _ = forms.scan_final_form(5000, (4,))
+    nodes = postorder(ir.root)
+    assert nodes[-1] is ir.root
+    assert len(nodes) == 1 + 3 * 5000 + 4999
+    pos = {n: i for i, n in enumerate(nodes)}
+    for n in nodes:
+        for a in n.args:
+            if isinstance(a, Op):
+                assert pos[a] < pos[n]
+
+
+# ------------------------------------------------------------- generic module
+
+
+def _chain_values(L, d, seed=0):
+    torch.manual_seed(seed)
+    layers = [torch.nn.Linear(d, d) for _ in range(L)]  # fp32: the GEMM kernels' dtype
+    vals = {}
+    for i, l in enumerate(layers):
+        vals[f"W{i + 1}"] = l.weight.detach()
+        vals[f"b{i + 1}"] = l.bias.detach()
+    return layers, vals
+
+
+def test_weight_chain_folds_to_one_gemm_with_bias():
+    L, d = 5, 32
+    ir, _ = forms.weight_chain_form(L, d, rows=7)
+    layers, vals = _chain_values(L, d)
+    mod = HipIRModule(ir, vals, ops=cpu_table())
+    assert [s[0] for s in mod._tape.steps] == ["hip_linear"]
+    assert mod.stats["fused"] == {"linear": 1, "bias_add": L - 1}
+    x = torch.randn(7, d)
+    ref = oracle.linear_chain(_np(x), [_np(l.weight) for l in layers], [_np(l.bias) for l in layers])
+    rep = oracle.verify_equiv(ref, _np(mod(x)), rtol=1e-5)
+    assert rep["passed"], rep
+
+
+def test_weight_chain_fold_pins_the_bias_spine():
+    # Planted mistake on the oracle side: dropping one pushed-through addend
+    # must be caught by the same comparison.
+    L, d = 4, 16
+    ir, _ = forms.weight_chain_form(L, d, rows=3)
+    layers, vals = _chain_values(L, d, seed=1)
+    W, adds = oracle.fold_linear_chain([_np(l.weight) for l in layers], [_np(l.bias) for l in layers])
+    x = torch.randn(3, d)
+    out = _np(HipIRModule(ir, vals, ops=cpu_table())(x))
+    assert oracle.verify_equiv(oracle.folded_chain_forward(_np(x), W, adds), out, rtol=1e-5)["passed"]
+    assert not oracle.verify_equiv(oracle.folded_chain_forward(_np(x), W, adds[:-1]), out, rtol=1e-6)["passed"]
+
+
+def test_swiglu_block_fuses_to_norm_and_two_gemms():
+    D, F_ = 16, 24
+    ir, shapes = forms.swiglu_block_form((2, 5), D, F_)
+    g = torch.Generator().manual_seed(3)
+    vals = {n: (torch.randn(s, generator=g) * (0.2 if n != "gamma" else 1)).to(torch.bfloat16)
+            for n, s in shapes.items()}
+    mod = HipIRModule(ir, vals, ops=cpu_table())
+    assert [s[0] for s in mod._tape.steps] == ["rms_norm", "hip_swiglu", "hip_linear"]
+    # the concat was folded into one weight; the separate halves are pruned
+    assert "W_gate" not in mod._param_map and "W_up" not in mod._param_map
+    x = torch.randn(2, 5, D, generator=g).to(torch.bfloat16)
+    h = oracle.rms_norm(_np(x), _np(vals["gamma"]), 1e-6)
+    ref = oracle.swiglu_fused(h, _np(vals["W_gate"]), _np(vals["W_up"]), _np(vals["W_down"]))
+    out = _np(mod(x).float())
+    assert oracle.verify_equiv(ref, out, rtol=2e-2)["passed"]
+    assert oracle.verify_equiv(oracle.swiglu_unfused(h, _np(vals["W_gate"]), _np(vals["W_up"]),
+                                                     _np(vals["W_down"])), out, rtol=2e-2)["passed"]
+
+
+def test_unfused_swiglu_spelling_takes_the_paired_epilogue_path():
+    x = Var("x", TensorType((4, 8)))
+    A, B = Param("A", TensorType((6, 8))), Param("B", TensorType((6, 8)))
+    root = mk("mul", mk("silu", mk("linear", x, A)), mk("linear", x, B))
+    vals = {"A": torch.randn(6, 8, dtype=torch.float64), "B": torch.randn(6, 8, dtype=torch.float64)}
+    mod = HipIRModule(IR(root, [x]), vals, ops=cpu_table())
+    # fp64 weights are outside the GEMM kernels' dtypes: nothing is fused
+    assert [s[0] for s in mod._tape.steps] == ["linear", "silu", "linear", "mul"]
+    vals16 = {k: v.to(torch.bfloat16) for k, v in vals.items()}
+    mod16 = HipIRModule(IR(root, [x]), vals16, ops=cpu_table())
+    assert [s[0] for s in mod16._tape.steps] == ["hip_swiglu"]
+    xx = torch.randn(4, 8).to(torch.bfloat16)
+    ref = oracle.silu(_np(xx) @ _np(vals16["A"]).T) * (_np(xx) @ _np(vals16["B"]).T)
+    assert oracle.verify_equiv(ref, _np(mod16(xx).float()), rtol=2e-2)["passed"]
+
+
+def test_missing_binding_is_loud():
+    x = Var("x", TensorType((2,)))
+    mod = HipIRModule(IR(mk("frobnicate", x), [x]), {}, ops=cpu_table())
+    with pytest.raises(ValueError, match="No HIP binding"):
+        mod(torch.zeros(2))
+
+
+# ----------------------------------------------------------------- om plan
+
+
+def test_triangle_offset_brute_force():
+    for t, k in [(8, 8), (5, 9), (9, 5), (1, 4)]:
+        for off in range(-k - 1, t + 2):
+            keep = torch.ones(t, k, dtype=torch.bool).tril(-off)
+            got = _triangle_offset(~keep)
+            if keep.any():
+                ref_keep = torch.ones(t, k, dtype=torch.bool).tril(-got)
+                assert torch.equal(ref_keep, keep), (t, k, off, got)
+            else:
+                assert got is None
+    m = torch.ones(6, 6, dtype=torch.bool).tril()
+    m[3, 1] = False  # one flipped bit is no longer a triangle
+    assert _triangle_offset(~m) is None
+
+
+def test_om_plan_causal_param_mask_and_cmask():
+    ir, shapes = forms.causal_attention_form(1, 2, 16, 64, mask="param")
+    vals = {"mask": torch.ones(16, 16, dtype=torch.bool).tril()}
+    mod = HipOMModule(ir, vals, ops=cpu_table())
+    lf = mod._plan["leaves"][0]
+    assert lf["mask_kind"] == "causal" and lf["causal_off"] == 0
+    assert math.isclose(lf["scale"], 1 / 8.0)
+    ir2, _ = forms.causal_attention_form(1, 2, 16, 64, mask="cmask")
+    mod2 = HipOMModule(ir2, {}, ops=cpu_table())
+    assert mod2._plan["leaves"][0]["mask_kind"] == "causal"
+    # a shifted triangle keeps its offset; a random mask becomes a keep-mask
+    vals3 = {"mask": torch.ones(16, 16, dtype=torch.bool).tril(2)}
+    assert HipOMModule(ir, vals3, ops=cpu_table())._plan["leaves"][0]["causal_off"] == 2
+    vals4 = {"mask": torch.rand(16, 16, generator=torch.Generator().manual_seed(0)) < 0.5}
+    lf4 = HipOMModule(ir, vals4, ops=cpu_table())._plan["leaves"][0]
+    assert lf4["mask_kind"] == "bool_const" and torch.equal(lf4["keep"], vals4["mask"])
+
+
+def test_om_parse_declines_a_finite_fill_and_an_untransposed_key():
+    q, k = Var("q", TensorType((4, 8))), Var("k", TensorType((4, 8)))
+    s = mk("matmul", q, mk("transpose", k, dim0=-2, dim1=-1))
+    m = Param("m", TensorType((4, 4)))
+    assert parse_score(mk("masked_fill", s, m, Const(float("-inf")))) is not None
+    assert parse_score(mk("masked_fill", s, m, Const(-1e9))) is None
+    assert parse_score(mk("matmul", q, k)) is None
+    assert parse_score(mk("matmul", q, mk("transpose", k, dim0=0, dim1=1))) is not None  # 2-D dims are free
+    sc = parse_score(mk("mul", mk("div", s, Const(4.0)), Const(3.0)))
+    assert math.isclose(sc["scale"], 0.75)
+
+
+def test_om_module_falls_back_on_host_inputs():
+    ir, _ = forms.causal_attention_form(1, 2, 16, 64, mask="param")
+    vals = {"mask": torch.ones(16, 16, dtype=torch.bool).tril()}
+    mod = HipOMModule(ir, vals, ops=cpu_table())
+    q, k, v = (torch.randn(1, 2, 16, 64, dtype=torch.float64) for _ in range(3))
+    out = mod(q, k, v)
+    assert mod.fallbacks == 1
+    ref = oracle.attention_om(_np(q), _np(k), _np(v), 1 / 8.0, causal=True)
+    assert oracle.verify_equiv(ref, _np(out), rtol=1e-12)["passed"]
+
+
+# --------------------------------------------------------------- decayed plan
+
+
+def _kway(K, C, *, off_bump=None, drop=None, sign=-1, swap=None, scale_div=None):
+    """The K-way RHS with optional planted mistakes."""
+    T = K * C
+    q, k, v = (Var(n, TensorType((1, 2, T, 128))) for n in "qkv")
+    g = Param("gamma", TensorType((2,)))
+    s = mk("matmul", q, mk("transpose", k, dim0=-2, dim1=-1))
+    if scale_div is not None:
+        s = mk("div", s, Const(scale_div))
+    SZ = (C,) * K
+
+    def score(i, j):
+        return mk("split", mk("split", s, sizes=SZ, dim=-2, index=i), sizes=SZ, dim=-1, index=j)
+
+    def value(j):
+        return mk("split", v, sizes=SZ, dim=-2, index=j)
+
+    blocks = []
+    for i in range(K):
+        acc = mk("om_decayed", score(i, i), mk("decay", g, t=C), value(i))
+        for j in range(i):
+            if drop == (i, j):
+                continue
+            off = (i - j) * C + (1 if off_bump == (i, j) else 0)
+            jj = swap[1] if swap is not None and swap[0] == (i, j) else j
+            row = mk("unsqueeze", mk("decay_vec", g, t=C, offset=off), dim=-1)
+            col = mk("unsqueeze", mk("decay_vec", g, t=C, sign=sign), dim=-2)
+            acc = mk("add", acc, mk("mul", row, mk("matmul", mk("mul", score(i, jj), col), value(jj))))
+        blocks.append(acc)
+    out = blocks[-1]
+    for blk in reversed(blocks[:-1]):
+        out = mk("concat", blk, out, dim=-2)
+    return IR(out, [q, k, v])
+
+
+def test_decayed_plan_accepts_the_kway_form_and_pins_its_integers():
+    p = build_decayed_plan(_kway(4, 32, scale_div=2.0).root)
+    assert (p["K"], p["C"]) == (4, 32) and math.isclose(p["scale"], 0.5)
+    assert build_decayed_plan(_kway(4, 32, off_bump=(2, 0)).root) is None
+    assert build_decayed_plan(_kway(4, 32, drop=(3, 1)).root) is None
+    assert build_decayed_plan(_kway(4, 32, sign=1).root) is None
+    assert build_decayed_plan(_kway(4, 32, swap=((3, 1), 2)).root) is None
+    ir, _ = forms.retention_kway_form(1, 2, 256, 128, 64)
+    assert build_decayed_plan(ir.root)["K"] == 4
+    irb, _ = forms.retention_block_form(1, 2, 128)
+    assert build_decayed_plan(irb.root)["K"] == 1
+
+
+def test_kway_form_equals_the_quadratic_form_on_cpu():
+    # The plan keeps only (q, k, v, γ, scale): legitimate because every K-way
+    # form equals the quadratic one.  Check that through the generic module.
+    ir = _kway(4, 8, scale_div=4.0)
+    gam = torch.tensor([0.9, 0.75], dtype=torch.float64)
+    mod = HipChunkedDecayModule(ir, {"gamma": gam}, ops=cpu_table())
+    assert mod.n_chunks == 4
+    q, k, v = (torch.randn(1, 2, 32, 128, dtype=torch.float64) * 0.1 for _ in range(3))
+    out = mod(q, k, v)  # host inputs: the generic module runs (fallback)
+    assert mod.fallbacks == 1
+    ref = oracle.retention_quadratic(_np(q), _np(k), _np(v), _np(gam), 0.25)
+    assert oracle.verify_equiv(ref, _np(out), rtol=1e-12)["passed"]
+
+
+# ------------------------------------------------------------------ scan plan
+
+
+def test_prefix_chunk_table_matches_the_blocked_plan():
+    for T in list(range(1, 300)) + [16384, 16385, 99991]:
+        assert prefix_chunk_table(T) == list(oracle.prefix_chunk_table(T)), T
+
+
+def test_scan_plans_final_and_prefix():
+    ir, _ = forms.scan_final_form(7, (3,))
+    p = build_scan_plan(ir.root)
+    assert p["mode"] == "final" and len(p["leaves"]) == 7 and p["gather"] is not None
+    irp, _ = forms.scan_prefix_form(7, (3,))
+    pp = build_scan_plan(irp.root)
+    assert pp["mode"] == "prefix" and len(pp["leaves"]) == 7
+    # a stacked form whose members are not successive prefixes is declined
+    a, u, h = (Var(n, TensorType((3,))) for n in "auh")
+    f0 = mk("aff_diag", a, u)
+    f1 = mk("affd_compose", mk("aff_diag", u, a), f0)
+    bad = mk("applyd", mk("aff_diag", mk("stack", mk("affd_a", f1), mk("affd_a", f0)),
+                          mk("stack", mk("affd_b", f1), mk("affd_b", f0))), h)
+    assert build_scan_plan(bad) is None
+
+
+def test_scan_module_fallback_matches_the_serial_recurrence():
+    T, S = 9, 5
+    ir, _ = forms.scan_final_form(T, (S,))
+    mod = HipScanModule(ir, {}, ops=cpu_table())
+    a = torch.rand(T, S, dtype=torch.float64)
+    u = torch.randn(T, S, dtype=torch.float64)
+    h = torch.randn(S, dtype=torch.float64)
+    out = mod(a, u, h)
+    assert mod.fallbacks == 1
+    ref = oracle.serial_affd_scan(_np(a), _np(u), _np(h))[-1]
+    assert oracle.verify_equiv(ref, _np(out), rtol=1e-12)["passed"]
+    irp, _ = forms.scan_prefix_form(T, (S,))
+    modp = HipScanModule(irp, {}, ops=cpu_table())
+    refp = oracle.serial_affd_scan(_np(a), _np(u), _np(h))
+    assert oracle.verify_equiv(refp, _np(modp(a, u, h)), rtol=1e-12)["passed"]
+
+
+# ---------------------------------------------------------------------- sink
+
+
+def test_sink_surface_routing_and_verify():
+    sink = HipSink(device="cpu", ops=cpu_table())
+    names = list(sink.executors)
+    assert names == ["om_decayed_chunked", "scan", "om_batched", "generic"]
+    assert sink.executors["generic"].carrier is None
+    assert {"linear", "matmul", "rms_norm", "om_elem", "om_compose", "om_apply", "om_decayed",
+            "decay", "decay_vec", "aff_diag", "affd_compose", "applyd"} <= sink.supported_ops
+    cases = [
+        (forms.retention_kway_form(1, 2, 128, 128, 64)[0], "om_decayed_chunked"),
+        (forms.scan_final_form(4, (2,))[0], "scan"),
+        (forms.causal_attention_form(1, 1, 8, 64, mask="cmask")[0], "om_batched"),
+    ]
+    for ir, want in cases:
+        assert route_spec(ir.root, sink).name == want
+    assert route_spec(forms.weight_chain_form(2, 8, 2)[0].root, sink) is None
+    ref = torch.tensor([1.0, -2.0])
+    assert verify_equiv(ref, ref + 1e-5, rtol=1e-4).passed
+    rep = verify_equiv(ref, torch.tensor([1.0, float("nan")]))
+    assert not rep.passed
+    assert math.isclose(verify_equiv(ref, torch.tensor([1.0, -2.1])).max_rel, 0.1 / (2 + 1e-8), rel_tol=1e-6)
