@@ -347,13 +347,30 @@ def decay_vec(gamma: torch.Tensor, t: int, offset: int = 0, sign: int = 1) -> to
 # ---------------------------------------------------------------------- scans
 
 
+_TABLES: dict = {}
+
+
 def _chunk_table(chunk_starts: Sequence[int] | torch.Tensor, T: int, device) -> tuple[torch.Tensor, int]:
-    cs = torch.as_tensor(chunk_starts, dtype=torch.int64).cpu()
-    if cs.dim() != 1 or cs.numel() < 2:
+    """The validated int64 chunk table on ``device``.
+
+    Validated on the host every call (the kernels index with it); the
+    device copy is cached per (table, device), so a forward recorded into a
+    hipGraph after a warm-up call makes no host-to-device copy."""
+    if isinstance(chunk_starts, torch.Tensor):
+        chunk_starts = chunk_starts.detach().cpu().tolist()
+    key_vals = tuple(int(c) for c in chunk_starts)
+    if len(key_vals) < 2:
         raise ValueError("chunk table needs at least [0, T]")
-    if int(cs[0]) != 0 or int(cs[-1]) != T or bool((cs[1:] <= cs[:-1]).any()) and T > 0:
+    if key_vals[0] != 0 or key_vals[-1] != T or (T > 0 and any(b <= a for a, b in zip(key_vals, key_vals[1:]))):
         raise ValueError(f"chunk table must rise strictly from 0 to T={T}")
-    return cs.to(device), cs.numel() - 1
+    key = (key_vals, str(device))
+    cs = _TABLES.get(key)
+    if cs is None:
+        if len(_TABLES) > 256:
+            _TABLES.clear()
+        cs = torch.tensor(key_vals, dtype=torch.int64).to(device)
+        _TABLES[key] = cs
+    return cs, len(key_vals) - 1
 
 
 def affd_scan(a: torch.Tensor, u: torch.Tensor, h0: torch.Tensor | None,

@@ -64,6 +64,9 @@ def test_weight_chain_full_config_with_graph_replay(sink, dev):
         torch.cuda.synchronize()
         _gate(ref, y, 1e-5)
         _ = torch.ones(8, device=dev).sum().item()
+    x2 = torch.randn(64, 512)
+    ref2 = oracle.linear_chain(x2.double().numpy(), [_np(l.weight) for l in layers], [_np(l.bias) for l in layers])
+    _gate(ref2, mod(x2.to(dev)).clone(), 1e-5)
 
 
 def _spelled_swiglu(D, F_, rows_shape, eps=1e-6):
@@ -108,6 +111,9 @@ def test_causal_attention_executor(sink, dev, mask):
     assert res.module.fallbacks == 0
     ref = oracle.attention_om(_np(q), _np(k), _np(v), 1 / math.sqrt(d), causal=True)
     _gate(ref, out, 2e-2)
+    q2 = _rand((B, H, T, d), torch.bfloat16, 99)  # replay on new inputs recomputes
+    out2 = res.module(q2.to(dev), k.to(dev), v.to(dev)).clone()
+    _gate(oracle.attention_om(_np(q2), _np(k), _np(v), 1 / math.sqrt(d), causal=True), out2, 2e-2)
 
 
 def test_attention_two_key_blocks_compose(sink, dev):
@@ -161,6 +167,10 @@ def test_retention_kway_executor(sink, dev, C):
     ref = oracle.retention_kway(_np(q), _np(k), _np(v), gam.double().numpy(), T // C, 0.5)
     _gate(ref, out, 2e-2)
     _gate(oracle.retention_quadratic(_np(q), _np(k), _np(v), gam.double().numpy(), 0.5), out, 2e-2)
+    assert res.stats["cuda_graph"] is True
+    v2 = _rand((B, H, T, 128), torch.bfloat16, 77, 1 / math.sqrt(128))
+    out2 = res.module(q.to(dev), k.to(dev), v2.to(dev)).clone()
+    _gate(oracle.retention_quadratic(_np(q), _np(k), _np(v2), gam.double().numpy(), 0.5), out2, 2e-2)
 
 
 def test_retention_verified_against_the_spelled_block_form(sink, dev):
@@ -184,7 +194,13 @@ def test_scan_executor(sink, dev, form):
     ins = tuple(torch.from_numpy(z).to(dev) for z in (a, u, h))
     res = deliver(ir, {}, sink, ins, runner=HipGraphRunner())
     assert res.stats["executor"] == "scan" and res.stats["hip_kernel"]
+    assert res.stats["cuda_graph"] is True and res.module.is_graph_captured
     out = res.module(*ins).clone()
     assert res.module.fallbacks == 0
     ref = oracle.serial_affd_scan(a.astype(np.float64), u.astype(np.float64), h.astype(np.float64))
     _gate(ref[-1] if form == "final" else ref, out, 1e-5)
+    # the replay recomputes from the new inputs (not the captured call's output)
+    a2 = rng.uniform(0.2, 0.9, (T, S)).astype(np.float32)
+    out2 = res.module(torch.from_numpy(a2).to(dev), ins[1], ins[2]).clone()
+    ref2 = oracle.serial_affd_scan(a2.astype(np.float64), u.astype(np.float64), h.astype(np.float64))
+    _gate(ref2[-1] if form == "final" else ref2, out2, 1e-5)
