@@ -1,62 +1,81 @@
 // Online-softmax attention forward for gfx950 (bf16 in, fp32 math).
 //
-// Transposed FlashAttention formulation chosen for the 32x32 MFMA layouts:
+// Transposed FlashAttention formulation for the 32x32x16 MFMA layouts:
 //
 //   Sᵀ = K · Qᵀ      A = K tile from LDS (key rows, d contiguous),
 //                    B = Q fragments held in registers for the whole loop.
-//   Oᵀ += Vᵀ · Pᵀ    A = Vᵀ from LDS, B = P straight from the Sᵀ
-//                    accumulator registers (converted to bf16).
+//   Oᵀ += Vᵀ · Pᵀ    A = Vᵀ read from the row-major V tile with the gfx950
+//                    transposing LDS read (ds_read_b64_tr_b16),
+//                    B = P straight from the Sᵀ accumulator (bf16).
 //
 // In both products the accumulator's column is the query, so every lane
-// owns exactly one query: the running max m, the denominator l and the
-// rescale of Oᵀ are lane-local, and only one cross-half shuffle per KV tile
-// (the row max) is needed.  Feeding P from the accumulator works because
-// the MFMA's k index is only a summation order: the PV product pairs
-// accumulator register r of half g with key 8*(r/4) + 4*g + r%4, and Vᵀ is
-// read from LDS with the same key permutation (two 8-byte runs per lane).
+// owns one query per 32-query block: the running max, the denominator and
+// the rescale of Oᵀ are lane-local, and only one cross-half shuffle per KV
+// tile is needed.  P feeds the PV product from the accumulator because the
+// MFMA's k index is only a summation order: accumulator register r of half
+// g holds key 8*(r/4) + 4*g + r%4, and the A operand is read with the same
+// key permutation (two runs of four consecutive keys per lane, which is one
+// transposing read each).
 //
-// Work split: one workgroup = 4 waves = 128 queries of one (b, h); each
-// wave 32 queries.  KV tiles of 64 keys are double buffered in LDS: K as
-// [key][d] with 16-byte chunks XOR-swizzled by the key, V transposed to
-// [d][key] with 8-byte key groups XOR-swizzled by d/2, both conflict-free
-// for the fragment reads.  Causal grids launch the longest query tiles
-// first.  Softmax runs in the exp2 domain with scale·log2(e) folded in.
+// Work split: one workgroup = 4 waves = 256 queries of one (b, h); each wave
+// owns 64 queries (two 32-query blocks) so every K / V fragment read from
+// LDS feeds two MFMAs.  KV tiles of 64 keys are double buffered in LDS and
+// filled by direct global->LDS loads (global_load_lds_dwordx4: no register
+// staging); K and V rows are 256 bytes with the 16-byte chunk index
+// XOR-swizzled by (key & 15).  A partial last tile zero-fills its missing V
+// rows.  Causal grids launch the longest query tiles first, skip tiles past
+// each wave's last key and apply the mask only on diagonal tiles.
+//
+// Softmax runs in the exp2 domain: p = exp2((s - m) * c), c = scale·log2(e).
+// The running max is only moved (and Oᵀ, l rescaled) when a tile raises it
+// by more than kLazy/c; between moves p ≤ 2^kLazy, exact in fp32 and
+// bf16's exponent range, and a / l is unchanged.  The true row max is
+// tracked separately so the emitted (m, l, a) carrier is the om_elem one.
 #include "common.hpp"
 
 namespace catopt {
 namespace {
 
-constexpr int NT = 256;  // 4 waves
-constexpr int QT = 128;  // queries per workgroup
-constexpr int KVB = 64;  // keys per KV tile
+constexpr int NT = 256;   // 4 waves
+constexpr int QW = 64;    // queries per wave
+constexpr int QT = 256;   // queries per workgroup
+constexpr int KVB = 64;   // keys per KV tile
+constexpr float kLazy = 8.0f;
+
+typedef __attribute__((ext_vector_type(4))) short s16x4;
+typedef __attribute__((address_space(3))) void* lds_ptr;
 
 template <int D>
 struct AttnLds {
-  static constexpr int K_ELEMS = KVB * D;
-  static constexpr int V_ELEMS = D * KVB;
-  static constexpr int STAGE = K_ELEMS + V_ELEMS;
-  static constexpr int BYTES = 2 * STAGE * 2;
-  static constexpr int KCH = D / 8;  // 16-byte chunks per K row
+  static constexpr int ROW_BYTES = D * 2;
+  static constexpr int CH = D / 8;                  // 16-byte chunks per row
+  static constexpr int TILE_BYTES = KVB * ROW_BYTES;
+  static constexpr int STAGE_BYTES = 2 * TILE_BYTES;  // K then V
+  static constexpr int BYTES = 2 * STAGE_BYTES;
+  static constexpr int SLOTS = KVB * CH;            // 16-byte slots per tile
+  static constexpr int SLOTS_PER_THREAD = SLOTS / NT;
 };
 
+// Byte offset of (key, 16-byte chunk) inside a swizzled tile.
 template <int D>
-__device__ __forceinline__ int k_off(int key, int chunk) {
-  return key * D + ((chunk ^ (key & (AttnLds<D>::KCH - 1))) << 3);
+__device__ __forceinline__ int tile_off(int key, int chunk) {
+  return key * AttnLds<D>::ROW_BYTES + ((chunk ^ (key & (AttnLds<D>::CH - 1) & 15)) << 4);
 }
-// Vᵀ row d holds 64 keys = 16 units of 4 keys (8 bytes).
-__device__ __forceinline__ int vt_off(int d, int unit) {
-  return d * KVB + ((unit ^ ((d >> 1) & 15)) << 2);
+
+__device__ __forceinline__ s16x4 ds_read_tr(const char* lds_base, int byte_off) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(lds_base + byte_off));
 }
 
 template <int D, int MASK>
-__global__ __launch_bounds__(NT) void attn_fwd_kernel(
+__global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
     const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh, int64_t qst,
     const uint16_t* __restrict__ k, int64_t ksb, int64_t ksh, int64_t kst,
     const uint16_t* __restrict__ v, int64_t vsb, int64_t vsh, int64_t vst,
     uint16_t* __restrict__ o, int64_t osb, int64_t osh, int64_t ost, float* __restrict__ m_out,
-    float* __restrict__ l_out, int H, int Tq, int Tk, float scale_log2, int64_t causal_off,
+    float* __restrict__ l_out, int H, int Tq, int Tk, float scale, int64_t causal_off,
     const uint8_t* __restrict__ mask, int64_t mask_ld, int normalize) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  extern __shared__ __attribute__((aligned(16))) char lds[];
   using L = AttnLds<D>;
   const int nqt = gridDim.x;
   const int qt = (MASK == CATOPT_MASK_CAUSAL) ? (nqt - 1 - (int)blockIdx.x) : (int)blockIdx.x;
@@ -66,198 +85,242 @@ __global__ __launch_bounds__(NT) void attn_fwd_kernel(
   v += b * vsb + h * vsh;
   o += b * osb + h * osh;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g = lane >> 5;
   const int q0 = qt * QT;
-  const int qrow = q0 + wave * 32 + l32;
-  const bool qok = qrow < Tq;
+  const int qw0 = q0 + wave * QW;  // first query of this wave
+  const float c = scale * 1.4426950408889634f;
 
-  // Q fragments (MFMA B operand): Q[qrow][16j + 8g .. +8]
-  bf16x8 qf[D / 16];
+  // Q fragments (MFMA B operand) for the wave's two 32-query blocks.
+  bf16x8 qf[2][D / 16];
 #pragma unroll
-  for (int j = 0; j < D / 16; ++j) {
-    u32x4 t = u32x4{0, 0, 0, 0};
-    if (qok) t = *reinterpret_cast<const u32x4*>(q + (int64_t)qrow * qst + 16 * j + 8 * g);
-    qf[j] = __builtin_bit_cast(bf16x8, t);
+  for (int qb = 0; qb < 2; ++qb) {
+    const int qrow = qw0 + 32 * qb + l32;
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) {
+      u32x4 t = u32x4{0, 0, 0, 0};
+      if (qrow < Tq) t = *reinterpret_cast<const u32x4*>(q + (int64_t)qrow * qst + 16 * j + 8 * g);
+      qf[qb][j] = __builtin_bit_cast(bf16x8, t);
+    }
   }
 
-  f32x16 oacc[D / 32];
+  f32x16 oacc[D / 32][2];
 #pragma unroll
   for (int i = 0; i < D / 32; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[i][r] = 0.f;
-  float m_run = -__builtin_inff();
-  float l_run = 0.f;
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[i][qb][r] = 0.f;
+  float m_run[2] = {-__builtin_inff(), -__builtin_inff()};   // raw-score units
+  float m_true[2] = {-__builtin_inff(), -__builtin_inff()};
+  float l_run[2] = {0.f, 0.f};
 
-  int64_t kv_end = Tk;
+  int64_t kv_end = Tk, wave_end = Tk;
   if (MASK == CATOPT_MASK_CAUSAL) {
-    const int64_t lim = (int64_t)q0 + QT + causal_off;  // last query's last key + 1
+    const int64_t lim = (int64_t)q0 + QT + causal_off;
     kv_end = lim < 0 ? 0 : (lim < Tk ? lim : Tk);
+    const int64_t wl = (int64_t)qw0 + QW + causal_off;
+    wave_end = wl < 0 ? 0 : (wl < Tk ? wl : Tk);
   }
   const int nkv = (int)((kv_end + KVB - 1) / KVB);
 
-  // Tile loaders: K rows (16-byte chunks), V as 4-key x 8-d blocks.
-  constexpr int K_UNITS = KVB * L::KCH;            // 16-byte chunks per K tile
-  constexpr int K_PER_T = K_UNITS / NT;
-  constexpr int V_UNITS = (KVB / 4) * (D / 8);     // 4-key x 8-d blocks per V tile
-  constexpr int V_PER_T = (V_UNITS + NT - 1) / NT;
-  u32x4 rk[K_PER_T];
-  u32x4 rv[V_PER_T][4];
-
-  auto gload = [&](int kvt) {
+  // Fill one stage: K and V tiles of keys [kv0, kv0 + 64) by direct
+  // global->LDS loads (rows past Tk re-read row Tk-1; see the tail fix).
+  auto issue_tile = [&](int kvt, int stage) {
     const int kv0 = kvt * KVB;
+    char* kst_base = lds + stage * L::STAGE_BYTES;
 #pragma unroll
-    for (int i = 0; i < K_PER_T; ++i) {
-      const int u = tid + i * NT;
-      const int key = u / L::KCH, ch = u % L::KCH;
-      const int gk = kv0 + key;
-      rk[i] = gk < Tk ? *reinterpret_cast<const u32x4*>(k + (int64_t)gk * kst + ch * 8)
-                      : u32x4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int i = 0; i < V_PER_T; ++i) {
-      const int u = tid + i * NT;
-      const int c = u % (D / 8), kk = u / (D / 8);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int gk = kv0 + 4 * kk + e;
-        rv[i][e] = (u < V_UNITS && gk < Tk)
-                       ? *reinterpret_cast<const u32x4*>(v + (int64_t)gk * vst + c * 8)
-                       : u32x4{0, 0, 0, 0};
-      }
+    for (int i = 0; i < L::SLOTS_PER_THREAD; ++i) {
+      const int s = i * NT + wave * 64 + lane;
+      const int row = s / L::CH, cp = s % L::CH;
+      const int chunk = cp ^ (row & (L::CH - 1) & 15);
+      int gk = kv0 + row;
+      gk = gk < Tk ? gk : Tk - 1;
+      char* dst = kst_base + (i * NT + wave * 64) * 16;
+      __builtin_amdgcn_global_load_lds(k + (int64_t)gk * kst + chunk * 8, (lds_ptr)dst, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(v + (int64_t)gk * vst + chunk * 8, (lds_ptr)(dst + L::TILE_BYTES), 16,
+                                       0, 0);
     }
   };
-  auto sstore = [&](int stage) {
-    uint16_t* Ks = lds + stage * L::STAGE;
-    uint16_t* Vt = Ks + L::K_ELEMS;
-#pragma unroll
-    for (int i = 0; i < K_PER_T; ++i) {
-      const int u = tid + i * NT;
-      *reinterpret_cast<u32x4*>(Ks + k_off<D>(u / L::KCH, u % L::KCH)) = rk[i];
-    }
-#pragma unroll
-    for (int i = 0; i < V_PER_T; ++i) {
-      const int u = tid + i * NT;
-      if (u >= V_UNITS) continue;
-      const int c = u % (D / 8), kk = u / (D / 8);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        // element e of the 8-d chunk: bf16 (e&1) of dword (e>>1), for 4 keys
-        const int sh = (e & 1) * 16, w = e >> 1;
-        const uint32_t k0 = (rv[i][0][w] >> sh) & 0xffffu, k1 = (rv[i][1][w] >> sh) & 0xffffu;
-        const uint32_t k2 = (rv[i][2][w] >> sh) & 0xffffu, k3 = (rv[i][3][w] >> sh) & 0xffffu;
-        *reinterpret_cast<u32x2*>(Vt + vt_off(c * 8 + e, kk)) = u32x2{k0 | (k1 << 16), k2 | (k3 << 16)};
-      }
+  // Zero the V rows of a tail tile that lie past Tk (called after the
+  // tile's loads have landed and a barrier).
+  auto zero_tail = [&](int kvt, int stage) {
+    const int kv0 = kvt * KVB;
+    char* vbase = lds + stage * L::STAGE_BYTES + L::TILE_BYTES;
+    for (int s = tid; s < L::SLOTS; s += NT) {
+      const int row = s / L::CH;
+      if (kv0 + row >= Tk) *reinterpret_cast<u32x4*>(vbase + s * 16) = u32x4{0, 0, 0, 0};
     }
   };
 
   if (nkv > 0) {
-    gload(0);
-    sstore(0);
+    issue_tile(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (KVB > Tk) {
+      zero_tail(0, 0);
+      __syncthreads();
+    }
   }
-  __syncthreads();
 
   for (int kvt = 0; kvt < nkv; ++kvt) {
     const int cur = kvt & 1;
-    if (kvt + 1 < nkv) gload(kvt + 1);
-    const uint16_t* Ks = lds + cur * L::STAGE;
-    const uint16_t* Vt = Ks + L::K_ELEMS;
+    if (kvt + 1 < nkv) issue_tile(kvt + 1, cur ^ 1);
+    const char* Ks = lds + cur * L::STAGE_BYTES;
+    const char* Vs = Ks + L::TILE_BYTES;
     const int kv0 = kvt * KVB;
 
-    // Sᵀ tile: keys 32*kb + acc_row(r, g), query = this lane's.
-    f32x16 sacc[2];
+    if (kv0 < wave_end) {
+      // ---- Sᵀ = K Qᵀ for 64 keys x 64 queries
+      f32x16 sacc[2][2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+        for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-    for (int j = 0; j < D / 16; ++j) {
+          for (int r = 0; r < 16; ++r) sacc[kb][qb][r] = 0.f;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(Ks + k_off<D>(32 * kb + l32, 2 * j + g));
-        sacc[kb] = mfma32x32x16(a, qf[j], sacc[kb]);
+      for (int j = 0; j < D / 16; ++j) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          const bf16x8 a = *reinterpret_cast<const bf16x8*>(Ks + tile_off<D>(32 * kb + l32, 2 * j + g));
+          sacc[kb][0] = mfma32x32x16(a, qf[0][j], sacc[kb][0]);
+          sacc[kb][1] = mfma32x32x16(a, qf[1][j], sacc[kb][1]);
+        }
+      }
+
+      // ---- mask (diagonal / tail / bool tiles only)
+      bool need_mask = kv0 + KVB > Tk;
+      if (MASK == CATOPT_MASK_CAUSAL) need_mask = need_mask || (int64_t)kv0 + KVB - 1 > (int64_t)qw0 + causal_off;
+      if (MASK == CATOPT_MASK_BOOL) need_mask = true;
+      if (need_mask) {
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          const int qrow = qw0 + 32 * qb + l32;
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              // Branch-free: every lane evaluates every predicate (the mask
+              // byte is read at a clamped, always-valid address) and the
+              // score is replaced by a select.
+              const int key = kv0 + 32 * kb + acc_row(r, g);
+              bool keep = key < Tk;
+              if (MASK == CATOPT_MASK_CAUSAL) keep = keep & ((int64_t)key <= (int64_t)qrow + causal_off);
+              if (MASK == CATOPT_MASK_BOOL) {
+                const int qc = qrow < Tq ? qrow : Tq - 1;
+                const int kc = key < Tk ? key : Tk - 1;
+                const bool mk = mask[(int64_t)qc * mask_ld + kc] != 0;
+                keep = keep & (qrow < Tq) & mk;
+              }
+              sacc[kb][qb][r] = keep ? sacc[kb][qb][r] : -__builtin_inff();
+            }
+          }
+        }
+      }
+
+      // ---- online softmax (lazy rescale), per 32-query block
+      bf16x8 pf[2][2][2];  // [kb][qb][u]
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        float mt = -__builtin_inff();
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[kb][qb][r]);
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        m_true[qb] = fmaxf(m_true[qb], mt);
+        // move the reference max only when this tile exceeds it by kLazy (log2 units)
+        const bool move = (mt - m_run[qb]) * c > kLazy;
+        if (__builtin_amdgcn_ballot_w64(move) != 0) {
+          const float m_new = fmaxf(m_run[qb], mt);
+          const float alpha = (m_run[qb] == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f((m_run[qb] - m_new) * c);
+          l_run[qb] *= alpha;
+#pragma unroll
+          for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[db][qb][r] *= alpha;
+          m_run[qb] = m_new;
+        }
+        const float mc = (m_run[qb] == -__builtin_inff()) ? 0.f : m_run[qb] * c;
+        float lsum = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][qb][r], c, -mc));
+            lsum += p;
+            pf[kb][qb][r >> 3][r & 7] = static_cast<__bf16>(p);
+          }
+        }
+        l_run[qb] += lsum;
+      }
+
+      // ---- Oᵀ += Vᵀ Pᵀ
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            // lane: group G = lane/16, j = lane%16 -> key kA + j/4 (+8), d block 4*(j%4)
+            const int G = lane >> 4, jj = lane & 15;
+            const int key0 = 32 * kb + 16 * u + 4 * (G >> 1) + (jj >> 2);
+            const int d = 32 * db + 16 * (G & 1) + 4 * (jj & 3);
+            const int chunk = d >> 3, half = (d & 7) * 2;
+            const s16x4 lo = ds_read_tr(Vs, tile_off<D>(key0, chunk) + half);
+            const s16x4 hi = ds_read_tr(Vs, tile_off<D>(key0 + 8, chunk) + half);
+            const bf16x8 a = __builtin_bit_cast(
+                bf16x8, u32x4{__builtin_bit_cast(u32x2, lo)[0], __builtin_bit_cast(u32x2, lo)[1],
+                              __builtin_bit_cast(u32x2, hi)[0], __builtin_bit_cast(u32x2, hi)[1]});
+            oacc[db][0] = mfma32x32x16(a, pf[kb][0][u], oacc[db][0]);
+            oacc[db][1] = mfma32x32x16(a, pf[kb][1][u], oacc[db][1]);
+          }
+        }
       }
     }
 
-    float mloc = -__builtin_inff();
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kv0 + 32 * kb + acc_row(r, g);
-        float t = sacc[kb][r] * scale_log2;
-        bool keep = key < Tk;
-        if (MASK == CATOPT_MASK_CAUSAL) keep = keep && (int64_t)key <= (int64_t)qrow + causal_off;
-        if (MASK == CATOPT_MASK_BOOL) keep = keep && qok && mask[(int64_t)qrow * mask_ld + key] != 0;
-        t = keep ? t : -__builtin_inff();
-        sacc[kb][r] = t;
-        mloc = fmaxf(mloc, t);
+    if (kvt + 1 < nkv) {
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if ((kvt + 2) * KVB > Tk) {
+        zero_tail(kvt + 1, cur ^ 1);
+        __syncthreads();
       }
     }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float m_new = fmaxf(m_run, mloc);
-    const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    float lsum = 0.f;
-    bf16x8 pf[2][2];
+  }
+
+  // ---- epilogue: back to the true max, normalise, store
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(sacc[kb][r] - m_use);
-        lsum += p;
-        pf[kb][r >> 3][r & 7] = static_cast<__bf16>(p);
-      }
-    }
-    l_run = l_run * alpha + lsum;
-    m_run = m_new;
+  for (int qb = 0; qb < 2; ++qb) {
+    const int qrow = qw0 + 32 * qb + l32;
+    // a and l are both relative to m_run; the carrier is relative to m_true
+    float fix = 1.f;
+    if (m_true[qb] != -__builtin_inff() && m_run[qb] != -__builtin_inff())
+      fix = __builtin_amdgcn_exp2f((m_run[qb] - m_true[qb]) * c);
+    const float l_sum = l_run[qb] + __shfl_xor(l_run[qb], 32, 64);
+    const float l_tot = l_sum * fix;
+    if (qrow >= Tq) continue;
+    const float inv = normalize ? 1.0f / l_sum : fix;
+    const bool nan_row = normalize && l_sum == 0.f;  // fully masked row: 0/0 (om_apply)
+    uint16_t* orow = o + (int64_t)qrow * ost;
 #pragma unroll
     for (int db = 0; db < D / 32; ++db) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int unit = 8 * kb + 4 * u + g;
-          const int d = 32 * db + l32;
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(Vt + vt_off(d, unit));
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(Vt + vt_off(d, unit + 2));
-          const bf16x8 a = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
-          oacc[db] = mfma32x32x16(a, pf[kb][u], oacc[db]);
-        }
+      for (int rg = 0; rg < 4; ++rg) {
+        const int d = 32 * db + 8 * rg + 4 * g;
+        float x0 = oacc[db][qb][4 * rg + 0] * inv, x1 = oacc[db][qb][4 * rg + 1] * inv;
+        float x2 = oacc[db][qb][4 * rg + 2] * inv, x3 = oacc[db][qb][4 * rg + 3] * inv;
+        if (nan_row) x0 = x1 = x2 = x3 = __builtin_nanf("");
+        *reinterpret_cast<u32x2*>(orow + d) = u32x2{pack_bf16x2(x0, x1), pack_bf16x2(x2, x3)};
       }
     }
-
-    if (kvt + 1 < nkv) sstore(cur ^ 1);
-    __syncthreads();
-  }
-
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  if (!qok) return;
-  const float inv = normalize ? 1.0f / l_tot : 1.0f;  // l_tot == 0 -> inf; 0 * inf = NaN (om_apply)
-  uint16_t* orow = o + (int64_t)qrow * ost;
-#pragma unroll
-  for (int db = 0; db < D / 32; ++db) {
-#pragma unroll
-    for (int rg = 0; rg < 4; ++rg) {
-      const int d = 32 * db + 8 * rg + 4 * g;
-      float x0 = oacc[db][4 * rg + 0], x1 = oacc[db][4 * rg + 1];
-      float x2 = oacc[db][4 * rg + 2], x3 = oacc[db][4 * rg + 3];
-      if (normalize) {
-        if (l_tot == 0.f) {
-          x0 = x1 = x2 = x3 = __builtin_nanf("");
-        } else {
-          x0 *= inv; x1 *= inv; x2 *= inv; x3 *= inv;
-        }
-      }
-      *reinterpret_cast<u32x2*>(orow + d) = u32x2{pack_bf16x2(x0, x1), pack_bf16x2(x2, x3)};
+    if (g == 0) {
+      const int64_t mi = (b * H + h) * (int64_t)Tq + qrow;
+      if (m_out) m_out[mi] = m_true[qb] * scale;  // natural-log units of the scaled score
+      if (l_out) l_out[mi] = l_tot;
     }
-  }
-  if (g == 0) {
-    const int64_t mi = (b * H + h) * (int64_t)Tq + qrow;
-    if (m_out) m_out[mi] = m_run * 0.69314718055994531f;  // back to natural-log units
-    if (l_out) l_out[mi] = l_tot;
   }
 }
 
@@ -275,11 +338,9 @@ int32_t attn_launch(const uint16_t* q, const int64_t* qs, const uint16_t* k, con
     attr_done = true;
   }
   const int64_t nqt = (Tq + QT - 1) / QT;
-  const float scale_log2 = scale * 1.4426950408889634f;
   attn_fwd_kernel<D, MASK><<<dim3((uint32_t)nqt, (uint32_t)H, (uint32_t)B), dim3(NT), AttnLds<D>::BYTES, s>>>(
       q, qs[0], qs[1], qs[2], k, ks[0], ks[1], ks[2], v, vs[0], vs[1], vs[2], o, os[0], os[1],
-      os[2], m_out, l_out, (int)H, (int)Tq, (int)Tk, scale_log2, causal_off, mask, mask_ld,
-      normalize);
+      os[2], m_out, l_out, (int)H, (int)Tq, (int)Tk, scale, causal_off, mask, mask_ld, normalize);
   CATOPT_LAUNCH_CHECK();
   return CATOPT_OK;
 }
@@ -323,6 +384,7 @@ extern "C" int32_t catopt_hip_attn_fwd(int32_t dtype, int64_t B, int64_t H, int6
   if (mask_mode < CATOPT_MASK_NONE || mask_mode > CATOPT_MASK_BOOL) return CATOPT_E_INVAL;
   if (dtype != CATOPT_BF16) return CATOPT_E_UNSUPPORTED;
   if (d != dv || (d != 128 && d != 64)) return CATOPT_E_UNSUPPORTED;
+  if (!(scale > 0.f) || !__builtin_isfinite(scale)) return CATOPT_E_UNSUPPORTED;
   if (B == 0 || H == 0 || Tq == 0) return CATOPT_OK;
   if (!q || !k || !v || !o) return CATOPT_E_INVAL;
   if (!strides_ok(q_strides) || !strides_ok(k_strides) || !strides_ok(v_strides) ||
