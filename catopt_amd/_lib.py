@@ -92,6 +92,13 @@ def load(path: Path | str | None = None) -> C.CDLL:
         if _lib is not None and path is None:
             return _lib
         p = Path(path) if path is not None else LIB_PATH
+        # torch ships its own HIP runtime under the same soname as ROCm's; it
+        # must be loaded first so that this library binds to that instance
+        # (one runtime per process: torch's streams and allocations are then
+        # valid here).  Loading this library first pulls in /opt/rocm's copy
+        # and the two runtimes disagree (hipErrorNoDevice on launch).
+        import torch  # noqa: F401
+
         if not p.exists():
             raise HipExtensionMissing(
                 f"{p} not found: build it with `python -m catopt_amd.build` "

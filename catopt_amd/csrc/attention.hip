@@ -37,8 +37,12 @@ namespace catopt {
 namespace {
 
 constexpr int NT = 256;   // 4 waves
-constexpr int QW = 64;    // queries per wave
-constexpr int QT = 256;   // queries per workgroup
+#ifndef CATOPT_ATTN_QB
+#define CATOPT_ATTN_QB 1
+#endif
+constexpr int QB = CATOPT_ATTN_QB;  // 32-query blocks per wave
+constexpr int QW = 32 * QB;         // queries per wave
+constexpr int QT = 4 * QW;          // queries per workgroup
 constexpr int KVB = 64;   // keys per KV tile
 constexpr float kLazy = 8.0f;
 
@@ -68,7 +72,7 @@ __device__ __forceinline__ s16x4 ds_read_tr(const char* lds_base, int byte_off) 
 }
 
 template <int D, int MASK>
-__global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
+__global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
     const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh, int64_t qst,
     const uint16_t* __restrict__ k, int64_t ksb, int64_t ksh, int64_t kst,
     const uint16_t* __restrict__ v, int64_t vsb, int64_t vsh, int64_t vst,
@@ -93,9 +97,9 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
   const float c = scale * 1.4426950408889634f;
 
   // Q fragments (MFMA B operand) for the wave's two 32-query blocks.
-  bf16x8 qf[2][D / 16];
+  bf16x8 qf[QB][D / 16];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
     const int qrow = qw0 + 32 * qb + l32;
 #pragma unroll
     for (int j = 0; j < D / 16; ++j) {
@@ -105,16 +109,19 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
     }
   }
 
-  f32x16 oacc[D / 32][2];
+  f32x16 oacc[D / 32][QB];
 #pragma unroll
   for (int i = 0; i < D / 32; ++i)
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
+    for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) oacc[i][qb][r] = 0.f;
-  float m_run[2] = {-__builtin_inff(), -__builtin_inff()};   // raw-score units
-  float m_true[2] = {-__builtin_inff(), -__builtin_inff()};
-  float l_run[2] = {0.f, 0.f};
+  float m_run[QB], m_true[QB], l_run[QB];  // maxima in raw-score units
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    m_run[qb] = m_true[qb] = -__builtin_inff();
+    l_run[qb] = 0.f;
+  }
 
   int64_t kv_end = Tk, wave_end = Tk;
   if (MASK == CATOPT_MASK_CAUSAL) {
@@ -173,11 +180,11 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
 
     if (kv0 < wave_end) {
       // ---- Sᵀ = K Qᵀ for 64 keys x 64 queries
-      f32x16 sacc[2][2];
+      f32x16 sacc[2][QB];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
+        for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) sacc[kb][qb][r] = 0.f;
 #pragma unroll
@@ -185,8 +192,8 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
           const bf16x8 a = *reinterpret_cast<const bf16x8*>(Ks + tile_off<D>(32 * kb + l32, 2 * j + g));
-          sacc[kb][0] = mfma32x32x16(a, qf[0][j], sacc[kb][0]);
-          sacc[kb][1] = mfma32x32x16(a, qf[1][j], sacc[kb][1]);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) sacc[kb][qb] = mfma32x32x16(a, qf[qb][j], sacc[kb][qb]);
         }
       }
 
@@ -196,7 +203,7 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
       if (MASK == CATOPT_MASK_BOOL) need_mask = true;
       if (need_mask) {
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
+        for (int qb = 0; qb < QB; ++qb) {
           const int qrow = qw0 + 32 * qb + l32;
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb) {
@@ -221,9 +228,9 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
       }
 
       // ---- online softmax (lazy rescale), per 32-query block
-      bf16x8 pf[2][2][2];  // [kb][qb][u]
+      bf16x8 pf[2][QB][2];  // [kb][qb][u]
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
+      for (int qb = 0; qb < QB; ++qb) {
         float mt = -__builtin_inff();
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
@@ -274,8 +281,8 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
             const bf16x8 a = __builtin_bit_cast(
                 bf16x8, u32x4{__builtin_bit_cast(u32x2, lo)[0], __builtin_bit_cast(u32x2, lo)[1],
                               __builtin_bit_cast(u32x2, hi)[0], __builtin_bit_cast(u32x2, hi)[1]});
-            oacc[db][0] = mfma32x32x16(a, pf[kb][0][u], oacc[db][0]);
-            oacc[db][1] = mfma32x32x16(a, pf[kb][1][u], oacc[db][1]);
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) oacc[db][qb] = mfma32x32x16(a, pf[kb][qb][u], oacc[db][qb]);
           }
         }
       }
@@ -293,7 +300,7 @@ __global__ __launch_bounds__(NT, 1) void attn_fwd_kernel(
 
   // ---- epilogue: back to the true max, normalise, store
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
     const int qrow = qw0 + 32 * qb + l32;
     // a and l are both relative to m_run; the carrier is relative to m_true
     float fix = 1.f;
