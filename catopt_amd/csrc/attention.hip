@@ -81,9 +81,18 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
     const uint8_t* __restrict__ mask, int64_t mask_ld, int normalize) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   using L = AttnLds<D>;
-  const int nqt = gridDim.x;
-  const int qt = (MASK == CATOPT_MASK_CAUSAL) ? (nqt - 1 - (int)blockIdx.x) : (int)blockIdx.x;
-  const int64_t b = blockIdx.z, h = blockIdx.y;
+  // 1-D grid of nqt x H x B tiles.  Workgroups are dealt round robin over
+  // the 8 XCDs, so linear id L runs on XCD L % 8; work item w is chosen so
+  // that each XCD owns a contiguous range of (b, h) with all of their query
+  // tiles, and K / V of one head stay in one XCD's L2.  Within a head the
+  // causal order is longest tile first.
+  const int nqt = (Tq + QT - 1) / QT;
+  const int nblk = gridDim.x;
+  int w = blockIdx.x;
+  if ((nblk & 7) == 0) w = (w & 7) * (nblk >> 3) + (w >> 3);
+  const int bh = w / nqt, qi = w - bh * nqt;
+  const int qt = (MASK == CATOPT_MASK_CAUSAL) ? (nqt - 1 - qi) : qi;
+  const int64_t b = bh / H, h = bh - (int64_t)(bh / H) * H;
   q += b * qsb + h * qsh;
   k += b * ksb + h * ksh;
   v += b * vsb + h * vsh;
@@ -133,21 +142,48 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
   const int nkv = (int)((kv_end + KVB - 1) / KVB);
 
   // Fill one stage: K and V tiles of keys [kv0, kv0 + 64) by direct
-  // global->LDS loads (rows past Tk re-read row Tk-1; see the tail fix).
+  // global->LDS loads.  Each thread owns SLOTS_PER_THREAD fixed 16-byte
+  // slots; their element offsets inside a tile are computed once (the host
+  // guarantees 64 rows of either stride fit in 31 bits), so a full tile
+  // costs a scalar base update per load.  A tail tile clamps rows past Tk
+  // to row Tk-1 (its V rows are zeroed afterwards).
+  // (literal array bounds: with a bound that depends on D the host pass
+  // takes the arrays for variable-length ones and silently drops the
+  // kernel's launch stub; 4 = SLOTS_PER_THREAD at D = 128, the largest)
+  static_assert(AttnLds<D>::SLOTS_PER_THREAD <= 4, "slot arrays hold 4 entries");
+  int t_row[4], t_koff[4], t_voff[4], t_chunk8[4];
+#pragma unroll
+  for (int i = 0; i < L::SLOTS_PER_THREAD; ++i) {
+    const int s = i * NT + wave * 64 + lane;
+    const int row = s / L::CH, cp = s % L::CH;
+    const int chunk = cp ^ (row & (L::CH - 1) & 15);
+    t_row[i] = row;
+    t_chunk8[i] = chunk * 8;
+    t_koff[i] = row * (int)kst + chunk * 8;
+    t_voff[i] = row * (int)vst + chunk * 8;
+  }
   auto issue_tile = [&](int kvt, int stage) {
     const int kv0 = kvt * KVB;
     char* kst_base = lds + stage * L::STAGE_BYTES;
+    const uint16_t* kt = k + (int64_t)kv0 * kst;
+    const uint16_t* vt = v + (int64_t)kv0 * vst;
+    if (kv0 + KVB <= Tk) {
 #pragma unroll
-    for (int i = 0; i < L::SLOTS_PER_THREAD; ++i) {
-      const int s = i * NT + wave * 64 + lane;
-      const int row = s / L::CH, cp = s % L::CH;
-      const int chunk = cp ^ (row & (L::CH - 1) & 15);
-      int gk = kv0 + row;
-      gk = gk < Tk ? gk : Tk - 1;
-      char* dst = kst_base + (i * NT + wave * 64) * 16;
-      __builtin_amdgcn_global_load_lds(k + (int64_t)gk * kst + chunk * 8, (lds_ptr)dst, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(v + (int64_t)gk * vst + chunk * 8, (lds_ptr)(dst + L::TILE_BYTES), 16,
-                                       0, 0);
+      for (int i = 0; i < L::SLOTS_PER_THREAD; ++i) {
+        char* dst = kst_base + (i * NT + wave * 64) * 16;
+        __builtin_amdgcn_global_load_lds(kt + t_koff[i], (lds_ptr)dst, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vt + t_voff[i], (lds_ptr)(dst + L::TILE_BYTES), 16, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < L::SLOTS_PER_THREAD; ++i) {
+        int gk = kv0 + t_row[i];
+        gk = gk < Tk ? gk : Tk - 1;
+        char* dst = kst_base + (i * NT + wave * 64) * 16;
+        __builtin_amdgcn_global_load_lds(k + (int64_t)gk * kst + t_chunk8[i], (lds_ptr)dst, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(v + (int64_t)gk * vst + t_chunk8[i], (lds_ptr)(dst + L::TILE_BYTES),
+                                         16, 0, 0);
+      }
     }
   };
   // Zero the V rows of a tail tile that lie past Tk (called after the
@@ -345,7 +381,9 @@ int32_t attn_launch(const uint16_t* q, const int64_t* qs, const uint16_t* k, con
     attr_done = true;
   }
   const int64_t nqt = (Tq + QT - 1) / QT;
-  attn_fwd_kernel<D, MASK><<<dim3((uint32_t)nqt, (uint32_t)H, (uint32_t)B), dim3(NT), AttnLds<D>::BYTES, s>>>(
+  const int64_t nblk = nqt * H * B;
+  if (nblk > 0x7fffffffLL) return CATOPT_E_UNSUPPORTED;
+  attn_fwd_kernel<D, MASK><<<dim3((uint32_t)nblk), dim3(NT), AttnLds<D>::BYTES, s>>>(
       q, qs[0], qs[1], qs[2], k, ks[0], ks[1], ks[2], v, vs[0], vs[1], vs[2], o, os[0], os[1],
       os[2], m_out, l_out, (int)H, (int)Tq, (int)Tk, scale, causal_off, mask, mask_ld, normalize);
   CATOPT_LAUNCH_CHECK();
@@ -400,6 +438,9 @@ extern "C" int32_t catopt_hip_attn_fwd(int32_t dtype, int64_t B, int64_t H, int6
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return CATOPT_E_INVAL;
   if (mask_mode == CATOPT_MASK_BOOL && (!mask || mask_ld < Tk)) return CATOPT_E_INVAL;
   if (Tq > 0x7fffffffLL || Tk > 0x7fffffffLL || H > 65535 || B > 65535) return CATOPT_E_UNSUPPORTED;
+  // per-thread tile offsets are 32-bit: 64 rows of either stride must fit
+  if ((k_strides[2] + 1) * 64 + d >= 0x7fffffffLL || (v_strides[2] + 1) * 64 + d >= 0x7fffffffLL)
+    return CATOPT_E_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto qp = static_cast<const uint16_t*>(q);
   auto kp = static_cast<const uint16_t*>(k);
