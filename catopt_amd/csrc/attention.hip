@@ -17,9 +17,12 @@
 // key permutation (two runs of four consecutive keys per lane, which is one
 // transposing read each).
 //
-// Work split: one workgroup = 4 waves = 256 queries of one (b, h); each wave
-// owns 64 queries (two 32-query blocks) so every K / V fragment read from
-// LDS feeds two MFMAs.  KV tiles of 64 keys are double buffered in LDS and
+// Work split: one workgroup = 4 waves = 128 queries of one (b, h), 32 per
+// wave (QB = 1).  That keeps a wave within 256 registers, so two waves share
+// each SIMD and one's softmax overlaps the other's MFMAs; QB = 2 (each K / V
+// fragment feeding two MFMAs) needs AGPRs and measured 1.33x slower, from
+// accumulator copies between the register files.  Waves raise their
+// priority around the MFMA blocks.  KV tiles of 64 keys are double buffered in LDS and
 // filled by direct global->LDS loads (global_load_lds_dwordx4: no register
 // staging); K and V rows are 256 bytes with the 16-byte chunk index
 // XOR-swizzled by (key & 15).  A partial last tile zero-fills its missing V
@@ -37,10 +40,7 @@ namespace catopt {
 namespace {
 
 constexpr int NT = 256;   // 4 waves
-#ifndef CATOPT_ATTN_QB
-#define CATOPT_ATTN_QB 1
-#endif
-constexpr int QB = CATOPT_ATTN_QB;  // 32-query blocks per wave
+constexpr int QB = 1;               // 32-query blocks per wave
 constexpr int QW = 32 * QB;         // queries per wave
 constexpr int QT = 4 * QW;          // queries per workgroup
 constexpr int KVB = 64;   // keys per KV tile
@@ -216,6 +216,7 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
 
     if (kv0 < wave_end) {
       // ---- Sᵀ = K Qᵀ for 64 keys x 64 queries
+      __builtin_amdgcn_s_setprio(1);
       f32x16 sacc[2][QB];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -233,6 +234,7 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
         }
       }
 
+      __builtin_amdgcn_s_setprio(0);
       // ---- mask (diagonal / tail / bool tiles only)
       bool need_mask = kv0 + KVB > Tk;
       if (MASK == CATOPT_MASK_CAUSAL) need_mask = need_mask || (int64_t)kv0 + KVB - 1 > (int64_t)qw0 + causal_off;
@@ -301,6 +303,7 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
       }
 
       // ---- Oᵀ += Vᵀ Pᵀ
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int db = 0; db < D / 32; ++db) {
 #pragma unroll
@@ -324,6 +327,7 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
       }
     }
 
+    __builtin_amdgcn_s_setprio(0);
     if (kvt + 1 < nkv) {
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
