@@ -8,12 +8,18 @@
 // (each lane supplies 8 consecutive k of one row/column).
 //
 // Tiling: 256x256 block tile, BK = 64, 4 waves in a 2x2 grid, each wave a
-// 128x128 sub-tile = 4x4 MFMA blocks (256 fp32 accumulators per lane).  The
-// K loop is double buffered: global loads for tile k+1 are issued into
-// registers before the MFMAs of tile k, then stored to the other LDS stage,
+// 128x128 sub-tile = 4x4 MFMA blocks (256 fp32 accumulators per lane, held
+// in AGPRs; the loop never touches them with VALU).  Tiles reach LDS by
+// direct global->LDS loads (global_load_lds_dwordx4): no register staging,
+// no LDS store instructions.  Two LDS stages (2 x 64 KB): the loads of K
+// tile t+1 are issued before the MFMAs of tile t and waited for after them,
 // one barrier per K tile.  LDS rows are 128 B (64 bf16) with the 16-byte
-// chunk index XOR-swizzled by (row & 7) so that both the row-wise stores and
-// the MFMA fragment reads are bank-conflict free.
+// chunk index XOR-swizzled by (row & 7), so the MFMA fragment reads (eight
+// consecutive rows, one chunk) hit eight different bank groups.
+//
+// Edges: rows past M (A) or N (B) load a clamped, valid row and are never
+// stored; a K tail (K % 64 != 0, K % 8 == 0) loads clamped chunks and then
+// zeroes the chunks past K in LDS before they are read.
 //
 // Paired epilogues (SILU_MUL / GLU): the B tile holds 128 rows of the first
 // projection and the 128 matching rows of the second (row n and row n + N of
@@ -22,20 +28,31 @@
 // SWIGLU_FUSE form never touch HBM.
 //
 // Block-to-tile mapping is XCD-aware: the hardware deals workgroups round
-// robin over 8 XCDs, so consecutive logical tiles (grouped 8 M-tiles at a
-// time) are gathered onto the same XCD to share its L2.
+// robin over 8 XCDs, so each XCD is given a contiguous range of logical tiles
+// (grouped 8 M-tiles at a time), which march through K together and share
+// that XCD's L2.
 #include "common.hpp"
 
 namespace catopt {
 namespace {
 
 constexpr int BM = 256, BN = 256, BK = 64;
-constexpr int NT = 256;
-constexpr int STAGE_ELEMS = (BM + BN) * BK;              // bf16 elements per stage
-constexpr int LDS_BYTES = 2 * STAGE_ELEMS * 2;           // two stages
+#ifndef CATOPT_GEMM_NWN
+#define CATOPT_GEMM_NWN 4
+#endif
+constexpr int NWN = CATOPT_GEMM_NWN;    // waves along N (2 along M)
+constexpr int NT = 128 * NWN;           // threads per block
+constexpr int WCOLS = BN / NWN;         // output columns per wave (B rows)
+constexpr int TJ = WCOLS / 32;          // 32-wide MFMA blocks per wave along N
+constexpr int TILE_BYTES = BM * BK * 2;                 // one operand tile (A or B), 32 KB
+constexpr int STAGE_BYTES = 2 * TILE_BYTES;             // A then B
+constexpr int LDS_BYTES = 2 * STAGE_BYTES;              // two stages, 128 KB
+constexpr int SLOTS_PER_THREAD = (BM * BK / 8) / NT;    // 16-byte slots per thread per operand: 8
 
-__device__ __forceinline__ int swz(int row, int chunk) {  // element offset of chunk in LDS
-  return row * BK + ((chunk ^ (row & 7)) << 3);
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+__device__ __forceinline__ int swz(int row, int chunk) {  // byte offset of (row, chunk) in a tile
+  return row * (BK * 2) + ((chunk ^ (row & 7)) << 4);
 }
 
 struct TileMap {
@@ -62,12 +79,12 @@ __device__ __forceinline__ TileMap map_tile(int tiles_m, int tiles_n) {
 }
 
 template <int EPI>
-__global__ __launch_bounds__(NT) void gemm_bf16_nt(
+__global__ __launch_bounds__(NT, 1) void gemm_bf16_nt(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb,
     const uint16_t* __restrict__ bias, const uint16_t* __restrict__ bias2,
     uint16_t* __restrict__ C, int64_t ldc, int M, int N, int K, int tiles_m, int tiles_n,
     int64_t sA, int64_t sB, int64_t sC) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  extern __shared__ __attribute__((aligned(16))) char lds[];
   A += (int64_t)blockIdx.y * sA;
   B += (int64_t)blockIdx.y * sB;
   C += (int64_t)blockIdx.y * sC;
@@ -79,104 +96,117 @@ __global__ __launch_bounds__(NT) void gemm_bf16_nt(
   const int n0 = tile.tn * (PAIRED ? BN / 2 : BN);
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / NWN, wn = wave % NWN;
   const int l32 = lane & 31, g = lane >> 5;
 
-  // Global load assignment: 8 threads per 128-byte row slice, 32 rows per pass.
-  const int ld_row = tid >> 3, ld_chunk = tid & 7;
-  const uint16_t* a_src[8];
-  bool a_ok[8];
-  const uint16_t* b_src[8];
-  bool b_ok[8];
+  // This thread's load slots: slot s = i*NT + wave*64 + lane of a tile is
+  // (row s/8, swizzled chunk s%8); the global row is clamped to a valid one.
+  int64_t a_off[SLOTS_PER_THREAD], b_off[SLOTS_PER_THREAD];
+  int s_chunk[SLOTS_PER_THREAD];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = ld_row + 32 * i;
-    const int am = m0 + r;
-    a_ok[i] = am < M;
-    a_src[i] = A + (int64_t)(a_ok[i] ? am : 0) * lda + ld_chunk * 8;
+  for (int i = 0; i < SLOTS_PER_THREAD; ++i) {
+    const int s = i * NT + wave * 64 + lane;
+    const int r = s >> 3, cp = s & 7;
+    const int chunk = cp ^ (r & 7);
+    s_chunk[i] = chunk;
+    const int am = min(m0 + r, M - 1);
     int bn;
-    bool ok;
     if (PAIRED) {
       const int half = r >> 7, rr = r & 127;
-      ok = n0 + rr < N;
-      bn = (ok ? n0 + rr : 0) + half * N;
+      bn = min(n0 + rr, N - 1) + half * N;
     } else {
-      bn = n0 + r;
-      ok = bn < N;
-      if (!ok) bn = 0;
+      bn = min(n0 + r, N - 1);
     }
-    b_ok[i] = ok;
-    b_src[i] = B + (int64_t)bn * ldb + ld_chunk * 8;
+    a_off[i] = (int64_t)am * lda + chunk * 8;
+    b_off[i] = (int64_t)bn * ldb + chunk * 8;
   }
 
-  u32x4 ra[8], rb[8];
-  auto gload = [&](int k0) {
-    const bool kin = k0 + ld_chunk * 8 < K;
+  const int ktiles = (K + BK - 1) / BK;
+  const bool k_tail = (K % BK) != 0;
+
+  auto issue = [&](int kt, int stage) {
+    const int k0 = kt * BK;
+    char* sa = lds + stage * STAGE_BYTES;
+    const bool full = !k_tail || kt + 1 < ktiles;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      ra[i] = (a_ok[i] && kin) ? *reinterpret_cast<const u32x4*>(a_src[i] + k0) : u32x4{0, 0, 0, 0};
-      rb[i] = (b_ok[i] && kin) ? *reinterpret_cast<const u32x4*>(b_src[i] + k0) : u32x4{0, 0, 0, 0};
+    for (int i = 0; i < SLOTS_PER_THREAD; ++i) {
+      // a chunk past K reads chunk 0 of the tile instead (zeroed below)
+      const int kk = (full || k0 + s_chunk[i] * 8 < K) ? k0 : k0 - s_chunk[i] * 8;
+      char* dst = sa + (i * NT + wave * 64) * 16;
+      __builtin_amdgcn_global_load_lds(A + a_off[i] + kk, (lds_ptr)dst, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(B + b_off[i] + kk, (lds_ptr)(dst + TILE_BYTES), 16, 0, 0);
     }
   };
-  auto sstore = [&](int stage) {
-    uint16_t* As = lds + stage * STAGE_ELEMS;
-    uint16_t* Bs = As + BM * BK;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = ld_row + 32 * i;
-      *reinterpret_cast<u32x4*>(As + swz(r, ld_chunk)) = ra[i];
-      *reinterpret_cast<u32x4*>(Bs + swz(r, ld_chunk)) = rb[i];
+  // zero the chunks past K of the tail tile (after its loads landed)
+  auto zero_k_tail = [&](int kt, int stage) {
+    const int k0 = kt * BK;
+    char* sa = lds + stage * STAGE_BYTES;
+    for (int s = tid; s < 2 * BM * 8; s += NT) {
+      const int t = s >> 11, rem = s & 2047;  // operand, slot
+      const int r = rem >> 3, cp = rem & 7;
+      const int chunk = cp ^ (r & 7);
+      if (k0 + chunk * 8 >= K) *reinterpret_cast<u32x4*>(sa + t * TILE_BYTES + rem * 16) = u32x4{0, 0, 0, 0};
     }
   };
 
-  f32x16 acc[4][4];
+  f32x16 acc[4][TJ];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < TJ; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  // B-tile row of the wave's column block j.
+  // B-tile row of the wave's column block j (paired: the first TJ/2 blocks
+  // are gate rows, the rest the matching up rows 128 further down).
   auto brow = [&](int j) {
-    return PAIRED ? (j >> 1) * 128 + wn * 64 + (j & 1) * 32 : wn * 128 + j * 32;
+    return PAIRED ? (j / (TJ / 2)) * 128 + wn * (WCOLS / 2) + (j % (TJ / 2)) * 32 : wn * WCOLS + j * 32;
   };
 
-  const int ktiles = (K + BK - 1) / BK;
-  gload(0);
-  sstore(0);
+  issue(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  if (k_tail && ktiles == 1) {
+    zero_k_tail(0, 0);
+    __syncthreads();
+  }
 
   for (int kt = 0; kt < ktiles; ++kt) {
     const int cur = kt & 1;
-    if (kt + 1 < ktiles) gload((kt + 1) * BK);
-    const uint16_t* As = lds + cur * STAGE_ELEMS;
-    const uint16_t* Bs = As + BM * BK;
+    if (kt + 1 < ktiles) issue(kt + 1, cur ^ 1);
+    const char* As = lds + cur * STAGE_BYTES;
+    const char* Bs = As + TILE_BYTES;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
-      bf16x8 af[4], bfr[4];
+      bf16x8 af[4], bfr[TJ];
       const int chunk = 2 * ks + g;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         af[i] = *reinterpret_cast<const bf16x8*>(As + swz(wm * 128 + i * 32 + l32, chunk));
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < TJ; ++j)
         bfr[j] = *reinterpret_cast<const bf16x8*>(Bs + swz(brow(j) + l32, chunk));
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma32x32x16(af[i], bfr[j], acc[i][j]);
+        for (int j = 0; j < TJ; ++j) acc[i][j] = mfma32x32x16(af[i], bfr[j], acc[i][j]);
     }
-    if (kt + 1 < ktiles) sstore(cur ^ 1);
-    __syncthreads();
+    if (kt + 1 < ktiles) {
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (k_tail && kt + 2 == ktiles) {
+        zero_k_tail(kt + 1, cur ^ 1);
+        __syncthreads();
+      }
+    }
   }
 
   // Epilogue: lane owns output column (l32) of each 32-wide block and 16 rows.
   if (PAIRED) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = n0 + wn * 64 + j * 32 + l32;
+    for (int j = 0; j < TJ / 2; ++j) {
+      const int n = n0 + wn * (WCOLS / 2) + j * 32 + l32;
       if (n >= N) continue;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -184,7 +214,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_nt(
         for (int r = 0; r < 16; ++r) {
           const int m = m0 + wm * 128 + i * 32 + acc_row(r, g);
           if (m >= M) continue;
-          const float a = acc[i][j][r], b = acc[i][j + 2][r];
+          const float a = acc[i][j][r], b = acc[i][j + TJ / 2][r];
           const float o = (EPI == CATOPT_EPI_SILU_MUL) ? silu_f(a) * b : a * sigmoid_f(b);
           C[(int64_t)m * ldc + n] = f32_to_bf16(o);
         }
@@ -192,8 +222,8 @@ __global__ __launch_bounds__(NT) void gemm_bf16_nt(
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = n0 + wn * 128 + j * 32 + l32;
+    for (int j = 0; j < TJ; ++j) {
+      const int n = n0 + wn * WCOLS + j * 32 + l32;
       if (n >= N) continue;
       float badd = 0.f;
       if (EPI == CATOPT_EPI_BIAS || EPI == CATOPT_EPI_BIAS_ADD2) badd = bf16_to_f32(bias[n]);
