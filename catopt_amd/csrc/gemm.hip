@@ -111,6 +111,91 @@ __global__ __launch_bounds__(NTH) void gemm_generic(
   }
 }
 
+// ---------------------------------------------------------------- skinny fp32
+// fp32 C[M, N] = epi(A[M, K] · W[N, K]ᵀ) for few rows (the folded weight
+// chain: one 64 x 512 x 512 GEMM that the 64x64 tiles above spread over only
+// 8 workgroups).  One workgroup per 16x16 output tile; its 4 waves split K
+// into quarters and reduce the four 16x16 partials through LDS in a fixed
+// order (deterministic).  16x16x4 fp32 MFMA: lane l supplies A row l%16 and
+// W row l%16 at k-group l/16; accumulator register r of lane l is output
+// (4*(l/16) + r, l%16).  The k index of the MFMA is only a summation order,
+// so each lane loads 4 consecutive k with one 16-byte load and feeds them to
+// 4 consecutive MFMA steps (the same permutation on both operands).
+constexpr int SK_CHUNK = 64;  // k per wave per pass: 16 per lane group
+
+__device__ __forceinline__ f32x4 mfma16x16x4f32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_f32_skinny(
+    const float* __restrict__ A, int64_t lda, const float* __restrict__ W, int64_t ldw,
+    const float* __restrict__ bias, const float* __restrict__ bias2, float* __restrict__ C,
+    int64_t ldc, int M, int N, int K) {
+  __shared__ float part[4][16][17];
+  const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 16;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, kq = lane >> 4;
+  const int am = min(m0 + r16, M - 1), wn = min(n0 + r16, N - 1);  // clamped rows are never stored
+  const float* arow = A + (int64_t)am * lda;
+  const float* wrow = W + (int64_t)wn * ldw;
+  const int kper = ((K + 4 * SK_CHUNK - 1) / (4 * SK_CHUNK)) * SK_CHUNK;  // k per wave, multiple of 64
+  const int kbeg = wave * kper, kend = min(K, kbeg + kper);
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int kb = kbeg; kb < kend; kb += SK_CHUNK) {
+    f32x4 av[4], bv[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int k = kb + 16 * s + 4 * kq;  // K % 4 == 0: a group is wholly in or out
+      const bool ok = k < kend;
+      av[s] = ok ? *reinterpret_cast<const f32x4*>(arow + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+      bv[s] = ok ? *reinterpret_cast<const f32x4*>(wrow + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = mfma16x16x4f32(av[s][e], bv[s][e], acc);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) part[wave][4 * kq + r][r16] = acc[r];
+  __syncthreads();
+  const int i = tid >> 4, j = tid & 15;  // 256 threads: one output each
+  const int m = m0 + i, n = n0 + j;
+  if (m >= M || n >= N) return;
+  float o = ((part[0][i][j] + part[1][i][j]) + part[2][i][j]) + part[3][i][j];
+  if (EPI == CATOPT_EPI_BIAS || EPI == CATOPT_EPI_BIAS_ADD2) o += bias[n];
+  if (EPI == CATOPT_EPI_BIAS_ADD2) o += bias2[n];
+  C[(int64_t)m * ldc + n] = o;
+}
+
+bool skinny_ok(int64_t M, int64_t N, int64_t K, const void* x, int64_t ldx, const void* w,
+               int64_t ldw) {
+  const int64_t tiles64 = ((M + TM - 1) / TM) * ((N + TN - 1) / TN);
+  return tiles64 < 256 && M <= 1024 && K % 4 == 0 && ldx % 4 == 0 && ldw % 4 == 0 &&
+         aligned16(x) && aligned16(w) && (N + 15) / 16 <= 0x7fffffffLL && (M + 15) / 16 <= 65535;
+}
+
+int32_t launch_skinny(int32_t epi, const float* A, int64_t lda, const float* W, int64_t ldw,
+                      const float* bias, const float* bias2, float* C, int64_t ldc, int64_t M,
+                      int64_t N, int64_t K, hipStream_t s) {
+  const dim3 grid((uint32_t)((N + 15) / 16), (uint32_t)((M + 15) / 16));
+  switch (epi) {
+    case CATOPT_EPI_NONE:
+      gemm_f32_skinny<CATOPT_EPI_NONE><<<grid, 256, 0, s>>>(A, lda, W, ldw, bias, bias2, C, ldc, (int)M, (int)N, (int)K);
+      break;
+    case CATOPT_EPI_BIAS:
+      gemm_f32_skinny<CATOPT_EPI_BIAS><<<grid, 256, 0, s>>>(A, lda, W, ldw, bias, bias2, C, ldc, (int)M, (int)N, (int)K);
+      break;
+    case CATOPT_EPI_BIAS_ADD2:
+      gemm_f32_skinny<CATOPT_EPI_BIAS_ADD2><<<grid, 256, 0, s>>>(A, lda, W, ldw, bias, bias2, C, ldc, (int)M, (int)N, (int)K);
+      break;
+    default:
+      return CATOPT_E_INVAL;
+  }
+  CATOPT_LAUNCH_CHECK();
+  return CATOPT_OK;
+}
+
 template <typename T, bool TA, bool TB, int EPI>
 int32_t launch_generic(const void* A, int64_t lda, int64_t sA, const void* B, int64_t ldb,
                        int64_t sB, const void* bias, const void* bias2, void* C, int64_t ldc,
@@ -172,6 +257,10 @@ extern "C" int32_t catopt_hip_linear(int32_t dtype, int64_t M, int64_t N, int64_
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == CATOPT_BF16 && gemm_bf16_nt_fast_ok(M, N, K, x, ldx, w, ldw, y, ldy))
     return gemm_bf16_nt_launch(epilogue, M, N, K, x, ldx, w, ldw, bias, bias2, y, ldy, 1, 0, 0, 0, s);
+  if (dtype == CATOPT_F32 && !paired && skinny_ok(M, N, K, x, ldx, w, ldw))
+    return launch_skinny(epilogue, static_cast<const float*>(x), ldx, static_cast<const float*>(w), ldw,
+                         static_cast<const float*>(bias), static_cast<const float*>(bias2),
+                         static_cast<float*>(y), ldy, M, N, K, s);
   if (paired) {
     return dtype == CATOPT_BF16 ? dispatch_paired<uint16_t>(epilogue, x, ldx, w, ldw, y, ldy, M, N, K, s)
                                 : dispatch_paired<float>(epilogue, x, ldx, w, ldw, y, ldy, M, N, K, s);

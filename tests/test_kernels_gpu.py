@@ -98,13 +98,22 @@ def test_linear_paired_unaligned_falls_to_generic(dev):
     _gate(oracle.silu(g) * u, y, TOL_BF16)
 
 
-@pytest.mark.parametrize("M,N,Kd", [(64, 512, 512), (7, 33, 129)])
+@pytest.mark.parametrize("M,N,Kd", [(64, 512, 512), (7, 33, 129), (30, 100, 260), (1, 17, 4),
+                                    (129, 40, 1000), (600, 700, 2048)])
 def test_linear_fp32(dev, M, N, Kd):
+    # (64,512,512), (30,100,260), (1,17,4), (129,40,1000): the skinny split-K
+    # kernel (ragged tiles, K not a multiple of 64); (7,33,129): K % 4 != 0,
+    # the tiled kernel; (600,700,2048): enough tiles for the tiled kernel.
     x = _rand((M, Kd), torch.float32, 30)
     w = _rand((N, Kd), torch.float32, 31, 1 / math.sqrt(Kd))
     b = _rand((N,), torch.float32, 32)
     y = K.linear(x.to(dev), w.to(dev), b.to(dev))
     _gate(oracle.linear(_np(x), _np(w), _np(b)), y, TOL_F32)
+    b2 = _rand((N,), torch.float32, 33)
+    y2 = K.linear(x.to(dev), w.to(dev), b.to(dev), b2.to(dev))
+    _gate(oracle.linear(_np(x), _np(w), _np(b)) + _np(b2), y2, TOL_F32)
+    y0 = K.linear(x.to(dev), w.to(dev))
+    _gate(oracle.linear(_np(x), _np(w)), y0, TOL_F32)
 
 
 @pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
