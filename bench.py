@@ -91,6 +91,30 @@ def time_cpu(fn, budget_s: float, min_reps: int = 2) -> tuple[float, int, object
     return times[len(times) // 2], len(times), out
 
 
+# --------------------------------------------------------------------- traffic
+
+#: rocprofv3 counter calibration, from a 2 GiB device copy on the MI355X box:
+#: FETCH_SIZE reads half the bytes copied, WRITE_SIZE all of them.
+FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
+TRAFFIC_TABLE = ROOT / "profiles" / "pmc_traffic_all_forms.md"
+
+
+def traffic_bytes(kernel_key: str) -> float | None:
+    """HBM bytes per launch of a kernel from the committed counter summary:
+    (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0) KiB per dispatch, averaged over
+    its dispatches (rows ``| key | fetch KiB | write KiB | ... |``)."""
+    if not kernel_key or not TRAFFIC_TABLE.exists():
+        return None
+    for line in TRAFFIC_TABLE.read_text().splitlines():
+        cells = [c.strip().strip("`") for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 3 and cells[0] == kernel_key:
+            try:
+                return round((float(cells[1]) * FETCH_SCALE + float(cells[2]) * WRITE_SCALE) * 1024.0)
+            except ValueError:
+                return None
+    return None
+
+
 # ---------------------------------------------------------------------- forms
 
 
@@ -105,6 +129,7 @@ class Form:
     peak = 0.0
     work = 0.0         # algorithmic flops or bytes per step
     dom_name = ""
+    dom_key = ""       # the dominant kernel's row in the counter summary
     dom_work = 0.0     # algorithmic flops or bytes per dominant-kernel launch
 
     def setup(self, dev) -> None: ...
@@ -127,38 +152,61 @@ def _gen(seed=0):
     return torch.Generator(device="cuda").manual_seed(seed)
 
 
+_SINKS: dict = {}
+
+
+def _sink(dev):
+    """The drop-in sink (one per device): every form below except C5 is
+    delivered through its executor table exactly as catopt routes a term."""
+    from catopt_amd.sink import HipSink
+
+    key = str(dev)
+    if key not in _SINKS:
+        _SINKS[key] = HipSink(device=dev)
+    return _SINKS[key]
+
+
 class C1WeightChain(Form):
     name, dtype, unit, bound = "c1", "f32", "TFLOP/s", "mfma"
     workload = "C1 deep linear weight chain: 8x nn.Linear(512,512)+bias folded to one GEMM+bias, x[64,512] fp32"
     peak = PEAK["fp32_tflops"]
     work = dom_work = 2.0 * 64 * 512 * 512
-    dom_name = "gemm_generic<float,NT,BIAS>"
+    dom_name = "gemm_f32_skinny<BIAS> (hipGraph replay)"
+    dom_key = "gemm_f32_skinny<1>"
 
     def setup(self, dev):
         import torch
 
+        from catopt_amd import forms
         from catopt_amd import kernels as K
+        from catopt_amd.runner import HipGraphRunner
+        from catopt_amd.sink import deliver
 
         torch.manual_seed(0)
         layers = [torch.nn.Linear(512, 512) for _ in range(8)]
         self.x_cpu = torch.randn(64, 512)
-        self.Ws = [l.weight.detach().to(dev) for l in layers]
-        self.bs = [l.bias.detach().to(dev) for l in layers]
         self.Ws_cpu = [l.weight.detach().numpy() for l in layers]
         self.bs_cpu = [l.bias.detach().numpy() for l in layers]
+        vals = {}
+        for i, l in enumerate(layers):
+            vals[f"W{i + 1}"], vals[f"b{i + 1}"] = l.weight.detach(), l.bias.detach()
         self.x = self.x_cpu.to(dev)
-        # construction-time fold on the device (7 GEMMs + bias mat-vecs)
-        W = self.Ws[0]
-        c = self.bs[0]
-        for Wl, bl in zip(self.Ws[1:], self.bs[1:]):
-            W = K.matmul(Wl, W)
-            c = K.matmul(Wl, c.unsqueeze(-1)).squeeze(-1) + bl
-        self.W_eff, self.c = W.contiguous(), c.contiguous()
+        # the delivered term through the sink: construction folds the chain on
+        # the device (7 GEMMs + bias mat-vecs); the hipGraph runner captures
+        # the one remaining GEMM + bias, so a step is one graph replay
+        ir, _ = forms.weight_chain_form(8, 512, 64)
+        res = deliver(ir, vals, _sink(dev), (self.x,), runner=HipGraphRunner())
+        self.mod, self.stats = res.module, res.stats
+        (_, refs, _), = self.mod._tape.steps
+        p = self.mod._param_map
+        self.W_eff, self.c = p[refs[1][1]], p[refs[2][1]]
         self.K = K
 
     def step(self):
-        self.y = self.K.linear(self.x, self.W_eff, self.c)
+        self.y = self.mod(self.x)
 
+    # one step is one graph replay of the one kernel: timing it is timing the
+    # kernel without the per-call Python/ctypes launch gap
     dominant = step
 
     def cpu(self, budget):
@@ -186,6 +234,7 @@ class C2SwiGLU(Form):
     M, D, F = 8 * 2048, 4096, 11008
     work = 2.0 * M * D * 2 * F + 2.0 * M * F * D
     dom_name = "gemm_bf16_nt<SILU_MUL>"
+    dom_key = "gemm_bf16_nt<3>"
     dom_work = 2.0 * M * D * 2 * F
 
     def setup(self, dev):
@@ -194,24 +243,37 @@ class C2SwiGLU(Form):
         from catopt_amd import _lib as L
         from catopt_amd import kernels as K
 
+        from catopt_amd import forms
+        from catopt_amd.sink import deliver
+
         g = _gen(0)
         bf = torch.bfloat16
         self.L = L
         self.x = torch.randn(8, 2048, self.D, device=dev, generator=g).to(bf)
-        self.gamma = (1 + 0.02 * torch.randn(self.D, device=dev, generator=g)).to(bf)
-        wg = (0.02 * torch.randn(self.F, self.D, device=dev, generator=g)).to(bf)
-        wu = (0.02 * torch.randn(self.F, self.D, device=dev, generator=g)).to(bf)
-        self.w_cat = torch.cat([wg, wu], 0).contiguous()  # the folded concat(W_gate, W_up)
-        del wg, wu
-        self.w_down = (0.02 * torch.randn(self.D, self.F, device=dev, generator=g)).to(bf)
+        vals = {
+            "gamma": (1 + 0.02 * torch.randn(self.D, device=dev, generator=g)).to(bf),
+            "W_gate": (0.02 * torch.randn(self.F, self.D, device=dev, generator=g)).to(bf),
+            "W_up": (0.02 * torch.randn(self.F, self.D, device=dev, generator=g)).to(bf),
+            "W_down": (0.02 * torch.randn(self.D, self.F, device=dev, generator=g)).to(bf),
+        }
+        # delivered term: rms_norm -> linear(concat(W_gate, W_up)) -> chunk/silu/mul
+        # -> linear(W_down); construction folds the concat and fuses the
+        # gate into the GEMM epilogue (tape: rms_norm, hip_swiglu, hip_linear)
+        ir, _ = forms.swiglu_block_form((8, 2048), self.D, self.F)
+        res = deliver(ir, vals, _sink(dev), (self.x,))
+        self.mod, self.stats = res.module, res.stats
+        del vals
+        steps = self.mod._tape.steps
+        assert [s[0] for s in steps] == ["rms_norm", "hip_swiglu", "hip_linear"], steps
+        p = self.mod._param_map
+        self.gamma = p[steps[0][1][1][1]]
+        self.w_cat = p[steps[1][1][1][1]]
+        self.w_down = p[steps[2][1][1][1]]
         self.K = K
         self.h = K.rmsnorm(self.x, self.gamma, 1e-6)
 
     def step(self):
-        K = self.K
-        h = K.rmsnorm(self.x, self.gamma, 1e-6)
-        a = K.linear(h, self.w_cat, epilogue=self.L.EPI_SILU_MUL)
-        self.y = K.linear(a, self.w_down)
+        self.y = self.mod(self.x)
 
     def dominant(self):
         self.K.linear(self.h, self.w_cat, epilogue=self.L.EPI_SILU_MUL)
@@ -249,6 +311,7 @@ class C3Attention(Form):
     peak = PEAK["bf16_tflops"]
     work = dom_work = 4.0 * B * H * T * T * Dh / 2  # causal half of the square
     dom_name = "attn_fwd_kernel<128,CAUSAL>"
+    dom_key = "attn_fwd_kernel<128, 1>"
 
     def setup(self, dev):
         import torch
@@ -262,11 +325,23 @@ class C3Attention(Form):
         self.v = torch.randn(shp, device=dev, generator=g).to(torch.bfloat16)
         self.scale = 1.0 / math.sqrt(self.Dh)
         self.K = K
+        from catopt_amd import forms
+        from catopt_amd.sink import deliver
+
+        # delivered term: om_apply(om_elem(masked_fill(q k^T / sqrt(d), !mask, -inf), v))
+        # with the lower-triangular bool mask as a Param; the OM executor finds
+        # the triangle bit-exactly at construction and runs the causal kernel
+        ir, _ = forms.causal_attention_form(self.B, self.H, self.T, self.Dh, mask="param")
+        mask = torch.ones(self.T, self.T, dtype=torch.bool, device=dev).tril()
+        res = deliver(ir, {"mask": mask}, _sink(dev), (self.q, self.k, self.v))
+        self.mod, self.stats = res.module, res.stats
+        assert self.mod._plan["leaves"][0]["mask_kind"] == "causal"
 
     def step(self):
-        self.o = self.K.attention(self.q, self.k, self.v, self.scale, causal=True)
+        self.o = self.mod(self.q, self.k, self.v)
 
-    dominant = step
+    def dominant(self):
+        self.K.attention(self.q, self.k, self.v, self.scale, causal=True)
 
     def cpu(self, budget):
         import oracle
@@ -290,7 +365,8 @@ class C4Retention(Form):
     peak = PEAK["hbm_gbs"]
     work = dom_work = 4.0 * B * H * T * Dh * 2  # q, k, v read + o written, bf16
     flops = B * H * (T / C) * (4 * C * C * Dh + 4 * C * Dh * Dh)
-    dom_name = "ret_seg_out"
+    dom_name = "ret_seg_state + ret_seg_carry + ret_seg_out"
+    dom_key = "retention (3 kernels)"
 
     def setup(self, dev):
         import torch
@@ -306,11 +382,22 @@ class C4Retention(Form):
         self.gamma = torch.tensor([1 - 2.0 ** (-5 - h / 2) for h in range(self.H)],
                                   dtype=torch.float32, device=dev)
         self.K = K
+        from catopt_amd import forms
+        from catopt_amd.sink import deliver
+
+        # delivered term: the K-way chunked form (K = T/C = 128 arms, 8128
+        # cross blocks), parsed once into (q, k, v, gamma, scale) by the
+        # chunked-decay executor
+        ir, _ = forms.retention_kway_form(self.B, self.H, self.T, self.Dh, self.C)
+        res = deliver(ir, {"gamma": self.gamma}, _sink(dev), (self.q, self.k, self.v))
+        self.mod, self.stats = res.module, res.stats
+        assert self.mod.n_chunks == self.T // self.C
 
     def step(self):
-        self.o = self.K.retention(self.q, self.k, self.v, self.gamma, 1.0)
+        self.o = self.mod(self.q, self.k, self.v)
 
-    dominant = step
+    def dominant(self):
+        self.K.retention(self.q, self.k, self.v, self.gamma, 1.0)
 
     def cpu(self, budget):
         import numpy as np
@@ -337,6 +424,7 @@ class C5SSM(Form):
     peak = PEAK["hbm_gbs"]
     work = dom_work = 4.0 * (B * T * D * N + 2 * B * T * N + 2 * B * T * D)
     dom_name = "ssm_stream<16,per-state a>"
+    dom_key = "ssm_stream<16, true>"
 
     def setup(self, dev):
         import torch
@@ -392,6 +480,7 @@ class CopyStream(Form):
     peak = PEAK["hbm_gbs"]
     work = dom_work = 2.0 * NBYTES
     dom_name = "torch copy kernel"
+    dom_key = "__amd_rocclr_copyBuffer (2 GiB)"
 
     def setup(self, dev):
         import torch
@@ -436,12 +525,14 @@ def measure(form: Form, dev, steps: int, warmup: int, cpu_budget: float | None) 
             "peak": form.peak,
             "unit": "TFLOP/s" if form.bound == "mfma" else "GB/s",
             "frac": round(achieved / form.peak, 4),
-            "traffic": None,
+            "traffic": traffic_bytes(form.dom_key),
             "avg_launch_us": round(dom_ms * 1e3, 3),
             "work_per_launch": form.dom_work,
         },
         "wall_ms_incl_warmup": round(wall_ms, 2),
     }
+    if getattr(form, "stats", None) is not None:
+        rec["delivery"] = {k: (v.value if hasattr(v, "value") else v) for k, v in form.stats.items()}
     if isinstance(form, C4Retention):
         rec["tflops_chunked_form"] = round(form.flops / (ms * 1e-3) / 1e12, 3)
     if cpu_budget:
