@@ -273,6 +273,120 @@ __global__ __launch_bounds__(kThreads) void ssm_chunk_apply(
                         cclamp(cs[k + 1], T), h, nullptr);
 }
 
+// ----------------------------------------------------- LDS-staged streaming
+// The streaming schedule for a per-state a (B, T, D, N), fed through LDS:
+// a workgroup owns DPW channels x N states (one 4 KB slice of a per step)
+// and streams U-step stages of a, b, c and x into LDS with direct
+// global->LDS loads (no registers held while the loads are in flight), two
+// stages deep: the loads of stage s+1 are issued before the arithmetic of
+// stage s and waited for after it, one barrier per stage.  Each workgroup
+// thus keeps U x ~4.4 KB of reads in flight, two workgroups per CU, which is
+// what HBM's bandwidth-latency product asks of 256 CUs.  The chunk table
+// tiles [0, T) in order, so one pass over t = 0 .. T-1 is that walk.
+constexpr int SU = 8;  // steps per LDS stage
+
+template <int N>
+struct SsmLds {
+  static constexpr int TPD = N / 4, DPW = kThreads / TPD;
+  static constexpr int A_BYTES = SU * DPW * N * 4;   // SU x 4 KB
+  static constexpr int X_BYTES = SU * DPW * 4;
+  static constexpr int V_BYTES = SU * N * 4;         // b or c
+  static constexpr int STAGE = A_BYTES + X_BYTES + 2 * V_BYTES;
+  static constexpr int BYTES = 2 * STAGE;
+  static constexpr int X_SLOTS = SU * DPW;           // 4-byte slots
+  static constexpr int V_SLOTS = SU * N;
+};
+
+typedef __attribute__((address_space(3))) void* lds_vptr;
+
+template <int N>
+__global__ __launch_bounds__(kThreads, 2) void ssm_stream_lds(
+    const float* __restrict__ a, const float* __restrict__ bx, const float* __restrict__ c,
+    const float* __restrict__ x, const float* __restrict__ h0, int64_t T, int64_t D,
+    float* __restrict__ y, float* __restrict__ hf) {
+  using L = SsmLds<N>;
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t b = blockIdx.y;
+  const int64_t d0 = (int64_t)blockIdx.x * L::DPW;
+  const int ch = tid / L::TPD, n0 = (tid % L::TPD) * 4;
+  const int64_t d = d0 + ch;
+  const bool dok = d < D;
+  // a slot of this thread: channel d (clamped to a valid one), states n0..n0+3
+  const int64_t a_lane = (((dok ? d : D - 1) * N) + n0);
+  const int64_t nst = (T + SU - 1) / SU;
+
+  auto issue = [&](int64_t st, int stage) {
+    char* base = lds + stage * L::STAGE;
+    const int64_t t0 = st * SU;
+#pragma unroll
+    for (int u = 0; u < SU; ++u) {
+      const int64_t t = t0 + u < T ? t0 + u : T - 1;
+      const float* src = a + ((b * T + t) * D) * N + a_lane;
+      __builtin_amdgcn_global_load_lds(src, (lds_vptr)(base + u * (L::DPW * N * 4) + wave * 1024), 16, 0, 0);
+    }
+    char* xb = base + L::A_BYTES;
+#pragma unroll
+    for (int i = 0; i < (L::X_SLOTS + kThreads - 1) / kThreads; ++i) {
+      const int s = i * kThreads + tid;
+      if (i * kThreads + wave * 64 < L::X_SLOTS) {  // whole waves: DPW*SU is a multiple of 64
+        const int u = s / L::DPW, cc = s % L::DPW;
+        const int64_t t = t0 + u < T ? t0 + u : T - 1;
+        const int64_t dd = d0 + cc < D ? d0 + cc : D - 1;
+        __builtin_amdgcn_global_load_lds(x + (b * T + t) * D + dd,
+                                         (lds_vptr)(xb + (i * kThreads + wave * 64) * 4), 4, 0, 0);
+      }
+    }
+    char* vb = xb + L::X_BYTES;
+#pragma unroll
+    for (int i = 0; i < (L::V_SLOTS + kThreads - 1) / kThreads; ++i) {
+      const int s = i * kThreads + tid;
+      if (s < L::V_SLOTS) {
+        const int u = s / N, n = s % N;
+        const int64_t t = t0 + u < T ? t0 + u : T - 1;
+        const int64_t off = (b * T + t) * N + n;
+        const int lbase = (i * kThreads + wave * 64) * 4;
+        __builtin_amdgcn_global_load_lds(bx + off, (lds_vptr)(vb + lbase), 4, 0, 0);
+        __builtin_amdgcn_global_load_lds(c + off, (lds_vptr)(vb + L::V_BYTES + lbase), 4, 0, 0);
+      }
+    }
+  };
+
+  f32x4 h = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int64_t sidx = (b * D + (dok ? d : 0)) * N + n0;
+  if (h0 && dok) h = *reinterpret_cast<const f32x4*>(h0 + sidx);
+  if (nst > 0) {
+    issue(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  for (int64_t st = 0; st < nst; ++st) {
+    const int cur = (int)(st & 1);
+    if (st + 1 < nst) issue(st + 1, cur ^ 1);
+    const char* base = lds + cur * L::STAGE;
+    const char* xb = base + L::A_BYTES;
+    const char* vb = xb + L::X_BYTES;
+    const int64_t t0 = st * SU;
+    const int un = T - t0 < SU ? (int)(T - t0) : SU;
+    for (int u = 0; u < un; ++u) {
+      const f32x4 av = *reinterpret_cast<const f32x4*>(base + u * (L::DPW * N * 4) + tid * 16);
+      const f32x4 bv = *reinterpret_cast<const f32x4*>(vb + (u * N + n0) * 4);
+      const f32x4 cv = *reinterpret_cast<const f32x4*>(vb + L::V_BYTES + (u * N + n0) * 4);
+      const float xv = *reinterpret_cast<const float*>(xb + (u * L::DPW + ch) * 4);
+      h = av * h + bv * xv;
+      const f32x4 chv = cv * h;
+      const float r = lane_reduce<N>(chv[0] + chv[1] + chv[2] + chv[3]);
+      if (dok && n0 == 0) y[(b * T + t0 + u) * D + d] = r;
+    }
+    if (st + 1 < nst) {
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+  }
+  if (hf && dok) *reinterpret_cast<f32x4*>(hf + sidx) = h;
+}
+
 // Lanes that fill the GPU: 256 CUs x 8 waves x 64 lanes.
 constexpr int64_t kFillThreads = 256LL * 8 * 64;
 
@@ -287,6 +401,19 @@ int32_t ssm_launch(int64_t B, int64_t T, int64_t D, const float* a, const float*
   bool chunked = schedule == CATOPT_SCAN_CHUNKED;
   if (schedule == CATOPT_SCAN_AUTO) chunked = nc > 1 && threads < kFillThreads;
   if (gx > 0x7fffffff || B > 65535 || nc > 65535) return CATOPT_E_UNSUPPORTED;
+  if (!chunked && APS) {
+    static bool attr_done = false;
+    if (!attr_done) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ssm_stream_lds<N>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, SsmLds<N>::BYTES);
+      if (e != hipSuccess) return set_hip_error(e);
+      attr_done = true;
+    }
+    ssm_stream_lds<N><<<dim3((uint32_t)gx, (uint32_t)B), dim3(kThreads), SsmLds<N>::BYTES, s>>>(
+        a, bx, c, x, h0, T, D, y, hf);
+    CATOPT_LAUNCH_CHECK();
+    return CATOPT_OK;
+  }
   if (!chunked) {
     ssm_stream<N, APS><<<dim3((uint32_t)gx, (uint32_t)B), dim3(kThreads), 0, s>>>(
         a, bx, c, x, h0, cs, nc, T, D, y, hf);
