@@ -8,7 +8,11 @@ the library travels with the repository snapshot).  Compile flags:
 * ``-Xclang -target-feature -Xclang -packed-fp32-ops`` disables packed
   fp32 instruction selection (the host pass warns it does not know the
   feature; that warning is harmless);
-* ``-O3 -std=c++17 -fPIC``.
+* ``-O3 -std=c++17 -fPIC``;
+* per-source extras in ``SOURCE_FLAGS``: the retention scan keeps its MFMA
+  accumulators in VGPRs (``-amdgpu-mfma-vgpr-form``) because its loop scales
+  and converts them on the VALU every chunk, and AGPR-resident accumulators
+  would cost a copy in and out for each of those operations.
 
 Run ``python -m catopt_amd.build`` (or ``__graft_entry__.build()``).
 """
@@ -44,6 +48,11 @@ HIPCC_FLAGS = [
 ]
 
 
+SOURCE_FLAGS = {
+    "retention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _hipcc() -> str:
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(exe).exists():
@@ -52,7 +61,8 @@ def _hipcc() -> str:
 
 
 def _compile(src: Path, obj: Path, extra: list[str]) -> tuple[Path, str]:
-    cmd = [_hipcc(), *HIPCC_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(src.name, []), *extra, "-c", str(src), "-o",
+           str(obj)]
     p = subprocess.run(cmd, capture_output=True, text=True)
     if p.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{p.stdout}\n{p.stderr}")

@@ -2,29 +2,42 @@
 //
 //   o[t] = scale * sum_{s <= t} γ^(t-s) (q[t]·k[s]) v[s]
 //
-// computed chunk-wise with chunk length C = 64 and head dim 128, exactly the
-// K-way block decomposition (diagonal blocks with decay(γ, C), strict-lower
-// blocks with the rank-1 decay_vec factors γ^(r+(i-j)C) and γ^(-c)), with the
-// strict-lower blocks of row i folded into the state
-//   S_i = sum_{j<i} sum_c γ^((i-j)C - c) k_jc ⊗ v_jc,
-//   S_{i+1} = γ^C S_i + sum_c γ^(C-c) k_ic ⊗ v_ic,
-// so that chunk i's output is
-//   oᵀ_i = scale * ( vᵀ_i (s_iᵀ ⊙ Dᵀ) + diag(γ^r) Sᵀ_i q_iᵀ ).
+// evaluated chunk-wise with chunk length C = 64 and head dim 128.  Chunk i
+// (rows t = iC + q) takes its diagonal block with decay(γ, C) and every
+// strict-lower block through the carried state
+//   S_i = sum_{j<i} sum_c γ^((i-j)C - c) k_jc ⊗ v_jc,   S_{i+1} = γ^C S_i + sum_c γ^(C-c) k_ic ⊗ v_ic,
+// so that  o_i = scale * ( (q_i k_iᵀ ⊙ D) v_i + diag(γ^q) q_i S_i ),  D[q][c] = γ^(q-c) (c <= q):
+// the K-way block decomposition's algebra, with its rank-1 decay_vec factors
+// γ^(q + (i-j)C) · γ^(-c) folded into the state.
 //
-// Parallel schedule over (b·h) x segments of G chunks (three launches):
-//   seg_state : each segment accumulates its local end state from zero;
-//   seg_carry : per state element, exclusive fold over segments
-//               (Start_{s+1} = γ^(C·G) Start_s + E_s), in place;
-//   seg_out   : each segment re-walks its chunks from Start_s, emitting o.
-// HBM traffic: k, v twice, q once, o once, plus the fp32 segment states.
+// Single pass.  One workgroup per (b, h, 32-column slice of v): the state
+// slice S[:, slice] (128 x 32 fp32) stays in registers while the workgroup
+// walks its head's chunks in order, so q, k, v and o each cross HBM once.
+// The four slices of a head are dealt to one XCD (workgroups go round robin
+// over the 8 XCDs), so the q and k chunks all four read come from its L2.
 //
-// MFMA mapping (32x32x16 bf16, fp32 accumulate), 4 waves per workgroup:
-//   wave w: query block qb = w & 1 (32 queries), value half dh = w >> 1;
-//   sᵀ = k qᵀ          A = k rows (LDS), B = q fragments (registers)
-//   intraᵀ = vᵀ Pᵀ     A = vᵀ (LDS, key-permuted 8-byte runs), B = Pᵀ from
-//                      the sᵀ accumulator (the attention-kernel trick)
-//   crossᵀ = Sᵀ qᵀ     A = Sᵀ bf16 copy (LDS), B = q fragments
-//   S += k̃ᵀ v          A = k̃ᵀ (LDS), B = vᵀ (LDS); wave w owns dk rows 32w..
+// Per chunk, 4 waves, 32x32x16 bf16 MFMA with fp32 accumulation, all
+// products computed transposed (output column = query):
+//   wave (kb, qb) = (w >> 1, w & 1), keys 32kb.., queries 32qb..:
+//     X  = Sᵀ[:, dk half kb] Qᵀ          A = S fragments (LDS, bf16), B = q rows
+//     X *= scale γ^q                      (per lane: the lane's column is q)
+//     sᵀ = K Qᵀ  (kb <= qb only)          A = k rows, B = q rows
+//     X += Vᵀ (sᵀ ⊙ scale Dᵀ)             A = v via the transposing LDS read,
+//                                         B = P straight from the sᵀ accumulator
+//   wave w owns state rows dk = 32w..32w+31:
+//     S = γ^C S + Kᵀ (γ^(C-c) V)          A = k via the transposing LDS read,
+//                                         B = decayed v, likewise; the workgroup
+//                                         decays the v slice once per chunk
+//   o[q] = X(0, qb) + X(1, qb), the pair meeting in LDS.
+// An MFMA's k index is only a summation order: products over keys take their
+// keys in the sᵀ accumulator's row order 8(r/4) + 4g + r%4 (so P feeds an
+// MFMA without a shuffle), products over dk take dims in natural order, and
+// the owner waves re-lay their state rows into natural order in LDS.
+//
+// Tiles reach LDS by direct global->LDS loads through a ring of NSTAGE
+// stages: chunk i + NSTAGE - 1's loads are issued before chunk i's arithmetic,
+// which keeps several chunks of loads in flight per workgroup (one workgroup
+// per CU leaves nothing else to hide the memory latency behind).
 #include "common.hpp"
 
 namespace catopt {
@@ -33,307 +46,283 @@ namespace {
 constexpr int NT = 256;
 constexpr int CH = 64;    // chunk length
 constexpr int HD = 128;   // head dim (dk = dv)
-constexpr int KCH = HD / 8;
+constexpr int SL = 32;    // v columns per workgroup
+constexpr int NSL = HD / SL;
 
-// LDS layout (bf16 elements)
-constexpr int OFF_K = 0;                    // k  [64][128]  row-major, chunk-swizzled
-constexpr int OFF_KT = OFF_K + CH * HD;     // k̃ᵀ [128][64] unit-swizzled
-constexpr int OFF_VT = OFF_KT + HD * CH;    // vᵀ [128][64] unit-swizzled
-constexpr int OFF_ST = OFF_VT + HD * CH;    // Sᵀ [128][128] bf16, chunk-swizzled
-constexpr int LDS_ELEMS = OFF_ST + HD * HD;
-constexpr int LDS_BYTES = LDS_ELEMS * 2;
+typedef __attribute__((ext_vector_type(4))) short s16x4;
 
-__device__ __forceinline__ int k_off(int key, int chunk) {
-  return key * HD + ((chunk ^ (key & (KCH - 1))) << 3);
-}
-__device__ __forceinline__ int t_off(int d, int unit) {  // [128][64] transposed tiles
-  return d * CH + ((unit ^ ((d >> 1) & 15)) << 2);
-}
-__device__ __forceinline__ int st_off(int dv, int chunk) {
-  return dv * HD + ((chunk ^ (dv & (KCH - 1))) << 3);
-}
+// LDS layout (bytes).  Per stage: k and q tiles [64][128] bf16 whose 16-byte
+// chunks are XOR-swizzled by (row & 15), then the v slice [64][32] bf16.
+constexpr int KQ_BYTES = CH * HD * 2;             // 16 KB
+constexpr int V_BYTES = CH * SL * 2;              // 4 KB
+constexpr int STAGE = 2 * KQ_BYTES + V_BYTES;
+#ifndef CATOPT_RET_STAGES
+#define CATOPT_RET_STAGES 3
+#endif
+constexpr int NSTAGE = CATOPT_RET_STAGES;
+constexpr int OFF_SF = NSTAGE * STAGE;            // S fragments [4 waves][2][64 lanes] x 16 B
+constexpr int OFF_X = OFF_SF + 4 * 2 * 64 * 16;   // pair exchange [2 qb][4][64 lanes] x 16 B
+constexpr int OFF_VD = OFF_X + 2 * 4 * 64 * 16;   // decayed v slice γ^(C-c) v_c, [64][32] bf16
+constexpr int LDS_BYTES = OFF_VD + V_BYTES;
+static_assert(NSTAGE >= 2 && LDS_BYTES <= 160 * 1024, "LDS ring does not fit");
+constexpr int LOADS_PER_CHUNK = 9;  // global->LDS instructions per thread per chunk
 
-__device__ __forceinline__ bf16x8 read_t16(const uint16_t* base, int d, int unit0) {
-  const u32x2 lo = *reinterpret_cast<const u32x2*>(base + t_off(d, unit0));
-  const u32x2 hi = *reinterpret_cast<const u32x2*>(base + t_off(d, unit0 + 1));
-  return __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
-}
-
-struct ChunkRegs {
-  u32x4 k[4];  // keys 4*kk + e, d-chunk c
-  u32x4 v[4];
-};
-
-__device__ __forceinline__ void load_kv(ChunkRegs& r, const uint16_t* __restrict__ k,
-                                        const uint16_t* __restrict__ v, int64_t t0, int tid) {
-  const int c = tid % KCH, kk = tid / KCH;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int64_t row = t0 + 4 * kk + e;
-    r.k[e] = *reinterpret_cast<const u32x4*>(k + row * HD + c * 8);
-    r.v[e] = *reinterpret_cast<const u32x4*>(v + row * HD + c * 8);
-  }
+// s_waitcnt: vmcnt <= n, lgkmcnt = 0, expcnt not waited on (gfx9 encoding).
+template <int n>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(n >= 0 && n < 64, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | ((n >> 4) << 14));
 }
 
-__device__ __forceinline__ uint32_t scale_bf16x2(uint32_t w, float slo, float shi) {
-  return pack_bf16x2(__uint_as_float(w << 16) * slo, __uint_as_float(w & 0xffff0000u) * shi);
+__device__ __forceinline__ int kq_off(int row, int chunk) {  // byte offset in a k / q tile
+  return row * (HD * 2) + ((chunk ^ (row & 15)) << 4);
 }
 
-// Store k (row-major), k̃ᵀ = (γ^(C-key) k)ᵀ and vᵀ into LDS.
-template <bool WITH_K>
-__device__ __forceinline__ void store_kv(uint16_t* lds, const ChunkRegs& r, float lg, int tid) {
-  const int c = tid % KCH, kk = tid / KCH;
-  if (WITH_K) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) *reinterpret_cast<u32x4*>(lds + OFF_K + k_off(4 * kk + e, c)) = r.k[e];
-  }
-  float kd[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) kd[e] = __builtin_amdgcn_exp2f((float)(CH - (4 * kk + e)) * lg);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int sh = (e & 1) * 16, w = e >> 1;
-    uint32_t kv[4], vv[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t kb = (r.k[j][w] >> sh) & 0xffffu;
-      kv[j] = f32_to_bf16(__uint_as_float(kb << 16) * kd[j]);
-      vv[j] = (r.v[j][w] >> sh) & 0xffffu;
-    }
-    const int d = c * 8 + e;
-    *reinterpret_cast<u32x2*>(lds + OFF_KT + t_off(d, kk)) = u32x2{kv[0] | (kv[1] << 16), kv[2] | (kv[3] << 16)};
-    *reinterpret_cast<u32x2*>(lds + OFF_VT + t_off(d, kk)) = u32x2{vv[0] | (vv[1] << 16), vv[2] | (vv[3] << 16)};
-  }
+// Direct global->LDS load of 16 bytes per lane: lane l's bytes land at LDS
+// byte address lds_wave + 16 l (lds_wave is wave-uniform, it goes to M0).
+// Issued as inline asm so that the compiler does not treat every later LDS
+// read as a possible reader of this load (it would wait for all loads in
+// flight before each transposing read); completion is awaited explicitly
+// with s_waitcnt vmcnt before the workgroup barrier that publishes a stage.
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_wave) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_wave)
+               : "m0");
 }
 
-// S[dk = 32*w + row][dv = 32*cb + l32] accumulators: S = γ^C S + k̃ᵀ v.
-__device__ __forceinline__ void state_update(f32x16 (&S)[4], const uint16_t* lds, float gC,
-                                             int wave, int l32, int g) {
-#pragma unroll
-  for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) S[cb][r] *= gC;
-#pragma unroll
-  for (int j = 0; j < CH / 16; ++j) {
-    const bf16x8 a = read_t16(lds + OFF_KT, 32 * wave + l32, 4 * j + 2 * g);
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-      const bf16x8 b = read_t16(lds + OFF_VT, 32 * cb + l32, 4 * j + 2 * g);
-      S[cb] = mfma32x32x16(a, b, S[cb]);
-    }
-  }
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
 }
 
-struct SegGeom {
-  int64_t bh, seg, c0, c1;  // chunk range [c0, c1)
-};
-
-__device__ __forceinline__ SegGeom seg_geom(int nseg, int G, int64_t nchunks) {
-  SegGeom s;
-  s.bh = blockIdx.x / nseg;
-  s.seg = blockIdx.x % nseg;
-  s.c0 = s.seg * G;
-  s.c1 = s.c0 + G < nchunks ? s.c0 + G : nchunks;
-  return s;
+// Transposing LDS read (ds_read_b64_tr_b16).  Within each 16-lane group, when
+// lane j points at row (base + j/4), columns c0 + 4(j%4) .. +3, lane i gets
+// column c0 + i of rows base .. base+3.
+__device__ __forceinline__ s16x4 ds_read_tr(const char* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
 }
 
-__global__ __launch_bounds__(NT) void ret_seg_state(const uint16_t* __restrict__ k,
-                                                    const uint16_t* __restrict__ v,
-                                                    const float* __restrict__ gamma, int H,
-                                                    int64_t T, int nseg, int G,
-                                                    float* __restrict__ ws) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-  const int64_t nchunks = T / CH;
-  const SegGeom sg = seg_geom(nseg, G, nchunks);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
-  const float lg = __log2f(gamma[sg.bh % H]);
+__device__ __forceinline__ bf16x8 cat8(s16x4 lo, s16x4 hi) {
+  const u32x2 a = __builtin_bit_cast(u32x2, lo), b = __builtin_bit_cast(u32x2, hi);
+  return __builtin_bit_cast(bf16x8, u32x4{a[0], a[1], b[0], b[1]});
+}
+
+__global__ __launch_bounds__(NT, 1) void retention_scan(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const float* __restrict__ gamma, int H, int64_t T, float scale, uint16_t* __restrict__ o) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  // work item (b*h, slice), the four slices of a head on one XCD
+  const int nblk = gridDim.x;
+  int wid = blockIdx.x;
+  if ((nblk & 7) == 0) wid = (wid & 7) * (nblk >> 3) + (wid >> 3);
+  const int64_t bh = wid / NSL;
+  const int sl = wid % NSL;
+  const int64_t base = bh * T * HD;
+  q += base;
+  k += base;
+  v += base;
+  o += base;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, g = lane >> 5;
+  const int G = lane >> 4, jj = lane & 15;  // 16-lane group, lane within it
+  const int kb = wave >> 1, qb = wave & 1;
+  const float lg = __log2f(gamma[bh % H]);
   const float gC = __builtin_amdgcn_exp2f((float)CH * lg);
-  k += sg.bh * T * HD;
-  v += sg.bh * T * HD;
-  f32x16 S[4];
+  const int nchunks = (int)(T / CH);
+  const int qrow = 32 * qb + l32;  // this lane's query: sᵀ column and output column
+  // output scale folded into the per-query and per-entry decay factors
+  const float gq = scale * __builtin_amdgcn_exp2f((float)qrow * lg);
+
+  // scale * decay of this lane's sᵀ entries (key 32kb + acc_row(r, g), query qrow)
+  float dec[16];
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) S[cb][r] = 0.f;
-  ChunkRegs cur, nxt;
-  if (sg.c0 < sg.c1) load_kv(cur, k, v, sg.c0 * CH, tid);
-  for (int64_t ci = sg.c0; ci < sg.c1; ++ci) {
-    store_kv<false>(lds, cur, lg, tid);
-    __syncthreads();
-    if (ci + 1 < sg.c1) load_kv(nxt, k, v, (ci + 1) * CH, tid);
-    state_update(S, lds, gC, wave, l32, g);
-    __syncthreads();
-    if (ci + 1 < sg.c1) cur = nxt;
+  for (int r = 0; r < 16; ++r) {
+    const int key = 32 * kb + acc_row(r, g);
+    dec[r] = key <= qrow ? scale * __builtin_amdgcn_exp2f((float)(qrow - key) * lg) : 0.f;
   }
-  float* E = ws + (sg.bh * nseg + sg.seg) * (int64_t)(HD * HD);
-#pragma unroll
-  for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) E[(32 * wave + acc_row(r, g)) * HD + 32 * cb + l32] = S[cb][r];
-}
+  // γ^(C - key) of the v row this thread decays (row tid / 4)
+  const float vdec = __builtin_amdgcn_exp2f((float)(CH - (tid >> 2)) * lg);
 
-// In place: ws[bh][s] := state entering segment s.
-__global__ __launch_bounds__(NT) void ret_seg_carry(const float* __restrict__ gamma, int H,
-                                                    int nseg, int G, float* __restrict__ ws) {
-  const int64_t bh = blockIdx.y;
-  const int e = blockIdx.x * NT + threadIdx.x;  // element of the 128x128 state
-  const float gSeg = __builtin_amdgcn_exp2f((float)(CH * G) * __log2f(gamma[bh % H]));
-  float cin = 0.f;
-  float* base = ws + bh * nseg * (int64_t)(HD * HD) + e;
-  for (int s = 0; s < nseg; ++s) {
-    const float es = base[(int64_t)s * HD * HD];
-    base[(int64_t)s * HD * HD] = cin;
-    cin = gSeg * cin + es;
+  // load slots: k and q 4 x 16 B each, v one 16-byte slot
+  int kq_goff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int s = i * NT + wave * 64 + lane;
+    const int row = s >> 4, cp = s & 15;
+    kq_goff[i] = row * HD + ((cp ^ (row & 15)) << 3);
   }
-}
+  const int v_goff = (tid >> 2) * HD + sl * SL + (tid & 3) * 8;
+  const uint32_t lds_base = lds_u32(lds);
 
-__global__ __launch_bounds__(NT) void ret_seg_out(const uint16_t* __restrict__ q,
-                                                  const uint16_t* __restrict__ k,
-                                                  const uint16_t* __restrict__ v,
-                                                  const float* __restrict__ gamma, int H,
-                                                  int64_t T, int nseg, int G, float scale,
-                                                  int zero_start, const float* __restrict__ ws,
-                                                  uint16_t* __restrict__ o) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-  const int64_t nchunks = T / CH;
-  const SegGeom sg = seg_geom(nseg, G, nchunks);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
-  const int qb = wave & 1, dh = wave >> 1;
-  const float lg = __log2f(gamma[sg.bh % H]);
-  const float gC = __builtin_amdgcn_exp2f((float)CH * lg);
-  q += sg.bh * T * HD;
-  k += sg.bh * T * HD;
-  v += sg.bh * T * HD;
-  o += sg.bh * T * HD;
-
-  // Start state of this segment.
-  f32x16 S[4];
-  const float* Sst = ws + (sg.bh * nseg + sg.seg) * (int64_t)(HD * HD);
+  auto issue = [&](int ci, int stage) {
+    const uint32_t sb = lds_base + stage * STAGE + wave * 1024;
+    const int64_t t0 = (int64_t)ci * CH * HD;
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
-      S[cb][r] = zero_start ? 0.f : Sst[(32 * wave + acc_row(r, g)) * HD + 32 * cb + l32];
-
-  const int qi = 32 * qb + l32;  // this lane's query within the chunk
-  const float qrow_decay = __builtin_amdgcn_exp2f((float)qi * lg);
-  ChunkRegs cur, nxt;
-  bf16x8 qf[HD / 16], qn[HD / 16];
-  auto load_q = [&](bf16x8 (&dst)[HD / 16], int64_t t0) {
-#pragma unroll
-    for (int j = 0; j < HD / 16; ++j)
-      dst[j] = __builtin_bit_cast(
-          bf16x8, *reinterpret_cast<const u32x4*>(q + (t0 + qi) * HD + 16 * j + 8 * g));
+    for (int i = 0; i < 4; ++i) {
+      dma16(k + t0 + kq_goff[i], sb + i * NT * 16);
+      dma16(q + t0 + kq_goff[i], sb + KQ_BYTES + i * NT * 16);
+    }
+    dma16(v + t0 + v_goff, sb + 2 * KQ_BYTES);
   };
-  if (sg.c0 < sg.c1) {
-    load_kv(cur, k, v, sg.c0 * CH, tid);
-    load_q(qf, sg.c0 * CH);
-  }
-  for (int64_t ci = sg.c0; ci < sg.c1; ++ci) {
-    const int64_t t0 = ci * CH;
-    // 1. tiles + bf16 copy of the state entering this chunk (Sᵀ[dv][dk]).
-    store_kv<true>(lds, cur, lg, tid);
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-#pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        const int dv = 32 * cb + l32;
-        const int dk = 32 * wave + 8 * rg + 4 * g;
-        const u32x2 w = u32x2{pack_bf16x2(S[cb][4 * rg], S[cb][4 * rg + 1]),
-                              pack_bf16x2(S[cb][4 * rg + 2], S[cb][4 * rg + 3])};
-        *reinterpret_cast<u32x2*>(lds + OFF_ST + st_off(dv, dk >> 3) + (dk & 7)) = w;
-      }
-    }
-    __syncthreads();
-    if (ci + 1 < sg.c1) {
-      load_kv(nxt, k, v, t0 + CH, tid);
-      load_q(qn, t0 + CH);
-    }
-    // 2. sᵀ = k qᵀ over both key blocks of this wave's query block.
-    f32x16 sacc[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
-#pragma unroll
-    for (int j = 0; j < HD / 16; ++j)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(lds + OFF_K + k_off(32 * kb + l32, 2 * j + g));
-        sacc[kb] = mfma32x32x16(a, qf[j], sacc[kb]);
-      }
-    // 3. Pᵀ = sᵀ ⊙ Dᵀ, Dᵀ[key][q] = γ^(q-key) for key <= q.
-    bf16x8 pf[2][2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = 32 * kb + acc_row(r, g);
-        const float dcy = key <= qi ? __builtin_amdgcn_exp2f((float)(qi - key) * lg) : 0.f;
-        pf[kb][r >> 3][r & 7] = static_cast<__bf16>(sacc[kb][r] * dcy);
-      }
-    // 4./5. intraᵀ and crossᵀ for value rows 64*dh .. +64.
-    f32x16 oacc[2], cacc[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[i][r] = cacc[i][r] = 0.f;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int dv = 64 * dh + 32 * i + l32;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int unit = 8 * kb + 4 * u + g;
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(lds + OFF_VT + t_off(dv, unit));
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(lds + OFF_VT + t_off(dv, unit + 2));
-          oacc[i] = mfma32x32x16(__builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]}),
-                                 pf[kb][u], oacc[i]);
-        }
-#pragma unroll
-      for (int j = 0; j < HD / 16; ++j) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(lds + OFF_ST + st_off(dv, 2 * j + g));
-        cacc[i] = mfma32x32x16(a, qf[j], cacc[i]);
-      }
-    }
-    // 6. o[t0 + qi][dv] = scale * (intra + γ^qi cross)
-    uint16_t* orow = o + (t0 + qi) * HD;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        const int dv = 64 * dh + 32 * i + 8 * rg + 4 * g;
-        float x[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) x[e] = scale * (oacc[i][4 * rg + e] + qrow_decay * cacc[i][4 * rg + e]);
-        *reinterpret_cast<u32x2*>(orow + dv) = u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
-      }
-    // 7. state update with this chunk.
-    state_update(S, lds, gC, wave, l32, g);
-    __syncthreads();
-    if (ci + 1 < sg.c1) {
-      cur = nxt;
-#pragma unroll
-      for (int j = 0; j < HD / 16; ++j) qf[j] = qn[j];
-    }
-  }
-}
 
-struct RetPlan {
-  int nseg, G;
-};
+  f32x16 S;  // state rows dk = 32 * wave + acc_row(r, g), column dv = l32 of the slice
+#pragma unroll
+  for (int r = 0; r < 16; ++r) S[r] = 0.f;
+  // S fragments in LDS, natural dk order: entry (w, r4, dv) holds bf16
+  // S[32w + 8 r4 + (0..7)][dv]; the owner lane (dv, g) writes its half
+  // S[32w + 8 r4 + 4g + (0..3)] = its accumulator registers 4 r4 .. 4 r4 + 3.
+  char* sf_own = lds + OFF_SF + (wave * 128 + l32) * 16 + g * 8;  // + r4 * 512
+  char* xch = lds + OFF_X + qb * 4096 + lane * 16;
+#pragma unroll
+  for (int r4 = 0; r4 < 4; ++r4) *reinterpret_cast<u32x2*>(sf_own + r4 * 512) = u32x2{0, 0};
 
-RetPlan ret_plan(int64_t B, int64_t H, int64_t T) {
-  const int64_t bh = B * H, nchunks = T / CH;
-  int64_t nseg = (512 + bh - 1) / (bh > 0 ? bh : 1);
-  if (nseg < 1) nseg = 1;
-  if (nseg > nchunks) nseg = nchunks > 0 ? nchunks : 1;
-  int64_t G = (nchunks + nseg - 1) / nseg;
-  if (G < 1) G = 1;
-  nseg = (nchunks + G - 1) / G;
-  if (nseg < 1) nseg = 1;
-  return RetPlan{(int)nseg, (int)G};
+  // Prologue: chunks 0 .. NSTAGE-2 in flight.  Every thread issues exactly
+  // LOADS_PER_CHUNK loads per chunk slot (a slot past the end re-reads the
+  // last chunk into its unused stage), so "all but the newest
+  // (NSTAGE-2) groups complete" is one fixed vmcnt.
+#pragma unroll
+  for (int p = 0; p < NSTAGE - 1; ++p) issue(min(p, nchunks - 1), p);
+  wait_vm_lgkm0<LOADS_PER_CHUNK * (NSTAGE - 2)>();
+  __syncthreads();
+
+  int cur = 0;
+  for (int ci = 0; ci < nchunks; ++ci) {
+    {
+      const int ahead = ci + NSTAGE - 1;
+      const int st = cur == 0 ? NSTAGE - 1 : cur - 1;  // the stage chunk ci - 1 used
+      issue(min(ahead, nchunks - 1), st);
+    }
+    const char* Ks = lds + cur * STAGE;
+    const char* Qs = Ks + KQ_BYTES;
+    const char* Vs = Qs + KQ_BYTES;
+
+    // Reads are issued in batches ahead of the MFMAs that consume them; the
+    // scheduling fences keep the compiler from pairing each MFMA with the reads
+    // right before it, which would expose the LDS latency once per MFMA.
+
+    // ---- batch 1: this thread's piece of v to decay (row tid/4), the S
+    // fragments of dk blocks 2kb, 2kb+1 and the q dims they meet,
+    // 16 (4kb + i) + 8g + e (natural order)
+    const u32x4 vw = *reinterpret_cast<const u32x4*>(Vs + tid * 16);
+    bf16x8 sf[4], qc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sf[i] = *reinterpret_cast<const bf16x8*>(
+          lds + OFF_SF + (((2 * kb + (i >> 1)) * 4 + 2 * (i & 1) + g) * 32 + l32) * 16);
+      qc[i] = *reinterpret_cast<const bf16x8*>(Qs + kq_off(qrow, 2 * (4 * kb + i) + g));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- X = q S over dk half kb (scaled by scale γ^q below)
+    f32x16 X;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) X[r] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) X = mfma32x32x16(sf[i], qc[i], X);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- decayed v for the state update (VALU work beside the MFMAs)
+    {
+      u32x4 d;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        d[e] = pack_bf16x2(__uint_as_float(vw[e] << 16) * vdec,
+                           __uint_as_float(vw[e] & 0xffff0000u) * vdec);
+      *reinterpret_cast<u32x4*>(lds + OFF_VD + tid * 16) = d;
+    }
+    // transposed k rows dk = 32w + l32 for the state update, keys 16u + 4g + (0..3, +8)
+    bf16x8 kt[4];
+    const int dk = 32 * wave + 16 * (G & 1) + 4 * (jj & 3);
+    const int dvb = (16 * (G & 1) + 4 * (jj & 3)) * 2;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int key0 = 16 * u + 4 * (G >> 1) + (jj >> 2);
+      kt[u] = cat8(ds_read_tr(Ks + kq_off(key0, dk >> 3) + (dk & 7) * 2),
+                   ds_read_tr(Ks + kq_off(key0 + 8, dk >> 3) + (dk & 7) * 2));
+    }
+
+    // ---- diagonal block: sᵀ (keys 32kb.., queries 32qb..), decayed, times v
+    if (kb <= qb) {
+      bf16x8 kf[8], qf[8], vi[2];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        kf[j] = *reinterpret_cast<const bf16x8*>(Ks + kq_off(32 * kb + l32, 2 * j + g));
+        qf[j] = *reinterpret_cast<const bf16x8*>(Qs + kq_off(qrow, 2 * j + g));
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {  // vᵀ rows dv = l32, keys 32kb + 16u + 4g + (0..3, +8)
+        const int key0 = 32 * kb + 16 * u + 4 * (G >> 1) + (jj >> 2);
+        vi[u] = cat8(ds_read_tr(Vs + key0 * (SL * 2) + dvb), ds_read_tr(Vs + (key0 + 8) * (SL * 2) + dvb));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) X[r] *= gq;
+      f32x16 acc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+      for (int j = 0; j < HD / 16; ++j) acc = mfma32x32x16(kf[j], qf[j], acc);
+      bf16x8 pf[2];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) pf[r >> 3][r & 7] = static_cast<__bf16>(acc[r] * dec[r]);
+      X = mfma32x32x16(vi[0], pf[0], X);
+      X = mfma32x32x16(vi[1], pf[1], X);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) X[r] *= gq;
+    }
+
+    // ---- pair reduction: waves (1, qb) hand X to waves (0, qb)
+    if (kb == 1) {
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        *reinterpret_cast<f32x4*>(xch + r4 * 1024) =
+            f32x4{X[4 * r4], X[4 * r4 + 1], X[4 * r4 + 2], X[4 * r4 + 3]};
+    }
+    __syncthreads();  // exchange and decayed v written; all S fragments read
+
+    // ---- state update for rows dk = 32 * wave ..: S = γ^C S + kᵀ (decayed v)
+    bf16x8 vd[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int key0 = 16 * u + 4 * (G >> 1) + (jj >> 2);
+      const char* pv = lds + OFF_VD + key0 * (SL * 2) + dvb;
+      vd[u] = cat8(ds_read_tr(pv), ds_read_tr(pv + 8 * SL * 2));
+    }
+    f32x4 y[4];  // partner's X (waves kb = 0)
+    if (kb == 0) {
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) y[r4] = *reinterpret_cast<const f32x4*>(xch + r4 * 1024);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) S[r] *= gC;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) S = mfma32x32x16(kt[u], vd[u], S);
+    u32x2 ow[4];
+    if (kb == 0) {
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        ow[r4] = u32x2{pack_bf16x2(X[4 * r4] + y[r4][0], X[4 * r4 + 1] + y[r4][1]),
+                       pack_bf16x2(X[4 * r4 + 2] + y[r4][2], X[4 * r4 + 3] + y[r4][3])};
+    }
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4)
+      *reinterpret_cast<u32x2*>(sf_own + r4 * 512) =
+          u32x2{pack_bf16x2(S[4 * r4], S[4 * r4 + 1]), pack_bf16x2(S[4 * r4 + 2], S[4 * r4 + 3])};
+    // loads complete in issue order: all but the newest NSTAGE-2 groups means
+    // chunk ci+1's tiles have landed (earlier stores were issued before them)
+    wait_vm_lgkm0<LOADS_PER_CHUNK * (NSTAGE - 2)>();
+    __syncthreads();  // next chunk's tiles and S fragments in place; exchange, decayed v free
+    cur = cur + 1 == NSTAGE ? 0 : cur + 1;
+    if (kb == 0) {
+      // o[ci*C + qrow][sl*32 + 8 r4 + 4g .. +3]
+      uint16_t* orow = o + ((int64_t)ci * CH + qrow) * HD + sl * SL + 4 * g;
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) *reinterpret_cast<u32x2*>(orow + 8 * r4) = ow[r4];
+    }
+  }
 }
 
 }  // namespace
@@ -344,8 +333,7 @@ using namespace catopt;
 extern "C" int64_t catopt_hip_retention_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t d,
                                                         int64_t chunk) {
   if (B < 0 || H < 0 || T < 0 || d != HD || chunk != CH) return -1;
-  const RetPlan p = ret_plan(B, H, T);
-  return B * H * (int64_t)p.nseg * HD * HD * (int64_t)sizeof(float);
+  return 0;  // single pass: the carried state lives in registers
 }
 
 extern "C" int32_t catopt_hip_retention_fwd(int32_t dtype, int64_t B, int64_t H, int64_t T,
@@ -353,42 +341,25 @@ extern "C" int32_t catopt_hip_retention_fwd(int32_t dtype, int64_t B, int64_t H,
                                             const void* v, const float* gamma, float scale, void* o,
                                             void* workspace, int64_t workspace_bytes,
                                             void* stream) {
-  if (B < 0 || H < 0 || T < 0) return CATOPT_E_INVAL;
+  (void)workspace;
+  if (B < 0 || H < 0 || T < 0 || workspace_bytes < 0) return CATOPT_E_INVAL;
   if (dtype != CATOPT_BF16 || d != HD || chunk != CH) return CATOPT_E_UNSUPPORTED;
   if (T % CH != 0) return CATOPT_E_UNSUPPORTED;
   if (B == 0 || H == 0 || T == 0) return CATOPT_OK;
   if (!q || !k || !v || !gamma || !o) return CATOPT_E_INVAL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return CATOPT_E_INVAL;
-  if (B * H > 0x7fffffffLL / 64) return CATOPT_E_UNSUPPORTED;
-  const int64_t need = catopt_hip_retention_workspace_bytes(B, H, T, d, chunk);
-  if (!workspace || workspace_bytes < need) return CATOPT_E_WORKSPACE;
+  if (B * H > 0x7fffffffLL / NSL || T / CH > 0x7fffffffLL) return CATOPT_E_UNSUPPORTED;
   static bool attr_done = false;
   if (!attr_done) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ret_seg_state),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&retention_scan),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ret_seg_out),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
     if (e != hipSuccess) return set_hip_error(e);
     attr_done = true;
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const RetPlan p = ret_plan(B, H, T);
-  const int64_t blocks = B * H * p.nseg;
-  auto qp = static_cast<const uint16_t*>(q);
-  auto kp = static_cast<const uint16_t*>(k);
-  auto vp = static_cast<const uint16_t*>(v);
-  float* ws = static_cast<float*>(workspace);
-  // A single segment starts from the zero state and needs no carry pass.
-  if (p.nseg > 1) {
-    ret_seg_state<<<dim3((uint32_t)blocks), dim3(NT), LDS_BYTES, s>>>(kp, vp, gamma, (int)H, T, p.nseg, p.G, ws);
-    CATOPT_LAUNCH_CHECK();
-    ret_seg_carry<<<dim3(HD * HD / NT, (uint32_t)(B * H)), dim3(NT), 0, s>>>(gamma, (int)H, p.nseg, p.G, ws);
-    CATOPT_LAUNCH_CHECK();
-  }
-  ret_seg_out<<<dim3((uint32_t)blocks), dim3(NT), LDS_BYTES, s>>>(
-      qp, kp, vp, gamma, (int)H, T, p.nseg, p.G, scale, p.nseg > 1 ? 0 : 1, ws,
-      static_cast<uint16_t*>(o));
+  retention_scan<<<dim3((uint32_t)(B * H * NSL)), dim3(NT), LDS_BYTES, s>>>(
+      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+      static_cast<const uint16_t*>(v), gamma, (int)H, T, scale, static_cast<uint16_t*>(o));
   CATOPT_LAUNCH_CHECK();
   return CATOPT_OK;
 }

@@ -175,7 +175,9 @@ int32_t catopt_hip_om_compose(int64_t rows, int64_t dv, const float* m1,
  * carried across chunks (the rank-1 decay_vec factors of the cross blocks,
  * om.py:1075-1089).  q, k, v, o: [B, H, T, d] contiguous, bf16; gamma: [H]
  * fp32; chunk ∈ {64}; d = 128; T a multiple of chunk.
- * Workspace: catopt_hip_retention_workspace_bytes(...) bytes, any contents.
+ * Workspace: catopt_hip_retention_workspace_bytes(...) bytes, any contents
+ * (0 here: one pass whose carried state stays in registers; the query keeps
+ * callers independent of that).  -1 for an unsupported d / chunk.
  */
 int64_t catopt_hip_retention_workspace_bytes(int64_t B, int64_t H, int64_t T,
                                              int64_t d, int64_t chunk);
