@@ -395,8 +395,8 @@ class C4Retention(Form):
     peak = PEAK["hbm_gbs"]
     work = dom_work = 4.0 * B * H * T * Dh * 2  # q, k, v read + o written, bf16
     flops = B * H * (T / C) * (4 * C * C * Dh + 4 * C * Dh * Dh)
-    dom_name = "ret_seg_state + ret_seg_carry + ret_seg_out"
-    dom_key = "retention (3 kernels)"
+    dom_name = "retention_scan"
+    dom_key = "retention_scan"
 
     def setup(self, dev):
         import torch
@@ -453,8 +453,8 @@ class C5SSM(Form):
                 "a_t (B,T,D,N) = exp(-softplus(N(0,1))), b_t,c_t (B,T,N), x_t (B,T,D)")
     peak = PEAK["hbm_gbs"]
     work = dom_work = 4.0 * (B * T * D * N + 2 * B * T * N + 2 * B * T * D)
-    dom_name = "ssm_stream<16,per-state a>"
-    dom_key = "ssm_stream<16, true>"
+    dom_name = "ssm_stream_lds<16>"
+    dom_key = "ssm_stream_lds<16>"
 
     def setup(self, dev):
         import torch
