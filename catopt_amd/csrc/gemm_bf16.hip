@@ -7,15 +7,18 @@
 // are K-contiguous, which is the layout the 32x32x16 MFMA consumes directly
 // (each lane supplies 8 consecutive k of one row/column).
 //
-// Tiling: 256x256 block tile, BK = 64, 4 waves in a 2x2 grid, each wave a
-// 128x128 sub-tile = 4x4 MFMA blocks (256 fp32 accumulators per lane, held
-// in AGPRs; the loop never touches them with VALU).  Tiles reach LDS by
+// Tiling: 256x256 block tile, BK = 64, 8 waves in a 2x4 grid (two per
+// SIMD), each wave a 128x64 sub-tile = 4x2 MFMA blocks.  Tiles reach LDS by
 // direct global->LDS loads (global_load_lds_dwordx4): no register staging,
-// no LDS store instructions.  Two LDS stages (2 x 64 KB): the loads of K
-// tile t+1 are issued before the MFMAs of tile t and waited for after them,
-// one barrier per K tile.  LDS rows are 128 B (64 bf16) with the 16-byte
-// chunk index XOR-swizzled by (row & 7), so the MFMA fragment reads (eight
-// consecutive rows, one chunk) hit eight different bank groups.
+// no LDS store instructions.  A ring of LDS stages (two of 64 KB): the loads
+// of K tile t+1 are issued before the MFMAs of tile t, one barrier per K
+// tile.  Within a tile the fragments of k-step s+1 are read before the MFMAs
+// of k-step s, and the last k-step's MFMAs are issued after the barrier,
+// behind the next tile's first reads.  (Measured on MI355X: shallower K
+// tiles with a deeper ring lose more to the extra barriers than they gain
+// in loads in flight; 128x128 wave tiles at one wave per SIMD lose to the
+// two-waves-per-SIMD layout.)  The 16-byte chunk index of each LDS row is
+// XOR-swizzled so a fragment read's 16 rows per pass hit 16 bank groups.
 //
 // Edges: rows past M (A) or N (B) load a clamped, valid row and are never
 // stored; a K tail (K % 64 != 0, K % 8 == 0) loads clamped chunks and then
@@ -36,7 +39,14 @@
 namespace catopt {
 namespace {
 
-constexpr int BM = 256, BN = 256, BK = 64;
+#ifndef CATOPT_GEMM_BK
+#define CATOPT_GEMM_BK 64
+#endif
+#ifndef CATOPT_GEMM_STAGES
+#define CATOPT_GEMM_STAGES 2
+#endif
+constexpr int BM = 256, BN = 256, BK = CATOPT_GEMM_BK;
+constexpr int NSTAGE = CATOPT_GEMM_STAGES;
 #ifndef CATOPT_GEMM_NWN
 #define CATOPT_GEMM_NWN 4
 #endif
@@ -44,15 +54,31 @@ constexpr int NWN = CATOPT_GEMM_NWN;    // waves along N (2 along M)
 constexpr int NT = 128 * NWN;           // threads per block
 constexpr int WCOLS = BN / NWN;         // output columns per wave (B rows)
 constexpr int TJ = WCOLS / 32;          // 32-wide MFMA blocks per wave along N
-constexpr int TILE_BYTES = BM * BK * 2;                 // one operand tile (A or B), 32 KB
+constexpr int CPR = BK / 8;             // 16-byte chunks per tile row
+constexpr int RPB = 256 / (BK * 2);     // tile rows per 256 bytes (one pass of the LDS banks)
+constexpr int TILE_BYTES = BM * BK * 2;                 // one operand tile (A or B)
 constexpr int STAGE_BYTES = 2 * TILE_BYTES;             // A then B
-constexpr int LDS_BYTES = 2 * STAGE_BYTES;              // two stages, 128 KB
-constexpr int SLOTS_PER_THREAD = (BM * BK / 8) / NT;    // 16-byte slots per thread per operand: 8
+constexpr int LDS_BYTES = NSTAGE * STAGE_BYTES;
+constexpr int SLOTS_PER_THREAD = (BM * BK / 8) / NT;    // 16-byte slots per thread per operand
+static_assert(SLOTS_PER_THREAD >= 1 && (BM * BK / 8) % NT == 0, "tile / thread mismatch");
+static_assert(NSTAGE >= 2 && LDS_BYTES <= 160 * 1024, "LDS ring does not fit");
+static_assert(BK % 16 == 0 && RPB >= 1 && CPR * RPB == 16, "row geometry");
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
+// The 16-byte chunk index is XOR-swizzled by the row's position among the 16
+// consecutive rows that one 16-lane pass of a fragment read touches, so those
+// 16 rows land on 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int chunk_swizzle(int row) { return (row / RPB) % CPR; }
 __device__ __forceinline__ int swz(int row, int chunk) {  // byte offset of (row, chunk) in a tile
-  return row * (BK * 2) + ((chunk ^ (row & 7)) << 4);
+  return row * (BK * 2) + ((chunk ^ chunk_swizzle(row)) << 4);
+}
+
+// s_waitcnt: vmcnt <= n, lgkmcnt = 0, expcnt not waited on (gfx9 encoding).
+template <int n>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(n >= 0 && n < 64, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | ((n >> 4) << 14));
 }
 
 struct TileMap {
@@ -107,8 +133,8 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_nt(
 #pragma unroll
   for (int i = 0; i < SLOTS_PER_THREAD; ++i) {
     const int s = i * NT + wave * 64 + lane;
-    const int r = s >> 3, cp = s & 7;
-    const int chunk = cp ^ (r & 7);
+    const int r = s / CPR, cp = s % CPR;
+    const int chunk = cp ^ chunk_swizzle(r);
     s_chunk[i] = chunk;
     const int am = min(m0 + r, M - 1);
     int bn;
@@ -142,10 +168,10 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_nt(
   auto zero_k_tail = [&](int kt, int stage) {
     const int k0 = kt * BK;
     char* sa = lds + stage * STAGE_BYTES;
-    for (int s = tid; s < 2 * BM * 8; s += NT) {
-      const int t = s >> 11, rem = s & 2047;  // operand, slot
-      const int r = rem >> 3, cp = rem & 7;
-      const int chunk = cp ^ (r & 7);
+    for (int s = tid; s < 2 * BM * CPR; s += NT) {
+      const int t = s / (BM * CPR), rem = s % (BM * CPR);  // operand, slot
+      const int r = rem / CPR, cp = rem % CPR;
+      const int chunk = cp ^ chunk_swizzle(r);
       if (k0 + chunk * 8 >= K) *reinterpret_cast<u32x4*>(sa + t * TILE_BYTES + rem * 16) = u32x4{0, 0, 0, 0};
     }
   };
@@ -164,43 +190,77 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_nt(
     return PAIRED ? (j / (TJ / 2)) * 128 + wn * (WCOLS / 2) + (j % (TJ / 2)) * 32 : wn * WCOLS + j * 32;
   };
 
-  issue(0, 0);
-  __builtin_amdgcn_s_waitcnt(0);
+  // Prologue: tiles 0 .. NSTAGE-2 in flight.  Every thread issues the same
+  // number of loads per tile slot (slots past the last tile reload it into a
+  // stage nobody reads), so "all but the newest NSTAGE-2 tiles landed" is
+  // one fixed vmcnt.
+  constexpr int LOADS_PER_TILE = 2 * SLOTS_PER_THREAD;
+#pragma unroll
+  for (int p = 0; p < NSTAGE - 1; ++p) issue(min(p, ktiles - 1), p);
+  wait_vm_lgkm0<LOADS_PER_TILE * (NSTAGE - 2)>();
   __syncthreads();
   if (k_tail && ktiles == 1) {
     zero_k_tail(0, 0);
     __syncthreads();
   }
 
-  for (int kt = 0; kt < ktiles; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < ktiles) issue(kt + 1, cur ^ 1);
-    const char* As = lds + cur * STAGE_BYTES;
+  // Fragment registers: two sets, k-step ks of a tile uses set ks & 1.  The
+  // fragments of k-step ks+1 are read before the MFMAs of k-step ks are
+  // issued, and the last k-step's MFMAs are issued after the barrier that
+  // publishes the next tile, behind that tile's first fragment reads, so the
+  // matrix cores keep working across the barrier.
+  constexpr int KS = BK / 16;
+  static_assert(KS % 2 == 0, "the k-step register sets alternate within a tile");
+  bf16x8 af[2][4], bfr[2][TJ];
+  auto read_frags = [&](int stage, int ks, int set) {
+    const char* As = lds + stage * STAGE_BYTES;
     const char* Bs = As + TILE_BYTES;
+    const int chunk = 2 * ks + g;
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      bf16x8 af[4], bfr[TJ];
-      const int chunk = 2 * ks + g;
+    for (int i = 0; i < 4; ++i)
+      af[set][i] = *reinterpret_cast<const bf16x8*>(As + swz(wm * 128 + i * 32 + l32, chunk));
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        af[i] = *reinterpret_cast<const bf16x8*>(As + swz(wm * 128 + i * 32 + l32, chunk));
+    for (int j = 0; j < TJ; ++j)
+      bfr[set][j] = *reinterpret_cast<const bf16x8*>(Bs + swz(brow(j) + l32, chunk));
+  };
+  auto mfmas = [&](int set) {
 #pragma unroll
-      for (int j = 0; j < TJ; ++j)
-        bfr[j] = *reinterpret_cast<const bf16x8*>(Bs + swz(brow(j) + l32, chunk));
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int j = 0; j < TJ; ++j) acc[i][j] = mfma32x32x16(af[set][i], bfr[set][j], acc[i][j]);
+  };
+
+  read_frags(0, 0, 0);
+  int cur = 0;
+  for (int kt = 0; kt < ktiles; ++kt) {
+    // the stage tile kt-1 used receives tile kt + NSTAGE - 1 (its last reads
+    // happened before the barrier that ended iteration kt-1)
+    issue(min(kt + NSTAGE - 1, ktiles - 1), cur == 0 ? NSTAGE - 1 : cur - 1);
+    const int nxt = cur + 1 == NSTAGE ? 0 : cur + 1;
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) acc[i][j] = mfma32x32x16(af[i], bfr[j], acc[i][j]);
+    for (int ks = 0; ks + 1 < KS; ++ks) {
+      read_frags(cur, ks + 1, (ks + 1) & 1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(ks & 1);
+      __builtin_amdgcn_sched_barrier(0);
     }
     if (kt + 1 < ktiles) {
-      __builtin_amdgcn_s_waitcnt(0);
+      // loads land in issue order: all but the newest NSTAGE-2 tiles means
+      // tile kt+1 is in place
+      wait_vm_lgkm0<LOADS_PER_TILE * (NSTAGE - 2)>();
       __syncthreads();
       if (k_tail && kt + 2 == ktiles) {
-        zero_k_tail(kt + 1, cur ^ 1);
+        zero_k_tail(kt + 1, nxt);
         __syncthreads();
       }
+      read_frags(nxt, 0, 0);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas((KS - 1) & 1);
+    __builtin_amdgcn_sched_barrier(0);
+    cur = nxt;
   }
+  __builtin_amdgcn_s_waitcnt(0);  // drain the reloads past the last tile
 
   // Epilogue: lane owns output column (l32) of each 32-wide block and 16 rows.
   if (PAIRED) {
