@@ -23,9 +23,9 @@
 // fragment feeding two MFMAs) needs AGPRs and measured 1.33x slower, from
 // accumulator copies between the register files.  Waves raise their
 // priority around the MFMA blocks.  KV tiles of 64 keys are double buffered in LDS and
-// filled by direct global->LDS loads (global_load_lds_dwordx4: no register
-// staging); K and V rows are 256 bytes with the 16-byte chunk index
-// XOR-swizzled by (key & 15).  A partial last tile zero-fills its missing V
+// filled by direct global->LDS loads (dma16: no register
+// staging); K rows are 256 bytes with the 16-byte chunk index XOR-swizzled
+// by (key & 15), V rows with the transposing-read swizzle below.  A partial last tile zero-fills its missing V
 // rows.  Causal grids launch the longest query tiles first, skip tiles past
 // each wave's last key and apply the mask only on diagonal tiles.
 //
@@ -47,7 +47,6 @@ constexpr int KVB = 64;   // keys per KV tile
 constexpr float kLazy = 8.0f;
 
 typedef __attribute__((ext_vector_type(4))) short s16x4;
-typedef __attribute__((address_space(3))) void* lds_ptr;
 
 template <int D>
 struct AttnLds {
@@ -64,6 +63,21 @@ struct AttnLds {
 template <int D>
 __device__ __forceinline__ int tile_off(int key, int chunk) {
   return key * AttnLds<D>::ROW_BYTES + ((chunk ^ (key & (AttnLds<D>::CH - 1) & 15)) << 4);
+}
+
+// V tiles use their own swizzle.  A transposing read of Vᵀ covers, per
+// 32-lane pass, 4 consecutive keys x 4 adjacent 16-byte chunks; XOR-ing the
+// chunk index with 4 * (the key's position among those 4, per 256-byte bank
+// window) puts the 16 pieces in 16 different bank groups (the key-row
+// swizzle above would put all 4 keys on the same 4 groups).
+template <int D>
+__device__ __forceinline__ int vswz(int key) {
+  constexpr int R = 256 / AttnLds<D>::ROW_BYTES;  // tile rows per 256-byte bank window
+  return 4 * ((key / R) & (4 / R - 1));
+}
+template <int D>
+__device__ __forceinline__ int vtile_off(int key, int chunk) {
+  return key * AttnLds<D>::ROW_BYTES + ((chunk ^ vswz<D>(key)) << 4);
 }
 
 __device__ __forceinline__ s16x4 ds_read_tr(const char* lds_base, int byte_off) {
@@ -151,16 +165,18 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
   // takes the arrays for variable-length ones and silently drops the
   // kernel's launch stub; 4 = SLOTS_PER_THREAD at D = 128, the largest)
   static_assert(AttnLds<D>::SLOTS_PER_THREAD <= 4, "slot arrays hold 4 entries");
-  int t_row[4], t_koff[4], t_voff[4], t_chunk8[4];
+  int t_row[4], t_koff[4], t_voff[4], t_chunk8[4], t_vchunk8[4];
 #pragma unroll
   for (int i = 0; i < L::SLOTS_PER_THREAD; ++i) {
     const int s = i * NT + wave * 64 + lane;
     const int row = s / L::CH, cp = s % L::CH;
     const int chunk = cp ^ (row & (L::CH - 1) & 15);
+    const int vchunk = cp ^ vswz<D>(row);
     t_row[i] = row;
     t_chunk8[i] = chunk * 8;
+    t_vchunk8[i] = vchunk * 8;
     t_koff[i] = row * (int)kst + chunk * 8;
-    t_voff[i] = row * (int)vst + chunk * 8;
+    t_voff[i] = row * (int)vst + vchunk * 8;
   }
   auto issue_tile = [&](int kvt, int stage) {
     const int kv0 = kvt * KVB;
@@ -170,19 +186,18 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
     if (kv0 + KVB <= Tk) {
 #pragma unroll
       for (int i = 0; i < L::SLOTS_PER_THREAD; ++i) {
-        char* dst = kst_base + (i * NT + wave * 64) * 16;
-        __builtin_amdgcn_global_load_lds(kt + t_koff[i], (lds_ptr)dst, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vt + t_voff[i], (lds_ptr)(dst + L::TILE_BYTES), 16, 0, 0);
+        const uint32_t dst = lds_u32(kst_base) + (i * NT + wave * 64) * 16;
+        dma16(kt + t_koff[i], dst);
+        dma16(vt + t_voff[i], dst + L::TILE_BYTES);
       }
     } else {
 #pragma unroll
       for (int i = 0; i < L::SLOTS_PER_THREAD; ++i) {
         int gk = kv0 + t_row[i];
         gk = gk < Tk ? gk : Tk - 1;
-        char* dst = kst_base + (i * NT + wave * 64) * 16;
-        __builtin_amdgcn_global_load_lds(k + (int64_t)gk * kst + t_chunk8[i], (lds_ptr)dst, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(v + (int64_t)gk * vst + t_chunk8[i], (lds_ptr)(dst + L::TILE_BYTES),
-                                         16, 0, 0);
+        const uint32_t dst = lds_u32(kst_base) + (i * NT + wave * 64) * 16;
+        dma16(k + (int64_t)gk * kst + t_chunk8[i], dst);
+        dma16(v + (int64_t)gk * vst + t_vchunk8[i], dst + L::TILE_BYTES);
       }
     }
   };
@@ -315,8 +330,8 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
             const int key0 = 32 * kb + 16 * u + 4 * (G >> 1) + (jj >> 2);
             const int d = 32 * db + 16 * (G & 1) + 4 * (jj & 3);
             const int chunk = d >> 3, half = (d & 7) * 2;
-            const s16x4 lo = ds_read_tr(Vs, tile_off<D>(key0, chunk) + half);
-            const s16x4 hi = ds_read_tr(Vs, tile_off<D>(key0 + 8, chunk) + half);
+            const s16x4 lo = ds_read_tr(Vs, vtile_off<D>(key0, chunk) + half);
+            const s16x4 hi = ds_read_tr(Vs, vtile_off<D>(key0 + 8, chunk) + half);
             const bf16x8 a = __builtin_bit_cast(
                 bf16x8, u32x4{__builtin_bit_cast(u32x2, lo)[0], __builtin_bit_cast(u32x2, lo)[1],
                               __builtin_bit_cast(u32x2, hi)[0], __builtin_bit_cast(u32x2, hi)[1]});

@@ -81,4 +81,22 @@ __device__ __forceinline__ constexpr int acc_row(int r, int g) {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// LDS byte address of a pointer into dynamic shared memory.
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
+}
+
+// Direct global->LDS load of 16 bytes per lane: lane l's bytes land at LDS
+// byte address lds_wave + 16 l (lds_wave is wave-uniform; it goes to M0).
+// Issued as inline asm: for the builtin form the compiler treats every later
+// transposing LDS read (ds_read_b64_tr_b16) as a possible reader of the load
+// and waits for all loads in flight before it, which serialises a prefetch
+// with the tile being computed.  Callers wait with s_waitcnt vmcnt before
+// the barrier that publishes the loaded stage.
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_wave) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_wave)
+               : "m0");
+}
+
 }  // namespace catopt

@@ -78,22 +78,6 @@ __device__ __forceinline__ int kq_off(int row, int chunk) {  // byte offset in a
   return row * (HD * 2) + ((chunk ^ (row & 15)) << 4);
 }
 
-// Direct global->LDS load of 16 bytes per lane: lane l's bytes land at LDS
-// byte address lds_wave + 16 l (lds_wave is wave-uniform, it goes to M0).
-// Issued as inline asm so that the compiler does not treat every later LDS
-// read as a possible reader of this load (it would wait for all loads in
-// flight before each transposing read); completion is awaited explicitly
-// with s_waitcnt vmcnt before the workgroup barrier that publishes a stage.
-__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_wave) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_wave)
-               : "m0");
-}
-
-__device__ __forceinline__ uint32_t lds_u32(const void* p) {
-  return static_cast<uint32_t>(
-      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
-}
-
 // Transposing LDS read (ds_read_b64_tr_b16).  Within each 16-lane group, when
 // lane j points at row (base + j/4), columns c0 + 4(j%4) .. +3, lane i gets
 // column c0 + i of rows base .. base+3.
