@@ -47,7 +47,7 @@ from ..evaluator import HipIRModule
 from ..ir import IR, is_op
 from .base import HipExecutorBase
 
-__all__ = ["HipOMModule", "build_om_plan", "is_om_term", "om_leaves", "parse_score"]
+__all__ = ["HipOMModule", "build_om_plan", "is_om_term", "mask_kwargs", "om_leaves", "parse_score"]
 
 
 def is_om_term(term: Any) -> bool:
@@ -215,20 +215,26 @@ class HipOMModule(HipExecutorBase, nn.Module):
         return out.reshape(*lead, out.shape[-2], out.shape[-1])
 
     def _mask_kwargs(self, lf: dict, ev) -> dict | None:
-        kind = lf["mask_kind"]
-        if kind == "none":
-            return {}
-        if kind == "causal":
-            return {"causal": True, "causal_off": lf["causal_off"]}
-        if kind == "bool_const":
-            return {"mask": lf["keep"]}
-        masked = ev(lf["mask"])
-        if not isinstance(masked, torch.Tensor) or masked.dim() < 2:
-            return None
-        m2 = masked.reshape(-1, *masked.shape[-2:])
-        if m2.shape[0] != 1:
-            return None
-        return {"mask": torch.logical_not(m2[0].to(torch.bool))}
+        return mask_kwargs(lf, ev)
+
+
+def mask_kwargs(lf: dict, ev) -> dict | None:
+    """Attention-kernel mask arguments of a parsed leaf; ``None`` when a
+    runtime mask is not a single ``(Tq, Tk)`` plane shared over (B, H)."""
+    kind = lf["mask_kind"]
+    if kind == "none":
+        return {}
+    if kind == "causal":
+        return {"causal": True, "causal_off": lf["causal_off"]}
+    if kind == "bool_const":
+        return {"mask": lf["keep"]}
+    masked = ev(lf["mask"])
+    if not isinstance(masked, torch.Tensor) or masked.dim() < 2:
+        return None
+    m2 = masked.reshape(-1, *masked.shape[-2:])
+    if m2.shape[0] != 1:
+        return None
+    return {"mask": torch.logical_not(m2[0].to(torch.bool))}
 
 
 def _in_envelope(q, k, v) -> bool:

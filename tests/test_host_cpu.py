@@ -340,3 +340,39 @@ def test_sink_surface_routing_and_verify():
     rep = verify_equiv(ref, torch.tensor([1.0, float("nan")]))
     assert not rep.passed
     assert math.isclose(verify_equiv(ref, torch.tensor([1.0, -2.1])).max_rel, 0.1 / (2 + 1e-8), rel_tol=1e-6)
+
+
+# ------------------------------------------------------------------ streaming om plan
+
+
+def test_streaming_plan_leaf_kinds_and_fold_order():
+    from catopt_amd.executors import HipStreamingOMModule, om_empty_state
+
+    q = Var("q", TensorType((1, 2, 8, 64)))
+    ks = [Var(f"k{i}", TensorType((1, 2, 4, 64))) for i in range(3)]
+    vs = [Var(f"v{i}", TensorType((1, 2, 4, 64))) for i in range(3)]
+    s_raw = Var("s", TensorType((1, 2, 8, 4)))
+    m, lv, a = (Var(n, TensorType((1, 2, 8, d))) for n, d in (("m", 1), ("l", 1), ("a", 64)))
+
+    def qk(i):
+        return mk("om_elem", mk("mul", mk("matmul", q, mk("transpose", ks[i], dim0=-2, dim1=-1)), Const(0.125)),
+                  vs[i])
+
+    # left-leaning tree mixing all three leaf kinds; a DAG-shared leaf counts twice
+    shared = qk(1)
+    tree = mk("om_compose", mk("om_compose", mk("om_compose", qk(0), shared),
+                               mk("om_elem", s_raw, vs[2])), mk("om_compose", mk("om", m, lv, a), shared))
+    ir = IR(mk("om_apply", tree), [q, *ks, *vs, s_raw, m, lv, a])
+    mod = HipStreamingOMModule(ir, ops=cpu_table())
+    assert mod.is_streaming and mod.n_blocks == 5
+    kinds = [lf["kind"] for lf in mod._plan["leaves"]]
+    assert kinds == ["qk", "qk", "elem", "om", "qk"]
+    assert [lf["scale"] for lf in mod._plan["leaves"] if lf["kind"] == "qk"] == [0.125] * 3
+    assert mod._plan["leaves"][1]["k"] is ks[1] and mod._plan["leaves"][4]["k"] is ks[1]
+    # a root that is not om_apply over an om tree: not streaming
+    assert not HipStreamingOMModule(IR(mk("relu", q), [q]), ops=cpu_table()).is_streaming
+    bad = mk("om_apply", mk("om_compose", qk(0), mk("relu", s_raw)))
+    assert not HipStreamingOMModule(IR(bad, [q, ks[0], vs[0], s_raw]), ops=cpu_table()).is_streaming
+    e_m, e_l, e_a = om_empty_state((2, 3), 5, dtype=torch.float64)
+    assert e_m.shape == (2, 3, 1) and e_a.shape == (2, 3, 5) and e_m.dtype == torch.float64
+    assert torch.isneginf(e_m).all() and not e_l.any() and not e_a.any()
