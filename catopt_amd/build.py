@@ -48,6 +48,9 @@ HIPCC_FLAGS = [
 ]
 
 
+# hipBLASLt runs the plain (epilogue-free) bf16 GEMMs; the fused ones are ours.
+LINK_LIBS = ["-lhipblaslt"]
+
 SOURCE_FLAGS = {
     "retention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
@@ -86,7 +89,7 @@ def build(verbose: bool = False, jobs: int | None = None, extra: list[str] | Non
             if verbose and log.strip():
                 print(log, file=sys.stderr)
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs), *LINK_LIBS]
     p = subprocess.run(cmd, capture_output=True, text=True)
     if p.returncode != 0:
         raise RuntimeError(f"link failed:\n{p.stdout}\n{p.stderr}")

@@ -93,6 +93,10 @@ int32_t catopt_hip_rmsnorm(int32_t dtype, int64_t rows, int64_t cols,
  * two projections, first half then second half).  bias / bias2 are [N]
  * vectors of `dtype` (NULL unless the epilogue reads them).  fp32
  * accumulation.  bf16 runs on 32x32x16 bf16 MFMA; fp32 on 32x32x2 fp32 MFMA.
+ * A bf16 call with CATOPT_EPI_NONE and M·N·K >= 2^30 (a plain library GEMM)
+ * runs hipBLASLt (first heuristic algorithm needing no workspace, cached per
+ * shape), falling back to the kernel above if hipBLASLt declines;
+ * CATOPT_HIP_NO_BLASLT=1 in the environment disables that route.
  * Replaces the "linear" binding (torch_bridge.py:1251-1253), the bias adds
  * of the ASSOC_LINEAR_BIAS RHS (laws/tensor.py:1374-1394), and the
  * chunk/silu/mul (or glu) bindings of the SWIGLU_FUSE / GLU_FOLD RHS
