@@ -234,6 +234,12 @@ HIP_BINDINGS: dict[str, Callable] = {
     "applyd": lambda f, h, *a, **kw: f[0] * h + f[1],
     "affd_a": lambda f, *a, **kw: f[0],
     "affd_b": lambda f, *a, **kw: f[1],
+    # ---- dense affine monoid (torch_bridge.py:1873-1881, xcarrier.py:460-472)
+    "aff": lambda A, b_, *x, **kw: (A, b_),
+    "aff_compose": lambda f, g, *a, **kw: (_matmul(f[0], g[0]), _matmul(f[0], g[1]) + f[1]),
+    "apply": lambda f, h, *a, **kw: _matmul(f[0], h) + f[1],
+    "aff_A": lambda f, *a, **kw: f[0],
+    "aff_b": lambda f, *a, **kw: f[1],
     # ---- elementwise / reductions (device ops)
     "add": lambda x, y, *a, **kw: torch.add(x, y),
     "sub": lambda x, y, *a, **kw: torch.sub(x, y),

@@ -1,37 +1,57 @@
-"""Diagonal-affine scan executor on the HIP scan kernels.
+"""Affine scan executor (diagonal and dense monoids) on the HIP scan kernels.
 
 The counterpart of ``BatchedScanModule`` (luisfuturist/catopt
 ``packages/catopt-carriers/src/catopt_carriers/scan_lower.py:427-807``,
 ``build_scan_plan`` :339-424) and of the fused level bodies
-``fused_diag_levels`` (``scan_fused.py:100-120``) for the diagonal-affine
-monoid (bindings ``aff_diag`` / ``affd_compose`` / ``applyd``,
-``torch_bridge.py:1895-1900``: ``compose(f, g) = (f.a·g.a, f.a·g.b + f.b)``,
-``g`` applied first).  Two roots are planned:
+``fused_diag_levels`` / ``fused_dense_levels`` (``scan_fused.py:100-143``)
+for both affine carriers:
 
-* **final state** — ``applyd(F, h)`` with ``F`` an ``affd_compose`` tree over
-  ``aff_diag(a_i, u_i)`` leaves.  Leaves are read in product order (leaf 0
-  is the outermost map, applied last; ``tests/test_scan_fused.py:105-107``),
-  so time runs over the reversed leaf list;
-* **every prefix state** — the stacked-map form of ``gather_applyd_stack``
-  (``xcarrier.py:2252-2273``):
-  ``applyd(aff_diag(stack(affd_a f_0 … f_n), stack(affd_b f_0 … f_n)), h)``
-  where each ``f_i = affd_compose(leaf_i, f_{i-1})`` extends the previous
-  prefix by one step (checked structurally, not assumed).
+* diagonal — ``aff_diag`` / ``affd_compose`` / ``applyd``
+  (``torch_bridge.py:1895-1900``): ``compose(f, g) = (f.a·g.a, f.a·g.b + f.b)``;
+* dense — ``aff`` / ``aff_compose`` / ``apply`` (``torch_bridge.py:1873-1881``):
+  ``compose(f, g) = (f.A @ g.A, f.A @ g.b + f.b)``, ``apply(f, h) = f.A @ h + f.b``;
 
-Instead of ``log₂ T`` levels of gathers and pointwise launches
-(``scan_lower.py:652-674``), the leaf operands are laid out as ``(T, S)``
-arrays and one kernel walks the steps: lane-parallel over the state, serial
-over time in registers, or chunk-parallel (local chunk maps, a carry fold
-over the chunk table, a re-scan) when the state is too small to fill the
-GPU.  The chunk table is the reference's blocked all-prefix plan
+``g`` is applied first.  Two roots are planned per carrier:
+
+* **final state** — ``apply[d](F, h)`` with ``F`` a compose tree over the
+  carrier's leaves.  Leaves are read in product order (leaf 0 is the
+  outermost map, applied last; ``tests/test_scan_fused.py:105-107``), so time
+  runs over the reversed leaf list;
+* **every prefix state** — the stacked-map form of ``gather_applyd_stack`` /
+  ``gather_apply_stack`` (``xcarrier.py:2252-2293``):
+  ``apply[d](pack(stack(proj_a f_0 … f_n), stack(proj_b f_0 … f_n)), h)``
+  where each ``f_i = compose(leaf_i, f_{i-1})`` extends the previous prefix by
+  one step (checked structurally, not assumed).
+
+As in the reference's plan builder, nested applications are folded into the
+compose spine first (``apply(f, apply(g, h)) → apply(compose(f, g), h)``,
+``scan_lower.py:131-165``) and pure view wrappers around the root are peeled
+off and re-applied to the result (``scan_lower.py:74-118``).
+
+Instead of ``log₂ T`` levels of gathers and batched products
+(``scan_lower.py:640-698``), the leaf operands are laid out as step-major
+arrays and one kernel walks the steps:
+
+* diagonal: lane-parallel over the state, serial over time in registers, or
+  chunk-parallel (local chunk maps, a carry fold over the chunk table, a
+  re-scan) when the state is too small to fill the GPU;
+* dense: the state columns are batched into fp32 MFMA tiles; a map shared by
+  every slot (the LTI ``LinearRecurrence`` case) makes each step one product
+  over all ``P·k`` columns, per-slot maps stream from HBM.  The same
+  chunk-parallel schedule composes dense chunk maps from the identity.
+
+The chunk table is the reference's blocked all-prefix plan
 (``omd_lower.py:771-824``: ``blk = ⌈√T⌉``, starts ``c·blk``) as an int64
-array.  When every leaf reads step ``t`` of one shared array
-(``select(X, dim, t)`` / ``getitem(X, t)``), that array is used in place
-instead of stacking ``T`` slices.
+array.  When every leaf reads a step of one shared array (``select(X, dim,
+t)`` / ``getitem(X, t)``), that array is used in place (or gathered once with
+``index_select``) instead of stacking ``T`` slices, and a linear part that is
+the same term in every leaf is evaluated once.
 
 The kernels compute in fp32: bf16/fp32 operands run on them (results cast
-back to the operand dtype); fp64 and host operands run the embedded generic
-module, counted in ``fallbacks``.
+back to the promoted operand dtype); fp64 and host operands, dense maps with
+``d > 64`` and operand shapes outside the two supported dense layouts (vector
+state ``h (d,)`` with ``b (d,)``; column state ``h (…, d, k)`` with
+``b (…, d, 1)``) run the embedded generic module, counted in ``fallbacks``.
 """
 
 from __future__ import annotations
@@ -46,10 +66,37 @@ from .. import _lib as L
 from .. import kernels as K
 from ..bindings import attr_of
 from ..evaluator import HipIRModule
-from ..ir import IR, is_op
+from ..ir import IR, Op, is_op
 from .base import HipExecutorBase
 
-__all__ = ["HipScanModule", "build_scan_plan", "is_scan_term", "prefix_chunk_table", "affd_leaves"]
+__all__ = [
+    "HipScanModule",
+    "build_scan_plan",
+    "is_scan_term",
+    "prefix_chunk_table",
+    "affd_leaves",
+    "map_leaves",
+    "fold_nested_apply",
+    "strip_output_views",
+]
+
+#: per root op: (leaf op, compose op, linear-part projection, offset projection, domain)
+_CARRIERS = {
+    "applyd": ("aff_diag", "affd_compose", "affd_a", "affd_b", "diag"),
+    "apply": ("aff", "aff_compose", "aff_A", "aff_b", "dense"),
+}
+
+#: Single-argument view / bookkeeping ops the plan is transparent to around
+#: the root (the set of ``scan_lower.py:74-104``): the executor re-applies
+#: them, innermost first, to the scan result.
+VIEW_OPS = frozenset({
+    "reshape", "view", "flatten", "unflatten", "squeeze", "unsqueeze", "expand", "broadcast_to",
+    "contiguous", "clone", "detach", "to", "alias", "transpose", "permute", "movedim", "t",
+    "select", "getitem", "slice", "chunk", "split", "unbind",
+})
+
+#: widest dense state the MFMA kernel holds in registers
+DENSE_MAX_D = 64
 
 
 def prefix_chunk_table(T: int) -> list[int]:
@@ -62,32 +109,79 @@ def prefix_chunk_table(T: int) -> list[int]:
     return [c * blk for c in range(C)] + [T]
 
 
-def affd_leaves(F: Any) -> list | None:
-    """``aff_diag`` leaves of an ``affd_compose`` tree in product order."""
+def map_leaves(F: Any, leaf_op: str, compose_op: str) -> list | None:
+    """Leaves of a ``compose_op`` tree in product order, with multiplicity
+    (a DAG-shared subtree contributes once per occurrence)."""
     out: list = []
     stack = [F]
     while stack:
         n = stack.pop()
-        if is_op(n, "affd_compose", 2):
+        if is_op(n, compose_op, 2):
             stack.append(n.args[1])
             stack.append(n.args[0])
-        elif is_op(n, "aff_diag", 2):
+        elif is_op(n, leaf_op, 2):
             out.append(n)
         else:
             return None
     return out
 
 
-def _prefix_chain(fs: list) -> list | None:
-    """Time-ordered leaves when ``fs[i] = affd_compose(leaf_i, fs[i-1])``."""
-    if not fs or not is_op(fs[0], "aff_diag", 2):
+def affd_leaves(F: Any) -> list | None:
+    """``aff_diag`` leaves of an ``affd_compose`` tree in product order."""
+    return map_leaves(F, "aff_diag", "affd_compose")
+
+
+def fold_nested_apply(term: Any) -> Any:
+    """``apply(f, apply(g, h)) → apply(compose(f, g), h)`` (and the diagonal
+    pair), bottom-up and memoised: one compose tree per application chain
+    (``scan_lower.py:131-165``).  Composition is sequential application, so
+    the value is unchanged."""
+    memo: dict[int, Any] = {}
+
+    def go(t: Any) -> Any:
+        if not isinstance(t, Op):
+            return t
+        key = id(t)
+        if key in memo:
+            return memo[key]
+        args = [go(a) for a in t.args]
+        r = t if all(a is b for a, b in zip(args, t.args)) else Op.make(t.op, *args, **dict(t.attrs))
+        if r.op in _CARRIERS and len(r.args) == 2:
+            comp = _CARRIERS[r.op][1]
+            f, h = r.args
+            folded = False
+            while is_op(h, r.op, 2):
+                f = Op.make(comp, f, h.args[0])
+                h = h.args[1]
+                folded = True
+            if folded:
+                r = Op.make(r.op, f, h)
+        memo[key] = r
+        return r
+
+    return go(term)
+
+
+def strip_output_views(root: Any) -> tuple[Any, list]:
+    """Peel single-argument view ops off the root: ``(inner, post)`` with
+    ``post`` the ``(op, attrs)`` wrappers outermost first."""
+    post: list = []
+    while isinstance(root, Op) and root.op in VIEW_OPS and len(root.args) == 1:
+        post.append((root.op, dict(root.attrs)))
+        root = root.args[0]
+    return root, post
+
+
+def _prefix_chain(fs: list, leaf_op: str, compose_op: str) -> list | None:
+    """Time-ordered leaves when ``fs[i] = compose(leaf_i, fs[i-1])``."""
+    if not fs or not is_op(fs[0], leaf_op, 2):
         return None
     leaves = [fs[0]]
     for i in range(1, len(fs)):
         f = fs[i]
-        if not is_op(f, "affd_compose", 2) or f.args[1] is not fs[i - 1] and f.args[1] != fs[i - 1]:
+        if not is_op(f, compose_op, 2) or f.args[1] is not fs[i - 1] and f.args[1] != fs[i - 1]:
             return None
-        if not is_op(f.args[0], "aff_diag", 2):
+        if not is_op(f.args[0], leaf_op, 2):
             return None
         leaves.append(f.args[0])
     return leaves
@@ -105,28 +199,60 @@ def _proj_list(t: Any, proj: str) -> tuple | None:
     return fs, int(attr_of(t.attrs, "dim", default=0))
 
 
+def _compose_levels(F: Any, compose_op: str) -> int:
+    """Depth of the compose tree: the number of dependent compose levels
+    (``levels`` of the reference plan, ``scan_lower.py:376-385``)."""
+    memo: dict[int, int] = {}
+
+    def depth(t: Any) -> int:
+        if not is_op(t, compose_op, 2):
+            return 0
+        key = id(t)
+        if key not in memo:
+            memo[key] = 1 + max(depth(t.args[0]), depth(t.args[1]))
+        return memo[key]
+
+    return depth(F)
+
+
+def _same_term(x: Any, y: Any) -> bool:
+    return x is y or x == y
+
+
 def build_scan_plan(root: Any) -> dict | None:
-    if not is_op(root, "applyd", 2):
+    root = fold_nested_apply(root)
+    root, post = strip_output_views(root)
+    if not isinstance(root, Op) or root.op not in _CARRIERS or len(root.args) != 2:
         return None
+    leaf_op, comp_op, proj_a, proj_b, domain = _CARRIERS[root.op]
     F, h = root.args
-    if is_op(F, "aff_diag", 2):
-        pa, pb = _proj_list(F.args[0], "affd_a"), _proj_list(F.args[1], "affd_b")
+    base = {"domain": domain, "h": h, "post": post}
+    if is_op(F, leaf_op, 2):
+        pa, pb = _proj_list(F.args[0], proj_a), _proj_list(F.args[1], proj_b)
         if pa is not None and pb is not None:
             fs_a, dim_a = pa
             fs_b, dim_b = pb
-            if dim_a != dim_b or len(fs_a) != len(fs_b) or any(x is not y and x != y for x, y in zip(fs_a, fs_b)):
+            if dim_a != dim_b or len(fs_a) != len(fs_b) or any(not _same_term(x, y) for x, y in zip(fs_a, fs_b)):
                 return None
-            leaves = _prefix_chain(fs_a)
+            leaves = _prefix_chain(fs_a, leaf_op, comp_op)
             if leaves is None:
                 return None
-            return {"mode": "prefix", "leaves": leaves, "h": h, "dim": dim_a,
-                    "gather": _shared_gather(leaves), "table": prefix_chunk_table(len(leaves))}
-    leaves = affd_leaves(F)
+            return {**base, "mode": "prefix", "leaves": leaves, "dim": dim_a, "levels": 0,
+                    "gather": _shared_gather(leaves), "a_shared": _a_shared(leaves),
+                    "table": prefix_chunk_table(len(leaves))}
+    leaves = map_leaves(F, leaf_op, comp_op)
     if leaves is None:
         return None
     leaves = leaves[::-1]  # time order: the innermost map runs first
-    return {"mode": "final", "leaves": leaves, "h": h, "gather": _shared_gather(leaves),
+    return {**base, "mode": "final", "leaves": leaves, "levels": _compose_levels(F, comp_op),
+            "gather": _shared_gather(leaves), "a_shared": _a_shared(leaves),
             "table": prefix_chunk_table(len(leaves))}
+
+
+def _a_shared(leaves: list) -> bool:
+    """Every leaf's linear part is the same term (an LTI system)."""
+    a0 = leaves[0].args[0]
+    return all(_same_term(lf.args[0], a0) for lf in leaves)
 
 
 def _step_index(t: Any) -> tuple | None:
@@ -140,20 +266,19 @@ def _step_index(t: Any) -> tuple | None:
     return None
 
 
-def _shared_gather(leaves: list) -> dict | None:
-    """When leaf ``t`` reads step ``t`` of shared ``a`` / ``u`` arrays (same
-    base, same axis, indices 0..T-1 in time order), the bases themselves."""
+def _shared_gather(leaves: list) -> dict:
+    """Per leaf slot (0: linear part, 1: offset) whose operands all index one
+    base term along one axis: ``(base, dim, indices)`` in time order
+    (``_leaf_b_gather``, scan_lower.py:308-337, extended to the linear part)."""
     out = {}
     for slot in (0, 1):
         idx = [_step_index(lf.args[slot]) for lf in leaves]
         if any(i is None for i in idx):
-            return None
+            continue
         base, dim = idx[0][0], idx[0][1]
-        if any(i[0] is not base and i[0] != base for i in idx) or any(i[1] != dim for i in idx):
-            return None
-        if [i[2] for i in idx] != list(range(len(leaves))):
-            return None
-        out[slot] = (base, dim)
+        if any(not _same_term(i[0], base) for i in idx) or any(i[1] != dim for i in idx):
+            continue
+        out[slot] = (base, dim, [i[2] for i in idx])
     return out
 
 
@@ -161,8 +286,12 @@ def is_scan_term(term: Any) -> bool:
     return build_scan_plan(term) is not None
 
 
+def _prod(shape) -> int:
+    return math.prod(int(s) for s in shape)
+
+
 class HipScanModule(HipExecutorBase, nn.Module):
-    """Planned executor for diagonal-affine scans (module docstring)."""
+    """Planned executor for affine scans, diagonal and dense (module docstring)."""
 
     def __init__(self, ir: IR, param_values: dict | None = None, *, eval_mod: HipIRModule | None = None,
                  device: Any = None, ops=None, schedule: int | None = None) -> None:
@@ -179,21 +308,40 @@ class HipScanModule(HipExecutorBase, nn.Module):
     def n_steps(self) -> int:
         return 0 if self._plan is None else len(self._plan["leaves"])
 
-    def _operands(self, ev) -> tuple:
+    @property
+    def n_levels(self) -> int:
+        """Compose levels of the planned tree (0 when not planned, and for the
+        stacked prefix form, whose map is one leaf in the reference's plan)."""
+        return 0 if self._plan is None else self._plan["levels"]
+
+    def _slot_values(self, ev, slot: int) -> torch.Tensor | None:
+        """Step-major stack of leaf operand ``slot`` (a step-0 axis)."""
         p = self._plan
         T = len(p["leaves"])
-        if p["gather"] is not None:
-            a_base, a_dim = p["gather"][0]
-            u_base, u_dim = p["gather"][1]
-            a = ev(a_base).movedim(a_dim, 0)
-            u = ev(u_base).movedim(u_dim, 0)
-            if a.shape[0] != T or u.shape[0] != T:
-                a = u = None
-            if a is not None:
-                return a, u
-        a = torch.stack([torch.as_tensor(ev(lf.args[0])) for lf in p["leaves"]])
-        u = torch.stack([torch.as_tensor(ev(lf.args[1])) for lf in p["leaves"]])
-        return a, u
+        g = p["gather"].get(slot)
+        if g is not None:
+            base_t, dim, idx = g
+            base = ev(base_t)
+            if isinstance(base, torch.Tensor) and -base.dim() <= dim < base.dim():
+                if idx == list(range(T)) and base.shape[dim] == T:
+                    return base.movedim(dim, 0)
+                if all(-base.shape[dim] <= i < base.shape[dim] for i in idx):
+                    ix = self._cached(("idx", slot, tuple(idx)), base,
+                                      lambda t: torch.tensor(idx, dtype=torch.long, device=t.device),
+                                      dtype=torch.long)
+                    return base.index_select(dim, ix).movedim(dim, 0)
+        vals = [torch.as_tensor(ev(lf.args[slot])) for lf in p["leaves"]]
+        try:
+            tgt = torch.broadcast_shapes(*[v.shape for v in vals])
+        except RuntimeError:
+            return None
+        return torch.stack([v.expand(tgt) for v in vals])
+
+    def _apply_post(self, out: Any) -> Any:
+        tab = self.eval_mod._bindings().torch_bindings
+        for op, attrs in reversed(self._plan["post"]):
+            out = tab[op](out, **attrs)
+        return out
 
     def _forward_impl(self, *xs: Any) -> Any:
         p = self._plan
@@ -201,18 +349,39 @@ class HipScanModule(HipExecutorBase, nn.Module):
             return self.eval_mod(*xs)
         x, env = self._input_env(xs)
         ev = self.ev_factory(env, x)
-        a, u = self._operands(ev)
-        h = ev(p["h"])
-        ts = (a, u, h)
-        if not all(isinstance(t, torch.Tensor) and t.device.type == "cuda"
-                   and t.dtype in (torch.float32, torch.bfloat16) for t in ts):
+        out = self._forward_diag(ev) if p["domain"] == "diag" else self._forward_dense(ev)
+        if out is None:
             self.fallbacks += 1
             return self.eval_mod(*xs)
-        out_dtype = torch.result_type(torch.empty((), dtype=a.dtype), torch.empty((), dtype=u.dtype))
-        out_dtype = torch.promote_types(out_dtype, h.dtype)
-        T = a.shape[0]
-        sshape = torch.broadcast_shapes(a.shape[1:], u.shape[1:], h.shape)
-        a_ = a.expand(T, *sshape)
+        return self._apply_post(out)
+
+    @staticmethod
+    def _kernel_ok(*ts: Any) -> bool:
+        return all(isinstance(t, torch.Tensor) and t.device.type == "cuda"
+                   and t.dtype in (torch.float32, torch.bfloat16) for t in ts)
+
+    # ------------------------------------------------------------- diagonal
+
+    def _forward_diag(self, ev) -> torch.Tensor | None:
+        p = self._plan
+        T = len(p["leaves"])
+        shared = p["a_shared"] and p["gather"].get(0) is None
+        if shared:
+            a = torch.as_tensor(ev(p["leaves"][0].args[0]))  # one map for every step: stride 0 over T
+        else:
+            a = self._slot_values(ev, 0)
+        u = self._slot_values(ev, 1)
+        h = ev(p["h"])
+        if a is None or u is None or not self._kernel_ok(a, u, h) or u.shape[0] != T:
+            return None
+        if not shared and a.shape[0] != T:
+            return None
+        out_dtype = torch.promote_types(torch.promote_types(a.dtype, u.dtype), h.dtype)
+        try:
+            sshape = torch.broadcast_shapes(a.shape if shared else a.shape[1:], u.shape[1:], h.shape)
+        except RuntimeError:
+            return None
+        a_ = a.expand(sshape) if shared else a.expand(T, *sshape)
         u_ = u.expand(T, *sshape)
         h_ = h.expand(sshape)
         states, hf = K.affd_scan(a_, u_, h_, p["table"], schedule=self.schedule,
@@ -220,3 +389,56 @@ class HipScanModule(HipExecutorBase, nn.Module):
         if p["mode"] == "final":
             return hf.to(out_dtype)
         return states.to(out_dtype).movedim(0, p["dim"])
+
+    # ---------------------------------------------------------------- dense
+
+    def _dense_linear(self, ev) -> torch.Tensor | None:
+        """Linear parts as ``(TA, *PA, d, d)``, ``TA = 1`` for a shared map."""
+        p = self._plan
+        if p["a_shared"]:
+            A = torch.as_tensor(ev(p["leaves"][0].args[0]))
+            return A.unsqueeze(0)
+        return self._slot_values(ev, 0)
+
+    def _forward_dense(self, ev) -> torch.Tensor | None:
+        p = self._plan
+        T = len(p["leaves"])
+        A = self._dense_linear(ev)
+        b = self._slot_values(ev, 1)
+        h = ev(p["h"])
+        if A is None or b is None or not self._kernel_ok(A, b, h) or b.shape[0] != T or A.dim() < 3:
+            return None
+        d = A.shape[-1]
+        if A.shape[-2] != d or not 1 <= d <= DENSE_MAX_D or A.shape[0] not in (1, T):
+            return None
+        out_dtype = torch.promote_types(torch.promote_types(A.dtype, b.dtype), h.dtype)
+        TA = A.shape[0]
+        if p["mode"] == "prefix" or (b.dim() == 2 and h.dim() == 1):
+            # vector state: A (d, d), b (d,), h (d,)
+            if A.dim() != 3 or b.shape[1:] != (d,) or h.shape != (d,):
+                return None
+            if p["mode"] == "prefix" and p["dim"] not in (0, 1):
+                return None  # the stacked maps and offsets would not line up
+            A4, b3, h3, pshape, k = A.reshape(TA, 1, d, d), b.reshape(T, 1, d), h.reshape(1, d, 1), (), 1
+        else:
+            # column state: A (…, d, d), b (…, d, 1), h (…, d, k)
+            if b.dim() < 3 or b.shape[-2:] != (d, 1) or h.dim() < 2 or h.shape[-2] != d:
+                return None
+            k = h.shape[-1]
+            PA, PB, PH = A.shape[1:-2], b.shape[1:-2], h.shape[:-2]
+            try:
+                pshape = torch.broadcast_shapes(PA, PB, PH)
+            except RuntimeError:
+                return None
+            Pn = _prod(pshape)
+            A4 = A.reshape(TA, 1, d, d) if _prod(PA) == 1 else A.expand(TA, *pshape, d, d).reshape(TA, Pn, d, d)
+            b3 = b.reshape(T, 1, d) if _prod(PB) == 1 else b.expand(T, *pshape, d, 1).reshape(T, Pn, d)
+            h3 = h.expand(*pshape, d, k).reshape(Pn, d, k)
+        if T == 0:
+            return None
+        states, hf = K.aff_scan(A4, b3, h3, p["table"], schedule=self.schedule, states=p["mode"] == "prefix")
+        if p["mode"] == "prefix":
+            return states.reshape(T, d).to(out_dtype).movedim(0, p["dim"])
+        if h.dim() == 1:
+            return hf.reshape(d).to(out_dtype)
+        return hf.reshape(*pshape, d, k).to(out_dtype)

@@ -19,7 +19,11 @@ can feed this package's sink exactly what the orchestrator would route:
 * :func:`scan_final_form` / :func:`scan_prefix_form` — the diagonal-affine
   chain ``applyd(affd_compose(…), h)`` and its stacked all-prefix form
   (``xcarrier.py:2252-2273``), with leaves reading step ``t`` of shared
-  ``a`` / ``u`` arrays.
+  ``a`` / ``u`` arrays;
+* :func:`linear_recurrence_form` / :func:`dense_scan_form` /
+  :func:`dense_scan_prefix_form` — the dense affine monoid: ``apply`` over a
+  balanced ``aff_compose`` tree (the depth-extracted ``LinearRecurrence``
+  term) and the stacked all-prefix form (``xcarrier.py:2276-2293``).
 
 Each returns ``(IR, param_shapes)``; parameter values come from the caller.
 """
@@ -38,6 +42,9 @@ __all__ = [
     "retention_block_form",
     "scan_final_form",
     "scan_prefix_form",
+    "linear_recurrence_form",
+    "dense_scan_form",
+    "dense_scan_prefix_form",
 ]
 
 mk = Op.make
@@ -172,3 +179,65 @@ def scan_prefix_form(T: int, state_shape: tuple) -> tuple[IR, dict]:
     A = mk("stack", *[mk("affd_a", f) for f in fs], dim=0)
     Bm = mk("stack", *[mk("affd_b", f) for f in fs], dim=0)
     return IR(mk("applyd", mk("aff_diag", A, Bm), h), [a, u, h]), {}
+
+
+def _balanced(leaves: list, compose: str):
+    """Balanced compose tree over ``leaves`` in product order."""
+    if len(leaves) == 1:
+        return leaves[0]
+    mid = len(leaves) // 2
+    return mk(compose, _balanced(leaves[:mid], compose), _balanced(leaves[mid:], compose))
+
+
+def linear_recurrence_form(T: int, d: int) -> tuple[IR, dict]:
+    """``LinearRecurrence`` (models/__init__.py:576-598, ``h_t = A h_{t-1} +
+    x_t``) as the depth-extracted scan term: ``apply(<balanced aff_compose
+    tree>, p_h0)`` over leaves ``aff(p_a, select(x, 0, t))``, later steps on
+    the left (the shape of ``_balanced_scan_ir``, tests/test_scan_batched.py:
+    56-88)."""
+    x = Var("x", TensorType((T, d)))
+    A = Param("p_a", TensorType((d, d)))
+    h0 = Param("p_h0", TensorType((d,)))
+    leaves = [mk("aff", A, mk("select", x, dim=0, index=t)) for t in reversed(range(T))]
+    return IR(mk("apply", _balanced(leaves, "aff_compose"), h0), [x]), {"p_a": (d, d), "p_h0": (d,)}
+
+
+def dense_scan_form(T: int, d: int, batch: tuple = (), k: int = 1, *, time_varying: bool = False,
+                    per_slot: bool = False) -> tuple[IR, dict]:
+    """Batched dense scan with column states: ``apply(<balanced tree>, h)``
+    over leaves ``aff(A_t, select(b, 0, t))`` with ``b (T, *batch, d, 1)``,
+    ``h (*batch, d, k)``; ``A_t`` is ``select(A, 0, t)`` of ``A (T, [*batch,]
+    d, d)`` when time-varying, else the shared ``A ([*batch,] d, d)``
+    (``per_slot`` adds the batch dims to the map)."""
+    mshape = (*batch, d, d) if per_slot else (d, d)
+    A = Var("A", TensorType((T, *mshape) if time_varying else mshape))
+    b = Var("b", TensorType((T, *batch, d, 1)))
+    h = Var("h", TensorType((*batch, d, k)))
+
+    def leaf(t):
+        At = mk("select", A, dim=0, index=t) if time_varying else A
+        return mk("aff", At, mk("select", b, dim=0, index=t))
+
+    leaves = [leaf(t) for t in reversed(range(T))]
+    return IR(mk("apply", _balanced(leaves, "aff_compose"), h), [A, b, h]), {}
+
+
+def dense_scan_prefix_form(T: int, d: int, *, time_varying: bool = True, dim: int = 0) -> tuple[IR, dict]:
+    """The stacked all-prefix form ``apply(aff(stack(aff_A f_t), stack(aff_b
+    f_t)), h)`` (gather_apply_stack, xcarrier.py:2276-2293) over the prefixes
+    ``f_t = aff_compose(leaf_t, f_{t-1})``: every state ``h_0 … h_{T-1}``,
+    stacked along ``dim``; vector state ``h (d,)``, ``b (T, d)``."""
+    A = Var("A", TensorType((T, d, d) if time_varying else (d, d)))
+    b = Var("b", TensorType((T, d)))
+    h = Var("h", TensorType((d,)))
+
+    def leaf(t):
+        At = mk("select", A, dim=0, index=t) if time_varying else A
+        return mk("aff", At, mk("select", b, dim=0, index=t))
+
+    fs = [leaf(0)]
+    for t in range(1, T):
+        fs.append(mk("aff_compose", leaf(t), fs[-1]))
+    SA = mk("stack", *[mk("aff_A", f) for f in fs], dim=dim)
+    SB = mk("stack", *[mk("aff_b", f) for f in fs], dim=dim)
+    return IR(mk("apply", mk("aff", SA, SB), h), [A, b, h]), {}

@@ -404,6 +404,42 @@ def affd_scan(a: torch.Tensor, u: torch.Tensor, h0: torch.Tensor | None,
     return (out.reshape(T, *sshape) if out is not None else None), hf.reshape(sshape)
 
 
+def aff_scan(A: torch.Tensor, b: torch.Tensor, h0: torch.Tensor, chunk_starts, *,
+             schedule: int = L.SCAN_AUTO, states: bool = True):
+    """Dense affine scan over the leading axis: ``X_t = A_t X_{t-1} + b_t 1ᵀ``.
+
+    ``A`` is ``(TA, PA, d, d)`` with ``TA`` in {1, T} (1: one map for every
+    step) and ``PA`` in {1, P} (1: one map for every slot); ``b`` is
+    ``(T, PB, d)`` with ``PB`` in {1, P}; ``h0`` is the ``(P, d, k)`` initial
+    state.  Returns ``(states (T, P, d, k) or None, h_final (P, d, k))`` in
+    fp32.
+    """
+    _need_device(A, b, h0)
+    lib = L.load()
+    if A.dim() != 4 or b.dim() != 3 or h0.dim() != 3:
+        raise ValueError("aff_scan wants A (TA, PA, d, d), b (T, PB, d), h0 (P, d, k)")
+    T, PB, d = b.shape
+    P, dh, k = h0.shape
+    TA, PA = A.shape[0], A.shape[1]
+    if A.shape[2:] != (d, d) or dh != d or TA not in (1, T) or PA not in (1, P) or PB not in (1, P):
+        raise ValueError(f"aff_scan shapes do not fit: A{tuple(A.shape)} b{tuple(b.shape)} h0{tuple(h0.shape)}")
+    f = lambda t: t.to(torch.float32).contiguous()  # noqa: E731
+    A2, b2, h2 = f(A), f(b), f(h0)
+    lda_t = d * d * PA if TA > 1 else 0
+    lda_p = d * d if PA > 1 else 0
+    ldb_t = d * PB
+    ldb_p = d if PB > 1 else 0
+    cs, nc = _chunk_table(chunk_starts, T, b.device)
+    out = torch.empty((T, P, d, k), dtype=torch.float32, device=b.device) if states else None
+    hf = torch.empty((P, d, k), dtype=torch.float32, device=b.device)
+    wsb = lib.catopt_hip_aff_scan_workspace_bytes(P, d, k, int(lda_p == 0), nc)
+    ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=b.device)
+    st = lib.catopt_hip_aff_scan(T, P, d, k, _ptr(A2), lda_t, lda_p, _ptr(b2), ldb_t, ldb_p, _ptr(h2),
+                                 _ptr(cs), nc, int(schedule), _ptr(out), _ptr(hf), _ptr(ws), wsb, _stream(b))
+    L.check("catopt_hip_aff_scan", st)
+    return out, hf
+
+
 def ssm_scan(a: torch.Tensor, bx: torch.Tensor, c: torch.Tensor, x: torch.Tensor,
              h0: torch.Tensor | None, chunk_starts, *, schedule: int = L.SCAN_AUTO,
              return_state: bool = False):

@@ -134,8 +134,9 @@ class HipSink:
             ("scan", ExecutorSpec(
                 "scan", planned(HipScanModule), is_scan_term,
                 lambda m: bool(getattr(m, "is_batched", False)),
-                (frozenset({"applyd"}), frozenset({"affd_compose", "stack", "affd_a", "affd_b"}),
-                 frozenset({"aff_diag"})))),
+                (frozenset({"apply", "applyd"}),
+                 frozenset({"aff_compose", "affd_compose", "stack", "aff_A", "aff_b", "affd_a", "affd_b"}),
+                 frozenset({"aff", "aff_diag"})))),
             ("om_batched", ExecutorSpec(
                 "om_batched", planned(HipOMModule), is_om_term,
                 lambda m: bool(getattr(m, "is_batched", False)),

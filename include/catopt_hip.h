@@ -259,6 +259,37 @@ int32_t catopt_hip_ssm_scan(int64_t B, int64_t T, int64_t D, int64_t N,
                             int64_t workspace_bytes, void* stream);
 
 /*
+ * Dense affine scan over T steps of P slots, each carrying a d x k state
+ * (fp32, 1 ≤ d ≤ 64, k ≥ 1):
+ *   X_t[p] = A_t[p] · X_{t-1}[p] + b_t[p] 1ᵀ,   X_{-1} = h0 (NULL = 0)
+ * A_t[p] is the row-major d x d block at A + t·lda_t + p·lda_p (lda_t = 0:
+ * one map for every step, the LTI case; lda_p = 0: one map for every slot,
+ * which batches all P·k columns into one MFMA product per step); b_t[p] the
+ * d-vector at b + t·ldb_t + p·ldb_p, added to every column.  h0, h_final:
+ * [P, d, k] contiguous; states (optional, [T, P, d, k]) receives every
+ * prefix state.  Chunk table and schedule as for catopt_hip_affd_scan (the
+ * chunk-parallel schedule composes each chunk's dense map from the
+ * identity); its workspace: catopt_hip_aff_scan_workspace_bytes(P, d, k,
+ * lda_p == 0, n_chunks) bytes (0 is enough for streaming).
+ * d > 64: CATOPT_E_UNSUPPORTED.
+ * Replaces the dense affine monoid's batched composition: the aff /
+ * aff_compose / apply bindings (torch_bridge.py:1873-1881), the
+ * homogeneous-matrix levels of BatchedScanModule (scan_lower.py:716-741,
+ * 640-698) and fused_dense_levels (scan_fused.py:123-143), and the stacked
+ * all-prefix form gather_apply_stack (xcarrier.py:2276-2293).
+ */
+int64_t catopt_hip_aff_scan_workspace_bytes(int64_t P, int64_t d, int64_t k,
+                                            int32_t shared_map,
+                                            int64_t n_chunks);
+int32_t catopt_hip_aff_scan(int64_t T, int64_t P, int64_t d, int64_t k,
+                            const float* A, int64_t lda_t, int64_t lda_p,
+                            const float* b, int64_t ldb_t, int64_t ldb_p,
+                            const float* h0, const int64_t* chunk_starts,
+                            int64_t n_chunks, int32_t schedule, float* states,
+                            float* h_final, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
+/*
  * Elementwise helpers behind the generic evaluator's bindings when no
  * fused form applies: silu (torch_bridge.py:1159), mul (the "mul"
  * binding) and the paired silu·mul of SWIGLU_FUSE.  n elements,

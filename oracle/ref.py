@@ -42,6 +42,12 @@ __all__ = [
     "serial_affd_scan",
     "ssm_serial",
     "ssm_chunked",
+    "aff_compose",
+    "aff_apply",
+    "aff_homogeneous",
+    "fused_dense_levels",
+    "serial_aff_scan",
+    "aff_chunked_scan",
 ]
 
 _REL_FLOOR = 1e-8
@@ -509,3 +515,93 @@ def ssm_chunked(a, bx, c, x, h0, table):
             hh = A[:, t] * hh + U[:, t]
             y[:, t] = np.einsum("bn,bdn->bd", c[:, t], hh)
     return y, h_final
+
+
+# ---------------------------------------------------------------- dense scans
+
+
+def aff_compose(f, g):
+    """"aff_compose" binding (torch_bridge.py:1877-1880): ``f ∘ g`` with g
+    applied first: ``(f.A @ g.A, f.A @ g.b + f.b)``."""
+    return f[0] @ g[0], f[0] @ g[1] + f[1]
+
+
+def aff_apply(f, h):
+    """"apply" binding (torch_bridge.py:1881): ``f.A @ h + f.b``."""
+    return f[0] @ h + f[1]
+
+
+def aff_homogeneous(A, b):
+    """Leaf packing of ``BatchedScanModule._leaf_homogeneous``
+    (scan_lower.py:716-741): ``[[A, b], [0 … 0, 1]]``, ``(n, d+1, d+1)`` from
+    ``A (n, d, d)`` and a vector ``b (n, d)``."""
+    A, b = np.asarray(A), np.asarray(b)
+    n, d = A.shape[0], A.shape[-1]
+    M = np.zeros((n, d + 1, d + 1), dtype=np.result_type(A, b))
+    M[:, :d, :d] = A
+    M[:, :d, d] = b
+    M[:, d, d] = 1
+    return M
+
+
+def fused_dense_levels(m_seq, h):
+    """``fused_dense_levels`` (scan_fused.py:123-143): leaf homogeneous
+    matrices in product order (leaf 0 is the OUTERMOST map), identity-padded
+    to a power of two, adjacent-pair levels ``m = m[0::2] @ m[1::2]``, read
+    out ``A_root h + b_root``."""
+    m = np.asarray(m_seq)
+    n, d1 = m.shape[0], m.shape[-1]
+    pad = (1 << max(n - 1, 0).bit_length()) - n
+    if pad:
+        m = np.concatenate([m, np.broadcast_to(np.eye(d1, dtype=m.dtype), (pad, d1, d1))])
+    while m.shape[0] > 1:
+        m = m[0::2] @ m[1::2]
+    r = m[0]
+    d = d1 - 1
+    return r[:d, :d] @ h + r[:d, d]
+
+
+def serial_aff_scan(A, b, h0):
+    """The dense recurrence one step at a time, every state (the "apply"
+    chain of LinearRecurrence, models/__init__.py:593-598, with batched
+    columns): ``X_t = A_t X_{t-1} + b_t 1ᵀ``.  ``A`` is ``(d, d)`` (one map),
+    ``(T, d, d)`` or ``(T, P, d, d)``; ``b`` is ``(T, d)`` or ``(T, P, d)``;
+    ``h0`` is ``(d, k)`` or ``(P, d, k)``.  Returns ``(T, *h0.shape)``."""
+    A, b, h = np.asarray(A), np.asarray(b), np.asarray(h0).copy()
+    T = b.shape[0]
+    out = np.empty((T, *h.shape), dtype=np.result_type(A, b, h))
+    for t in range(T):
+        At = A if A.ndim == 2 else A[t]
+        h = At @ h + b[t][..., None]
+        out[t] = h
+    return out
+
+
+def aff_chunked_scan(A, b, h0, table):
+    """The dense scan through the chunk-carry algebra of the HIP chunk-parallel
+    schedule (the blocked all-prefix plan, omd_lower.py:771-824, in the dense
+    domain): (1) each chunk's map ``(M_c, v_c)`` composed from the identity,
+    (2) carries folded over the chunks in table order, (3) each chunk re-run
+    from its carry.  Same function as ``serial_aff_scan``; shapes as there."""
+    A, b, h0 = np.asarray(A), np.asarray(b), np.asarray(h0)
+    T = b.shape[0]
+    d = b.shape[-1]
+    At = (lambda t: A) if A.ndim == 2 else (lambda t: A[t])
+    eye = np.broadcast_to(np.eye(d, dtype=A.dtype), (*b.shape[1:-1], d, d))
+    locs = []
+    for s, e in zip(table[:-1], table[1:]):
+        M, v = eye, np.zeros((*b.shape[1:], 1), dtype=b.dtype)  # v as a column: batched @ stays per slot
+        for t in range(s, e):
+            M, v = aff_compose((At(t), b[t][..., None]), (M, v))
+        locs.append((M, v))
+    carries, h = [], h0
+    for M, v in locs:
+        carries.append(h)
+        h = M @ h + v
+    out = np.empty((T, *h0.shape), dtype=np.result_type(A, b, h0))
+    for (s, e), carry in zip(zip(table[:-1], table[1:]), carries):
+        hh = carry
+        for t in range(s, e):
+            hh = At(t) @ hh + b[t][..., None]
+            out[t] = hh
+    return out, h

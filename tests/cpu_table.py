@@ -80,5 +80,7 @@ def cpu_table() -> HipOpTable:
         "hip_linear": lambda x, w, b=None, **kw: F.linear(x, w, b),
         "hip_swiglu": _swiglu,
         "hip_glu": _glu,
+        "aff_compose": lambda f, g, *a, **kw: (f[0] @ g[0], f[0] @ g[1] + f[1]),
+        "apply": lambda f, h, *a, **kw: f[0] @ h + f[1],
     })
     return t

@@ -68,6 +68,11 @@ def test_workspace_queries(lib):
     assert lib.catopt_hip_retention_workspace_bytes(1, 1, 64, 128, 32) == -1
     assert lib.catopt_hip_scan_workspace_bytes(10, 3) == 2 * 10 * 3 * 4
     assert lib.catopt_hip_scan_workspace_bytes(-1, 3) == -1
+    # dense scan: chunk maps (G·d², 256-byte rounded) + offsets (P·d) + carries (P·d·k), per chunk
+    up = lambda n: -(-n // 64) * 64  # noqa: E731
+    assert lib.catopt_hip_aff_scan_workspace_bytes(4, 16, 2, 1, 3) == 4 * (up(3 * 256) + up(3 * 64) + up(3 * 128))
+    assert lib.catopt_hip_aff_scan_workspace_bytes(4, 16, 2, 0, 3) == 4 * (up(3 * 4 * 256) + up(3 * 64) + up(3 * 128))
+    assert lib.catopt_hip_aff_scan_workspace_bytes(-1, 16, 1, 1, 3) == -1
 
 
 def test_host_argument_checks(lib):
@@ -87,3 +92,10 @@ def test_host_argument_checks(lib):
     table = (C.c_int64 * 2)(0, 4)
     assert lib.catopt_hip_affd_scan(4, 8, None, 8, None, 8, None, table, 1, 7, None, None, None, 0,
                                     None) == L.E_INVAL
+    # dense scan: bad schedule, d beyond the MFMA tiles, k < 1, negative stride
+    args = (None, 0, 0, None, 16, 0, None, table, 1)
+    assert lib.catopt_hip_aff_scan(4, 2, 16, 1, *args, 7, None, None, None, 0, None) == L.E_INVAL
+    assert lib.catopt_hip_aff_scan(4, 2, 65, 1, *args, 0, None, None, None, 0, None) == L.E_UNSUPPORTED
+    assert lib.catopt_hip_aff_scan(4, 2, 16, 0, *args, 0, None, None, None, 0, None) == L.E_INVAL
+    assert lib.catopt_hip_aff_scan(4, 2, 16, 1, None, -1, 0, None, 16, 0, None, table, 1, 0, None, None,
+                                   None, 0, None) == L.E_INVAL

@@ -326,7 +326,8 @@ def test_sink_surface_routing_and_verify():
     assert names == ["om_decayed_chunked", "scan", "om_batched", "generic"]
     assert sink.executors["generic"].carrier is None
     assert {"linear", "matmul", "rms_norm", "om_elem", "om_compose", "om_apply", "om_decayed",
-            "decay", "decay_vec", "aff_diag", "affd_compose", "applyd"} <= sink.supported_ops
+            "decay", "decay_vec", "aff_diag", "affd_compose", "applyd", "aff", "aff_compose",
+            "apply", "aff_A", "aff_b"} <= sink.supported_ops
     cases = [
         (forms.retention_kway_form(1, 2, 128, 128, 64)[0], "om_decayed_chunked"),
         (forms.scan_final_form(4, (2,))[0], "scan"),
@@ -376,3 +377,60 @@ def test_streaming_plan_leaf_kinds_and_fold_order():
     e_m, e_l, e_a = om_empty_state((2, 3), 5, dtype=torch.float64)
     assert e_m.shape == (2, 3, 1) and e_a.shape == (2, 3, 5) and e_m.dtype == torch.float64
     assert torch.isneginf(e_m).all() and not e_l.any() and not e_a.any()
+
+
+# ------------------------------------------------------------------ dense scan plan
+
+
+def test_dense_scan_plans_and_levels():
+    ir, _ = forms.linear_recurrence_form(8, 4)
+    p = build_scan_plan(ir.root)
+    assert p["domain"] == "dense" and p["mode"] == "final" and len(p["leaves"]) == 8
+    assert p["levels"] == 3 and p["a_shared"]  # balanced over 8 leaves: 4 + 2 + 1 composes
+    # time order: the innermost leaf reads step 0
+    assert [lf.args[1].attrs["index"] for lf in p["leaves"]] == list(range(8))
+    assert p["gather"][1][2] == list(range(8)) and 0 not in p["gather"]
+    irt, _ = forms.dense_scan_form(5, 4, (2,), 3, time_varying=True, per_slot=True)
+    pt = build_scan_plan(irt.root)
+    assert not pt["a_shared"] and pt["gather"][0][2] == list(range(5))
+    irp, _ = forms.dense_scan_prefix_form(6, 4)
+    pp = build_scan_plan(irp.root)
+    assert pp["domain"] == "dense" and pp["mode"] == "prefix" and len(pp["leaves"]) == 6 and pp["levels"] == 0
+    # mixed carriers are not one scan
+    A, b, h = Var("A", TensorType((3, 3))), Var("b", TensorType((3,))), Var("h", TensorType((3,)))
+    mixed = mk("apply", mk("aff_compose", mk("aff", A, b), mk("aff_diag", b, b)), h)
+    assert build_scan_plan(mixed) is None
+    assert build_scan_plan(mk("aff_compose", mk("aff", A, b), mk("aff", A, b))) is None  # no apply root
+
+
+def test_nested_apply_folds_and_output_views_strip():
+    A, b, h = Var("A", TensorType((3, 3))), Var("b", TensorType((3,))), Var("h", TensorType((3,)))
+    f = mk("aff", A, b)
+    g = mk("aff", mk("transpose", A, dim0=0, dim1=1), b)
+    nested = mk("reshape", mk("apply", f, mk("apply", g, mk("apply", f, h))), shape=(1, 3))
+    p = build_scan_plan(nested)
+    assert p is not None and p["mode"] == "final" and p["post"] == [("reshape", {"shape": (1, 3)})]
+    assert [lf is g for lf in p["leaves"]] == [False, True, False] and p["h"] is h
+    # the diagonal pair folds the same way
+    d = mk("applyd", mk("aff_diag", b, b), mk("applyd", mk("aff_diag", h, b), h))
+    pd = build_scan_plan(d)
+    assert pd["domain"] == "diag" and len(pd["leaves"]) == 2
+
+
+def test_dense_scan_module_fallback_matches_the_recurrence():
+    T, d = 9, 4
+    ir, _ = forms.linear_recurrence_form(T, d)
+    A = torch.randn(d, d, dtype=torch.float64) * 0.3
+    h0 = torch.randn(d, dtype=torch.float64)
+    mod = HipScanModule(ir, {"p_a": A, "p_h0": h0}, ops=cpu_table())
+    assert mod.is_batched and mod.n_levels == 4
+    x = torch.randn(T, d, dtype=torch.float64)
+    out = mod(x)  # host / fp64 operands: the generic module runs
+    assert mod.fallbacks == 1
+    ref = oracle.serial_aff_scan(_np(A), _np(x), _np(h0)[:, None])[-1, :, 0]
+    assert oracle.verify_equiv(ref, _np(out), rtol=1e-12)["passed"]
+    irp, _ = forms.dense_scan_prefix_form(T, d)
+    modp = HipScanModule(irp, {}, ops=cpu_table())
+    At = torch.randn(T, d, d, dtype=torch.float64) * 0.3
+    refp = oracle.serial_aff_scan(_np(At), _np(x), _np(h0)[:, None])[..., 0]
+    assert oracle.verify_equiv(refp, _np(modp(At, x, h0)), rtol=1e-12)["passed"]

@@ -358,3 +358,90 @@ def test_ssm_serial_brute_force_and_chunked(aps):
         yc, hc = oracle.ssm_chunked(a, bx, c, x, h0, np.asarray(table))
         _close(yc, yb, 1e-12)
         _close(hc, hT, 1e-12)
+
+
+# ------------------------------------------------------------------ dense scans
+
+
+def test_aff_compose_order_homogeneous_and_associative():
+    d = 5
+    f = (rng.standard_normal((d, d)), rng.standard_normal(d))
+    g = (rng.standard_normal((d, d)), rng.standard_normal(d))
+    e = (rng.standard_normal((d, d)), rng.standard_normal(d))
+    h = rng.standard_normal(d)
+    fg = oracle.aff_compose(f, g)
+    _close(oracle.aff_apply(fg, h), oracle.aff_apply(f, oracle.aff_apply(g, h)), 1e-12)  # g applied first
+    swapped = oracle.aff_compose(g, f)
+    assert np.max(np.abs(oracle.aff_apply(swapped, h) - oracle.aff_apply(fg, h))) > 1e-6
+    # the homogeneous-matrix trick: packing is a monoid homomorphism onto matmul
+    Mf, Mg = oracle.aff_homogeneous(f[0][None], f[1][None])[0], oracle.aff_homogeneous(g[0][None], g[1][None])[0]
+    Mfg = oracle.aff_homogeneous(fg[0][None], fg[1][None])[0]
+    _close(Mf @ Mg, Mfg, 1e-12)
+    _close((Mf @ np.append(h, 1.0))[:d], oracle.aff_apply(f, h), 1e-12)
+    l1 = oracle.aff_compose(oracle.aff_compose(f, g), e)
+    l2 = oracle.aff_compose(f, oracle.aff_compose(g, e))
+    _close(l1[0], l2[0], 1e-12)
+    _close(l1[1], l2[1], 1e-12)
+
+
+@pytest.mark.parametrize("n", [1, 2, 5, 8])
+def test_fused_dense_levels_reversed_leaf_order(n):
+    d = 4
+    A = rng.standard_normal((n, d, d)) * 0.5
+    b = rng.standard_normal((n, d))
+    h0 = rng.standard_normal(d)
+    h = h0.copy()
+    for t in reversed(range(n)):  # leaf 0 is the OUTERMOST map
+        h = np.array([sum(A[t, i, j] * h[j] for j in range(d)) for i in range(d)]) + b[t]
+    _close(oracle.fused_dense_levels(oracle.aff_homogeneous(A, b), h0), h, 1e-12)
+
+
+def test_serial_aff_scan_closed_form_lti():
+    T, d, k = 9, 4, 3
+    A = rng.standard_normal((d, d)) * 0.5
+    assert np.max(np.abs(A - A.T)) > 1e-3  # a transposed operand would show
+    b = rng.standard_normal((T, d))
+    h0 = rng.standard_normal((d, k))
+    out = oracle.serial_aff_scan(A, b, h0)
+    mp = np.linalg.matrix_power
+    for t in range(T):
+        closed = mp(A, t + 1) @ h0 + sum(mp(A, t - s) @ b[s] for s in range(t + 1))[:, None]
+        _close(out[t], closed, 1e-12)
+        wrong = mp(A.T, t + 1) @ h0 + sum(mp(A.T, t - s) @ b[s] for s in range(t + 1))[:, None]
+        if t > 0:
+            assert np.max(np.abs(out[t] - wrong)) > 1e-6
+
+
+def test_serial_aff_scan_special_cases():
+    T, d = 7, 3
+    b = rng.standard_normal((T, d))
+    h0 = rng.standard_normal((d, 1))
+    # A = I: running sums
+    _close(oracle.serial_aff_scan(np.eye(d), b, h0)[..., 0], h0[:, 0] + np.cumsum(b, axis=0), 1e-12)
+    # diagonal maps: the diagonal scan (pinned above by its closed form)
+    a = rng.random((T, d))
+    At = np.stack([np.diag(x) for x in a])
+    _close(oracle.serial_aff_scan(At, b, h0)[..., 0], oracle.serial_affd_scan(a, b, h0[:, 0]), 1e-12)
+    # per-slot maps: slot p evolves alone
+    P = 3
+    Ap = rng.standard_normal((T, P, d, d)) * 0.5
+    bp = rng.standard_normal((T, P, d))
+    hp = rng.standard_normal((P, d, 2))
+    out = oracle.serial_aff_scan(Ap, bp, hp)
+    for p in range(P):
+        _close(out[:, p], oracle.serial_aff_scan(Ap[:, p], bp[:, p], hp[p]), 1e-12)
+
+
+@pytest.mark.parametrize("T", [1, 7, 50])
+@pytest.mark.parametrize("per_slot", [False, True])
+def test_aff_chunked_scan_matches_serial(T, per_slot):
+    d, P, k = 4, 2, 3
+    A = rng.standard_normal((T, P, d, d) if per_slot else (d, d)) * 0.5
+    b = rng.standard_normal((T, P, d))
+    h0 = rng.standard_normal((P, d, k))
+    ser = oracle.serial_aff_scan(A, b, h0)
+    tables = [[0, T], list(oracle.prefix_chunk_table(T))] + ([[0, 3, 4, T]] if T > 4 else [])
+    for table in tables:
+        out, hT = oracle.aff_chunked_scan(A, b, h0, np.asarray(table))
+        _close(out, ser, 1e-10)
+        _close(hT, ser[-1], 1e-10)
