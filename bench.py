@@ -1,6 +1,6 @@
 """Delivered-form throughput of the HIP executor on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--forms c1,c2,c3,c4,c5]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--forms c1,c2,c3,c4,c5,aff,copy]
                     [--cpu-budget SECONDS] [--no-cpu]
 
 One "step" is one forward of a delivered form over one batch of synthetic
@@ -8,7 +8,9 @@ input that is already resident in HBM (BASELINE.json's five configs, seeded
 with ``torch.manual_seed(0)``).  The headline workload is config 2 (the
 SwiGLU MLP block with RMSNorm: rms_norm -> gate/up GEMM with the silu*mul
 epilogue -> down GEMM); its whole-step TFLOP/s is ``value``.  Every other
-config is measured the same way and reported under ``forms``.
+config is measured the same way and reported under ``forms``, and so is the
+dense affine scan (``aff``: a batched LTI recurrence delivered as
+``apply(<aff_compose tree>, h)``; not one of the BASELINE configs).
 
 Per form:
   * ``ms_per_step``  — HIP events on torch's current stream (the stream the
@@ -499,6 +501,58 @@ class C5SSM(Form):
                 "parity_max_rel": rel}
 
 
+class DenseScan(Form):
+    """The dense affine monoid (not a BASELINE config): a batched LTI
+    ``LinearRecurrence`` h_t = A h_{t-1} + x_t over many independent
+    sequences, delivered as ``apply(<balanced aff_compose tree>, h)`` with one
+    shared map; the kernel runs each step as one fp32 MFMA product over all
+    sequences' state columns."""
+
+    name, dtype, unit, bound = "aff", "f32", "TFLOP/s", "mfma"
+    B, d, T = 16384, 64, 1024
+    workload = ("dense affine scan apply(aff_compose tree, h): shared A (64x64), B=16384 sequences, "
+                "T=1024 steps, offsets b_t (T,B,64,1), final state (B,64,1), fp32")
+    peak = PEAK["fp32_tflops"]
+    work = dom_work = 2.0 * T * B * d * d
+    dom_name = dom_key = "aff_dense_scan<4, false, true, false, false>"
+
+    def setup(self, dev):
+        import torch
+
+        from catopt_amd import forms
+        from catopt_amd.sink import deliver
+
+        g = _gen(0)
+        B, d, T = self.B, self.d, self.T
+        self.A = torch.randn((d, d), device=dev, generator=g) * (0.9 / math.sqrt(d))
+        self.b = torch.randn((T, B, d, 1), device=dev, generator=g)
+        self.h = torch.randn((B, d, 1), device=dev, generator=g)
+        ir, _ = forms.dense_scan_form(T, d, (B,), 1)
+        res = deliver(ir, {}, _sink(dev), (self.A, self.b, self.h))
+        self.mod, self.stats = res.module, res.stats
+        assert self.mod.is_batched and self.mod._plan["a_shared"]
+
+    def step(self):
+        self.out = self.mod(self.A, self.b, self.h)
+
+    dominant = step  # one kernel launch per step
+
+    def cpu(self, budget):
+        import oracle
+
+        Bs = 256  # 256 of the 16384 sequences (independent: a subset is exact)
+        A = self.A.cpu().numpy()
+        b = self.b[:, :Bs, :, 0].cpu().numpy()
+        h = self.h[:Bs].cpu().numpy()
+        sec, reps, states = time_cpu(lambda: oracle.serial_aff_scan(A, b, h), budget)
+        self.step()
+        rel = oracle.verify_equiv(states[-1], self.out[:Bs].cpu().numpy())["max_rel"]
+        flops = 2.0 * self.T * Bs * self.d * self.d
+        return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": cpu_threads(), "kind": "port",
+                "sample": f"{Bs} of {self.B} sequences, all {self.T} steps, serial recurrence (numpy fp32), {reps} reps",
+                "parity_max_rel": rel}
+
+
 class CopyStream(Form):
     """STREAM-style device copy of 2 GiB fp32: the measured-achievable HBM
     figure reported beside the vendor peak, and the known-size kernel the
@@ -524,7 +578,7 @@ class CopyStream(Form):
     dominant = step
 
 
-FORMS = {f.name: f for f in (C1WeightChain, C2SwiGLU, C3Attention, C4Retention, C5SSM, CopyStream)}
+FORMS = {f.name: f for f in (C1WeightChain, C2SwiGLU, C3Attention, C4Retention, C5SSM, DenseScan, CopyStream)}
 HEADLINE = "c2"
 
 
@@ -584,7 +638,7 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--forms", default="c1,c2,c3,c4,c5,copy")
+    ap.add_argument("--forms", default="c1,c2,c3,c4,c5,aff,copy")
     ap.add_argument("--cpu-budget", type=float, default=10.0,
                     help="seconds of CPU oracle work for the headline form (others get a third)")
     ap.add_argument("--no-cpu", action="store_true")

@@ -12,7 +12,10 @@ the library travels with the repository snapshot).  Compile flags:
 * per-source extras in ``SOURCE_FLAGS``: the retention scan keeps its MFMA
   accumulators in VGPRs (``-amdgpu-mfma-vgpr-form``) because its loop scales
   and converts them on the VALU every chunk, and AGPR-resident accumulators
-  would cost a copy in and out for each of those operations.
+  would cost a copy in and out for each of those operations; the dense
+  affine scan feeds each step's accumulators back as the next step's MFMA
+  B operands, which read VGPRs only (AGPR-resident accumulators cost 16
+  ``v_accvgpr_read`` per step, each waiting on its MFMA).
 
 Run ``python -m catopt_amd.build`` (or ``__graft_entry__.build()``).
 """
@@ -53,6 +56,7 @@ LINK_LIBS = ["-lhipblaslt"]
 
 SOURCE_FLAGS = {
     "retention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "scan_dense.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

@@ -116,20 +116,21 @@ __device__ __forceinline__ void load_a(f32x4* af, const float* __restrict__ At, 
   }
 }
 
+// Every lane loads (columns without b read slot 0's offsets, which exist);
+// the rows past d and the columns without b are zeroed where the values are
+// used (dense_step), not here: a select right after the load would make the
+// wave wait for the prefetch it has just issued.
 template <int DT, bool FULL>
-__device__ __forceinline__ void load_b(f32x4* bf, const float* __restrict__ bt, bool aff, int64_t d,
-                                       int lane) {
+__device__ __forceinline__ void load_b(f32x4* bf, const float* __restrict__ bt, int64_t d, int lane) {
 #pragma unroll
   for (int rb = 0; rb < DT; ++rb) {
     const int64_t row0 = rb * 16 + 4 * (lane >> 4);
-    f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (aff) {
-      if (FULL) {
-        v = *reinterpret_cast<const f32x4*>(bt + row0);
-      } else {
+    f32x4 v;
+    if (FULL) {
+      v = *reinterpret_cast<const f32x4*>(bt + row0);
+    } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = row0 + i < d ? bt[row0 + i] : 0.f;
-      }
+      for (int i = 0; i < 4; ++i) v[i] = bt[row0 + i < d ? row0 + i : d - 1];
     }
     bf[rb] = v;
   }
@@ -139,15 +140,26 @@ template <int DT, bool AT, bool FULL>
 __device__ __forceinline__ void load_step(Frag<DT, AT>& f, const DenseScan& s, int64_t t, int64_t g,
                                           const Col& col, int lane) {
   if (AT) load_a<DT, FULL>(f.a, s.A + t * s.lda_t + g * s.lda_p, s.d, lane);
-  load_b<DT, FULL>(f.b, s.b + t * s.ldb_t + col.p * s.ldb_p, col.aff, s.d, lane);
+  load_b<DT, FULL>(f.b, s.b + t * s.ldb_t + (col.aff ? col.p : 0) * s.ldb_p, s.d, lane);
 }
 
 // X ← A·X + b over one step (accumulator tiles x[kb], see the file header).
-template <int DT>
-__device__ __forceinline__ void dense_step(f32x4* x, const f32x4* af, const f32x4* bf) {
+// MASKED: b enters only columns with aff set and rows below d (chunk-map
+// identity columns, padded tiles); otherwise every column takes b as loaded
+// (columns past the group's end are never stored).
+template <int DT, bool MASKED>
+__device__ __forceinline__ void dense_step(f32x4* x, const f32x4* af, const f32x4* bf, bool aff, int64_t d,
+                                           int lane) {
   f32x4 nx[DT];
 #pragma unroll
-  for (int rb = 0; rb < DT; ++rb) nx[rb] = bf[rb];
+  for (int rb = 0; rb < DT; ++rb) {
+    if (MASKED) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) nx[rb][i] = (aff && rb * 16 + 4 * (lane >> 4) + i < d) ? bf[rb][i] : 0.f;
+    } else {
+      nx[rb] = bf[rb];
+    }
+  }
 #pragma unroll
   for (int kb = 0; kb < DT; ++kb) {
 #pragma unroll
@@ -186,13 +198,67 @@ struct Unroll {
   static constexpr int U = AT ? (DT == 1 ? 8 : DT == 2 ? 2 : 1) : (DT == 1 ? 8 : DT == 2 ? 4 : 2);
 };
 
+// What a launch computes (phases of the header's schedules):
+//   STREAM_FINAL — [0, T) from h0, the last state only;
+//   STREAM_ALL   — [0, T) from h0, every state and the last;
+//   MAP          — chunk blockIdx.y's map (M_c, v_c) from the identity;
+//   RESCAN       — chunk blockIdx.y from its carry-in, every state.
+enum class Mode { STREAM_FINAL, STREAM_ALL, MAP, RESCAN };
+
+// Steps [t0, t1) in blocks of U: two fragment sets alternate, so the loads
+// of block n+1 are issued before block n's products and consumed in place
+// (a copy from a prefetch buffer would make the compiler wait for the
+// prefetch at the copy).  The prefetch never branches: past the last block
+// it re-reads a block in range.
+template <int DT, bool AT, bool FULL, bool EMIT, bool MASKED>
+__device__ __forceinline__ void run_steps(f32x4* x, const f32x4* a_lti, const DenseScan& s, int64_t g,
+                                          const Col& col, int lane, int64_t t0, int64_t t1) {
+  constexpr int U = Unroll<DT, AT>::U;
+  const int64_t slot_stride = s.P * s.d * s.k;
+  Frag<DT, AT> fa[U], fb[U];
+  auto load_blk = [&](Frag<DT, AT>* f, int64_t tb) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) load_step<DT, AT, FULL>(f[u], s, tb + u, g, col, lane);
+  };
+  auto run_blk = [&](const Frag<DT, AT>* f, int64_t tb) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      dense_step<DT, MASKED>(x, AT ? f[u].a : a_lti, f[u].b, col.aff, s.d, lane);
+      if (EMIT) store_state<DT, FULL>(s.states + (tb + u) * slot_stride, x, s, col, lane);
+    }
+  };
+  const int64_t nblk = (t1 - t0) / U;
+  int64_t t = t0, blk = 0;
+  if (nblk > 0) load_blk(fa, t);
+  for (; blk + 2 <= nblk; blk += 2, t += 2 * U) {
+    load_blk(fb, t + U);
+    __builtin_amdgcn_sched_barrier(0);
+    run_blk(fa, t);
+    __builtin_amdgcn_sched_barrier(0);
+    load_blk(fa, blk + 2 < nblk ? t + 2 * U : t + U);
+    __builtin_amdgcn_sched_barrier(0);
+    run_blk(fb, t + U);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (blk < nblk) {
+    run_blk(fa, t);
+    t += U;
+  }
+  for (; t < t1; ++t) {
+    Frag<DT, AT> f;
+    load_step<DT, AT, FULL>(f, s, t, g, col, lane);
+    dense_step<DT, MASKED>(x, AT ? f.a : a_lti, f.b, col.aff, s.d, lane);
+    if (EMIT) store_state<DT, FULL>(s.states + t * slot_stride, x, s, col, lane);
+  }
+}
+
 // grid: x = ⌈jobs / kWaves⌉ (job = group x 16-column tile), y = chunk (or 1).
-// MAP = chunk maps of phase 1; otherwise state columns.  CHUNKED: the step
-// range is chunk blockIdx.y of the table (and the init state its carry-in);
-// else [0, T) from h0.
-template <int DT, bool AT, bool FULL, bool MAP, bool CHUNKED>
+template <int DT, bool AT, bool FULL, Mode M>
 __global__ __launch_bounds__(64 * kWaves) void aff_dense_scan(DenseScan s, const int64_t* __restrict__ cs,
                                                               int64_t T, int64_t tiles, int64_t jobs) {
+  constexpr bool MAP = M == Mode::MAP;
+  constexpr bool CHUNKED = M == Mode::MAP || M == Mode::RESCAN;
+  constexpr bool EMIT = M == Mode::STREAM_ALL || M == Mode::RESCAN;
   const int lane = threadIdx.x & 63;
   const int64_t job = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (job >= jobs) return;  // whole wave
@@ -201,12 +267,11 @@ __global__ __launch_bounds__(64 * kWaves) void aff_dense_scan(DenseScan s, const
   const int64_t chunk = CHUNKED ? (int64_t)blockIdx.y : 0;
   const int64_t t0 = CHUNKED ? cclamp_d(cs[chunk], T) : 0;
   const int64_t t1 = CHUNKED ? cclamp_d(cs[chunk + 1], T) : T;
-  constexpr int U = Unroll<DT, AT>::U;
 
   // initial state
   f32x4 x[DT];
   const float* init = s.h0;
-  if (!MAP && CHUNKED && chunk > 0) init = s.carry + (chunk - 1) * s.P * s.d * s.k;
+  if (M == Mode::RESCAN && chunk > 0) init = s.carry + (chunk - 1) * s.P * s.d * s.k;
 #pragma unroll
   for (int rb = 0; rb < DT; ++rb) {
 #pragma unroll
@@ -224,37 +289,7 @@ __global__ __launch_bounds__(64 * kWaves) void aff_dense_scan(DenseScan s, const
 
   f32x4 a_lti[AT ? 1 : DT * DT];
   if (!AT) load_a<DT, FULL>(a_lti, s.A + g * s.lda_p, s.d, lane);
-  const int64_t slot_stride = s.P * s.d * s.k;
-  const bool emit = !MAP && s.states != nullptr;
-
-  Frag<DT, AT> cur[U], nxt[U];
-  int64_t t = t0;
-  if (t + U <= t1) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) load_step<DT, AT, FULL>(cur[u], s, t + u, g, col, lane);
-  }
-  for (; t + U <= t1; t += U) {
-    const bool more = t + 2 * U <= t1;
-    if (more) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) load_step<DT, AT, FULL>(nxt[u], s, t + U + u, g, col, lane);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      dense_step<DT>(x, AT ? cur[u].a : a_lti, cur[u].b);
-      if (emit) store_state<DT, FULL>(s.states + (t + u) * slot_stride, x, s, col, lane);
-    }
-    if (more) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) cur[u] = nxt[u];
-    }
-  }
-  for (; t < t1; ++t) {
-    Frag<DT, AT> f;
-    load_step<DT, AT, FULL>(f, s, t, g, col, lane);
-    dense_step<DT>(x, AT ? f.a : a_lti, f.b);
-    if (emit) store_state<DT, FULL>(s.states + t * slot_stride, x, s, col, lane);
-  }
+  run_steps<DT, AT, FULL, EMIT, MAP || !FULL>(x, a_lti, s, g, col, lane, t0, t1);
 
   if (MAP) {
     if (!col.live) return;
@@ -293,11 +328,11 @@ WsLayout ws_layout(int64_t P, int64_t d, int64_t k, bool shared, int64_t nc) {
   return w;
 }
 
-template <int DT, bool AT, bool FULL, bool MAP, bool CHUNKED>
+template <int DT, bool AT, bool FULL, Mode M>
 void launch_one(const DenseScan& s, const int64_t* cs, int64_t T, int64_t tiles, int64_t jobs, int64_t ny,
                 hipStream_t st) {
   const dim3 grid((uint32_t)((jobs + kWaves - 1) / kWaves), (uint32_t)ny);
-  aff_dense_scan<DT, AT, FULL, MAP, CHUNKED><<<grid, dim3(64 * kWaves), 0, st>>>(s, cs, T, tiles, jobs);
+  aff_dense_scan<DT, AT, FULL, M><<<grid, dim3(64 * kWaves), 0, st>>>(s, cs, T, tiles, jobs);
 }
 
 template <int DT, bool AT, bool FULL>
@@ -310,7 +345,10 @@ int32_t dense_launch(DenseScan s, int64_t T, const int64_t* cs, int64_t nc, int3
   if (schedule == CATOPT_SCAN_AUTO) chunked = nc > 1 && T >= 256 && jobs_state < kFillWaves;
   if (jobs_state > 0x7fffffffLL * kWaves) return CATOPT_E_UNSUPPORTED;
   if (!chunked) {
-    launch_one<DT, AT, FULL, false, false>(s, cs, T, tiles_state, jobs_state, 1, st);
+    if (s.states)
+      launch_one<DT, AT, FULL, Mode::STREAM_ALL>(s, cs, T, tiles_state, jobs_state, 1, st);
+    else
+      launch_one<DT, AT, FULL, Mode::STREAM_FINAL>(s, cs, T, tiles_state, jobs_state, 1, st);
     CATOPT_LAUNCH_CHECK();
     return CATOPT_OK;
   }
@@ -325,7 +363,7 @@ int32_t dense_launch(DenseScan s, int64_t T, const int64_t* cs, int64_t nc, int3
   m.hf = nullptr;
   const int64_t tiles_map = s.shared ? (s.d + s.P + 15) / 16 : (s.d + 1 + 15) / 16;
   if (G * tiles_map > 0x7fffffffLL * kWaves) return CATOPT_E_UNSUPPORTED;
-  launch_one<DT, AT, FULL, true, true>(m, cs, T, tiles_map, G * tiles_map, nc, st);
+  launch_one<DT, AT, FULL, Mode::MAP>(m, cs, T, tiles_map, G * tiles_map, nc, st);
   CATOPT_LAUNCH_CHECK();
   // (2) carries: A = M_c, b = v_c over the n_chunks "steps"
   DenseScan c = s;
@@ -337,14 +375,17 @@ int32_t dense_launch(DenseScan s, int64_t T, const int64_t* cs, int64_t nc, int3
   c.ldb_p = s.d;
   c.states = s.states ? wf + w.carry : nullptr;
   // FULL implies d = 16·DT: the workspace rows are then 16-byte aligned too
-  launch_one<DT, true, FULL, false, false>(c, cs, nc, tiles_state, jobs_state, 1, st);
+  if (c.states)
+    launch_one<DT, true, FULL, Mode::STREAM_ALL>(c, cs, nc, tiles_state, jobs_state, 1, st);
+  else
+    launch_one<DT, true, FULL, Mode::STREAM_FINAL>(c, cs, nc, tiles_state, jobs_state, 1, st);
   CATOPT_LAUNCH_CHECK();
   // (3) prefix states from each chunk's carry-in
   if (s.states) {
     DenseScan r = s;
     r.carry = wf + w.carry;
     r.hf = nullptr;
-    launch_one<DT, AT, FULL, false, true>(r, cs, T, tiles_state, jobs_state, nc, st);
+    launch_one<DT, AT, FULL, Mode::RESCAN>(r, cs, T, tiles_state, jobs_state, nc, st);
     CATOPT_LAUNCH_CHECK();
   }
   return CATOPT_OK;
