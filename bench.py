@@ -514,7 +514,7 @@ class DenseScan(Form):
                 "T=1024 steps, offsets b_t (T,B,64,1), final state (B,64,1), fp32")
     peak = PEAK["fp32_tflops"]
     work = dom_work = 2.0 * T * B * d * d
-    dom_name = dom_key = "aff_dense_scan<4, false, true, false, false>"
+    dom_name = dom_key = "aff_dense_scan<4, false, true, 0>"
 
     def setup(self, dev):
         import torch

@@ -203,7 +203,10 @@ struct Unroll {
 //   STREAM_ALL   — [0, T) from h0, every state and the last;
 //   MAP          — chunk blockIdx.y's map (M_c, v_c) from the identity;
 //   RESCAN       — chunk blockIdx.y from its carry-in, every state.
-enum class Mode { STREAM_FINAL, STREAM_ALL, MAP, RESCAN };
+// (plain ints, so kernel names stay readable in profiles: aff_dense_scan<DT, AT, FULL, MODE>)
+namespace Mode {
+constexpr int STREAM_FINAL = 0, STREAM_ALL = 1, MAP = 2, RESCAN = 3;
+}
 
 // Steps [t0, t1) in blocks of U: two fragment sets alternate, so the loads
 // of block n+1 are issued before block n's products and consumed in place
@@ -253,7 +256,7 @@ __device__ __forceinline__ void run_steps(f32x4* x, const f32x4* a_lti, const De
 }
 
 // grid: x = ⌈jobs / kWaves⌉ (job = group x 16-column tile), y = chunk (or 1).
-template <int DT, bool AT, bool FULL, Mode M>
+template <int DT, bool AT, bool FULL, int M>
 __global__ __launch_bounds__(64 * kWaves) void aff_dense_scan(DenseScan s, const int64_t* __restrict__ cs,
                                                               int64_t T, int64_t tiles, int64_t jobs) {
   constexpr bool MAP = M == Mode::MAP;
@@ -328,7 +331,7 @@ WsLayout ws_layout(int64_t P, int64_t d, int64_t k, bool shared, int64_t nc) {
   return w;
 }
 
-template <int DT, bool AT, bool FULL, Mode M>
+template <int DT, bool AT, bool FULL, int M>
 void launch_one(const DenseScan& s, const int64_t* cs, int64_t T, int64_t tiles, int64_t jobs, int64_t ny,
                 hipStream_t st) {
   const dim3 grid((uint32_t)((jobs + kWaves - 1) / kWaves), (uint32_t)ny);
