@@ -147,6 +147,47 @@ def om_elem_dense(s, v, *a, **kw):
     return m, e.sum(dim=-1, keepdim=True), _matmul(e, v)
 
 
+def _omd_elem(s, a, b, *x, **kw):
+    """``_omd_elem`` (xcarrier.py:380-400): ``(m, l, e@a, e@b)``; a coefficient
+    ``a`` of 3 or more axes is the dense fibre ``(…,K,d,i)`` (key axis
+    contracted through a ``(d·i)``-flattened view)."""
+    m = s.amax(dim=-1, keepdim=True)
+    e = torch.exp(s - m)
+    lv = e.sum(dim=-1, keepdim=True)
+    if a.dim() >= 3:
+        d, i = a.shape[-2], a.shape[-1]
+        ea = _matmul(e, a.reshape(*a.shape[:-2], d * i))
+        return m, lv, ea.reshape(*ea.shape[:-1], d, i), _matmul(e, b)
+    return m, lv, _matmul(e, a), _matmul(e, b)
+
+
+def _omd_compose(f, g, *a, **kw):
+    """``_omd_compose`` (xcarrier.py:407-440): the om combine applied to both
+    numerator parts; run as one om combine over the concatenated numerator."""
+    m1, l1, fa1, fb1 = f
+    m2, l2, fa2, fb2 = g
+    lead = m1.dim()
+    shape_a = fa1.shape
+    fl = lambda fa: fa.reshape(*fa.shape[:lead - 1], -1)  # noqa: E731  (…,Tq,d[,i]) -> (…,Tq,·)
+    n1 = torch.cat([fl(fa1), fb1], dim=-1)
+    n2 = torch.cat([fl(fa2), fb2], dim=-1)
+    m, lv, acc = _om_compose((m1, l1, n1), (m2, l2, n2))
+    wa = n1.shape[-1] - fb1.shape[-1]
+    return m, lv, acc[..., :wa].reshape(shape_a), acc[..., wa:]
+
+
+def _om_elem_affd(s, a, b, h, *x, **kw):
+    """``_om_elem_affd`` (xcarrier.py:348-359): ``(m, l, (e@a)⊙h + e@b)``."""
+    m, lv, ea, eb = _omd_elem(s, a, b)
+    return m, lv, ea * h + eb
+
+
+def _om_elem_aff(s, A, b, h, *x, **kw):
+    """``_om_elem_aff`` (xcarrier.py:362-377): ``(m, l, (e@A)@h + e@b)``."""
+    m, lv, ea, eb = _omd_elem(s, A, b)
+    return m, lv, _matmul(ea, h) + eb
+
+
 def _decay(g, *a, **kw):
     t = int(attr_of(kw, "t", default=0) or 0)
     g = torch.as_tensor(g)
@@ -234,6 +275,14 @@ HIP_BINDINGS: dict[str, Callable] = {
     "applyd": lambda f, h, *a, **kw: f[0] * h + f[1],
     "affd_a": lambda f, *a, **kw: f[0],
     "affd_b": lambda f, *a, **kw: f[1],
+    # ---- deferred-affine om carrier (xcarrier.py:380-472)
+    "omd_elem": _omd_elem,
+    "omd": lambda m, lv, fa, fb, *a, **kw: (m, lv, fa, fb),
+    "omd_compose": _omd_compose,
+    "omd_apply": lambda f, h, *a, **kw: (f[2] * h + f[3]) / f[1],
+    "omd_applym": lambda f, h, *a, **kw: (_matmul(f[2], h) + f[3]) / f[1],
+    "om_elem_affd": _om_elem_affd,
+    "om_elem_aff": _om_elem_aff,
     # ---- dense affine monoid (torch_bridge.py:1873-1881, xcarrier.py:460-472)
     "aff": lambda A, b_, *x, **kw: (A, b_),
     "aff_compose": lambda f, g, *a, **kw: (_matmul(f[0], g[0]), _matmul(f[0], g[1]) + f[1]),

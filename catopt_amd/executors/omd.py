@@ -1,0 +1,386 @@
+"""Deferred-affine attention (omd) executor.
+
+The counterpart of ``BatchedOmdModule`` / ``build_omd_plan`` (luisfuturist/
+catopt ``packages/catopt-carriers/src/catopt_carriers/omd_lower.py:213-558,
+562-1019``).  The term is softmax attention over values that are affine in
+one shared state ``h`` — attention over the states of a scan:
+
+    omd_apply(<omd_compose tree of omd_elem(s_i, a_i, b_i)>, h)      (diagonal)
+    omd_applym(<omd_compose tree of omd_elem(s_i, A_i, b_i)>, h)     (dense)
+
+with ``omd_elem(s, a, b) = (m, l, e@a, e@b)``, ``e = exp(s − m)``, and the
+readout ``(fa ⊙ h + fb) / l`` (``fa @ h`` for the dense fibre;
+``xcarrier.py:380-454``).  The coefficient arrays ``a_i``, ``b_i`` are
+usually ``stack(affd_a f_j)`` / ``stack(affd_b f_j)`` over the prefixes
+``f_j = affd_compose(leaf_j, f_{j-1})`` of one scan — O(T²) unrolled terms
+for a generic evaluator.
+
+Plan (as in the reference): the projections of maps inside the leaves
+(``affd_a``/``affd_b``/``aff_A``/``aff_b``, alone or stacked) are collected;
+when every projected map is a prefix of ONE leaf sequence of one carrier,
+the plan is ``chain`` and all prefix maps come from the HIP scan kernels in
+one pass, then answer every projection and stack by gather (seeded into the
+evaluator's memo, so the score terms around them evaluate unchanged).  Maps
+of any other bracketing (``forest``) are evaluated by the generic module.
+
+Execution on the device:
+
+* prefix maps — diagonal: one ``catopt_hip_affd_scan`` over ``[a | a]``
+  lanes from ``[1 | 0]`` with offsets ``[0 | b]`` gives
+  ``[∏a | prefix b]``; dense: two ``catopt_hip_aff_scan`` launches
+  (``I`` under the maps alone, ``0`` under the maps and offsets);
+* leaves — ``m``, ``l`` and one HIP GEMM ``e @ [a | b]`` per leaf (the two
+  numerator parts share the exponentials);
+* the compose tree — left-folded in product order by the HIP ``om_compose``
+  kernel over the concatenated numerator ``[fa | fb]`` (the omd combine is
+  om's applied to each part, ``xcarrier.py:407-440``; the ``isfinite``
+  guard of fully masked blocks is in the kernel);
+* the readout on the device.
+
+Carriers are fp32 (bf16 operands are widened); the result has the promoted
+operand dtype.  Other dtypes, host tensors, and shape surprises run the
+embedded generic module, counted in ``fallbacks`` (as the reference's
+``_forward_impl`` does on any exception); kernel errors raise.
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+import torch
+from torch import nn
+
+from .. import _lib as L
+from .. import kernels as K
+from ..bindings import _om_compose, attr_of
+from ..evaluator import HipIRModule
+from ..ir import IR, Op, is_op
+from .base import HipExecutorBase
+from .scan import prefix_chunk_table
+
+__all__ = ["HipOmdModule", "build_omd_plan", "is_omd_term", "to_batched_omd_module"]
+
+#: projection op -> (component, carrier)
+_PROJ = {"affd_a": (0, "diag"), "affd_b": (1, "diag"), "aff_A": (0, "dense"), "aff_b": (1, "dense")}
+_COMPOSE = {"affd_compose": "diag", "aff_compose": "dense"}
+_LEAF = {"aff_diag": "diag", "aff": "dense"}
+
+
+def _omd_leaves(t: Any) -> list | None:
+    """Leaves of an ``omd_compose`` tree in product order (with multiplicity)."""
+    out: list = []
+    stack = [t]
+    while stack:
+        n = stack.pop()
+        if is_op(n, "omd_compose", 2):
+            stack.append(n.args[1])
+            stack.append(n.args[0])
+        elif is_op(n, "omd_elem", 3) or is_op(n, "omd", 4):
+            out.append(n)
+        else:
+            return None
+    return out
+
+
+def is_omd_term(root: Any) -> bool:
+    """``omd_apply`` / ``omd_applym`` over an omd tree (``omd_lower.py:153-164``)."""
+    return (isinstance(root, Op) and root.op in ("omd_apply", "omd_applym") and len(root.args) == 2
+            and _omd_leaves(root.args[0]) is not None)
+
+
+def _app_order(mp: Any) -> list:
+    """Leaf maps of a compose term in application order (``compose(f, g)``
+    applies ``g`` first; ``omd_lower.py:167-186``)."""
+    out: list = []
+    stack = [mp]
+    while stack:
+        u = stack.pop()
+        if isinstance(u, Op) and u.op in _COMPOSE and len(u.args) == 2:
+            stack.append(u.args[0])
+            stack.append(u.args[1])
+        else:
+            out.append(u)
+    return out
+
+
+def _step_index(t: Any) -> tuple | None:
+    if is_op(t, "select", 1):
+        return t.args[0], int(attr_of(t.attrs, "dim", default=0)), int(attr_of(t.attrs, "index", default=0))
+    if is_op(t, "getitem", 1):
+        ix = t.attrs.get("index")
+        if isinstance(ix, int) and not isinstance(ix, bool):
+            return t.args[0], 0, ix
+    return None
+
+
+def _part_gather(leaves: list, slot: int) -> tuple | None:
+    """``(base, dim, indices)`` when every leaf's part ``slot`` indexes one base."""
+    idx = [_step_index(lf.args[slot]) for lf in leaves]
+    if any(i is None for i in idx):
+        return None
+    base, dim = idx[0][0], idx[0][1]
+    if any(not (i[0] is base or i[0] == base) or i[1] != dim for i in idx):
+        return None
+    return base, dim, [i[2] for i in idx]
+
+
+def build_omd_plan(root: Any) -> dict | None:
+    if not is_omd_term(root):
+        return None
+    F, h = root.args
+    leaves = _omd_leaves(F)
+    # ---- projections of maps inside the leaves (and h) -------------------
+    projs: list = []   # (node, component, map)
+    stacks: list = []  # (node, component, [maps], dim)
+    maps: dict = {}    # map term -> carrier
+    bad = False
+    seen: set = set()
+
+    def register(mp: Any, dom: str) -> None:
+        nonlocal bad
+        if maps.setdefault(mp, dom) != dom:
+            bad = True
+
+    def scan(t: Any) -> None:
+        if not isinstance(t, Op) or id(t) in seen:
+            return
+        seen.add(id(t))
+        info = _PROJ.get(t.op)
+        if info is not None and len(t.args) == 1:
+            projs.append((t, info[0], t.args[0]))
+            register(t.args[0], info[1])
+            return
+        if t.op == "stack" and t.args and all(isinstance(c, Op) and c.op in _PROJ and len(c.args) == 1
+                                              for c in t.args):
+            infos = {_PROJ[c.op] for c in t.args}
+            if len(infos) == 1:
+                ci, dom = next(iter(infos))
+                for c in t.args:
+                    register(c.args[0], dom)
+                    projs.append((c, ci, c.args[0]))
+                stacks.append((t, ci, [c.args[0] for c in t.args], int(attr_of(t.attrs, "dim", default=0))))
+                return
+        if t.op in _COMPOSE or t.op in _LEAF:
+            return  # map structure in a tensor position stays with the generic module
+        for a in t.args:
+            scan(a)
+
+    for lf in leaves:
+        for a in lf.args:
+            scan(a)
+    scan(h)
+    if bad:
+        return None
+    plan: dict = {"apply": root.op, "h": h, "leaves": leaves, "map_mode": None,
+                  "proj_seeds": [], "stack_seeds": [], "map_seeds": []}
+    if not maps:
+        return plan
+    # ---- chain: every projected map a prefix of one leaf sequence ---------
+    seqs = {mp: _app_order(mp) for mp in maps}  # terms are content-keyed (cached hashes)
+    base = max(seqs.values(), key=len)
+    doms = set(maps.values())
+    dom = next(iter(doms))
+    leaf_op = {"diag": "aff_diag", "dense": "aff"}[dom]
+    chain = (len(doms) == 1
+             and all(len(s) <= len(base) and all(x is y or x == y for x, y in zip(s, base)) for s in seqs.values())
+             and all(is_op(lf, leaf_op, 2) for lf in base))
+    if not chain:
+        plan["map_mode"] = "forest"
+        return plan
+    pos = {mp: len(s) - 1 for mp, s in seqs.items()}
+    plan.update(map_mode="chain", chain_domain=dom, chain_leaves=base,
+                chain_a_gather=_part_gather(base, 0), chain_b_gather=_part_gather(base, 1))
+    plan["proj_seeds"] = [(node, ci, pos[mp]) for node, ci, mp in projs]
+    plan["stack_seeds"] = [(node, ci, [pos[mp] for mp in mps], dim) for node, ci, mps, dim in stacks]
+    plan["map_seeds"] = [(mp, pos[mp]) for mp in maps]
+    return plan
+
+
+def _kernel_dtype(t: Any) -> bool:
+    return isinstance(t, torch.Tensor) and t.device.type == "cuda" and t.dtype in (torch.float32, torch.bfloat16)
+
+
+class HipOmdModule(HipExecutorBase, nn.Module):
+    """Planned executor for ``omd_apply[m](<omd tree>, h)`` (module docstring)."""
+
+    def __init__(self, ir: IR, param_values: dict | None = None, *, eval_mod: HipIRModule | None = None,
+                 device: Any = None, ops=None) -> None:
+        super().__init__()
+        self.eval_mod = eval_mod if eval_mod is not None else HipIRModule(ir, param_values, device=device, ops=ops)
+        self._inputs = list(ir.inputs)
+        self._const_cache: dict = {}
+        self.fallbacks = 0
+        self._plan = build_omd_plan(self.eval_mod._root)
+        self._init_graph_state()
+
+    @property
+    def map_mode(self) -> str | None:
+        return None if self._plan is None else self._plan["map_mode"]
+
+    # ------------------------------------------------------------ prefix maps
+
+    def _chain_parts(self, ev) -> tuple:
+        """Leaf ``(a, b)`` parts of the chain, step-major."""
+        p = self._plan
+        out = []
+        for slot in (0, 1):
+            g = p["chain_a_gather"] if slot == 0 else p["chain_b_gather"]
+            t = None
+            if g is not None:
+                base, dim, idx = g
+                bt = ev(base)
+                if idx == list(range(bt.shape[dim])):
+                    t = bt.movedim(dim, 0)
+                else:
+                    ix = self._cached(("idx", tuple(idx)), bt,
+                                      lambda x: torch.tensor(idx, dtype=torch.long, device=x.device),
+                                      dtype=torch.long)
+                    t = bt.index_select(dim, ix).movedim(dim, 0)
+            else:
+                t = torch.stack([torch.as_tensor(ev(lf.args[slot])) for lf in p["chain_leaves"]])
+            out.append(t)
+        return out[0], out[1]
+
+    def _prefix_maps(self, A: torch.Tensor, B: torch.Tensor) -> tuple:
+        """Every prefix map ``f_t = leaf_t ∘ … ∘ leaf_0`` of the chain (fp32)."""
+        T = A.shape[0]
+        table = prefix_chunk_table(T)  # lets the kernels go chunk-parallel when the lanes are few
+        if self._plan["chain_domain"] == "diag":
+            if A.shape != B.shape:
+                raise ValueError("diagonal chain parts differ in shape")
+            S = A[0].numel()
+            a2 = torch.cat([A.reshape(T, S), A.reshape(T, S)], dim=1)
+            u2 = torch.cat([torch.zeros_like(B.reshape(T, S)), B.reshape(T, S)], dim=1)
+            h2 = torch.cat([torch.ones(S, dtype=A.dtype, device=A.device),
+                            torch.zeros(S, dtype=A.dtype, device=A.device)])
+            states, _ = K.affd_scan(a2, u2, h2, table, states=True)
+            return states[:, :S].reshape(A.shape), states[:, S:].reshape(B.shape)
+        # dense: A (T, *P, d, d), B (T, *P, d)
+        d = A.shape[-1]
+        if A.shape[-2] != d or B.shape != A.shape[:-1]:
+            raise ValueError("dense chain parts do not form square maps with matching offsets")
+        pshape = A.shape[1:-2]
+        Pn = int(torch.Size(pshape).numel())
+        A4 = A.reshape(T, Pn, d, d)
+        eye = torch.eye(d, dtype=torch.float32, device=A.device).expand(Pn, d, d)
+        zero_b = torch.zeros((T, 1, d), dtype=torch.float32, device=A.device)
+        M, _ = K.aff_scan(A4, zero_b, eye, table, states=True)                     # X_t = A_t X, X = I
+        v, _ = K.aff_scan(A4, B.reshape(T, Pn, d), torch.zeros((Pn, d, 1), dtype=torch.float32, device=A.device),
+                          table, states=True)                                       # x_t = A_t x + b_t
+        return M.reshape(A.shape), v.reshape(B.shape)
+
+    def _seed(self, memo: dict, Pa: torch.Tensor, Pb: torch.Tensor) -> None:
+        parts = (Pa, Pb)
+        for node, ci, i in self._plan["proj_seeds"]:
+            memo[node] = parts[ci][i]
+        for mp, i in self._plan["map_seeds"]:
+            memo[mp] = (Pa[i], Pb[i])
+        for node, ci, idx, dim in self._plan["stack_seeds"]:
+            src = parts[ci]
+            ix = self._cached(("stk", tuple(idx)), src,
+                              lambda x: torch.tensor(idx, dtype=torch.long, device=x.device), dtype=torch.long)
+            t = src.index_select(0, ix)
+            dn = dim % t.dim()
+            memo[node] = t.movedim(0, dn) if dn else t
+
+    # ---------------------------------------------------------------- leaves
+
+    @staticmethod
+    def _leaf_carrier(s: torch.Tensor, a: torch.Tensor, b: torch.Tensor) -> tuple:
+        """``(m, l, e @ [a | b])`` in fp32, the dense ``a`` flattened; returns
+        the numerator width of ``fa`` and its trailing shape too."""
+        s32 = s.float()
+        m = s32.amax(dim=-1, keepdim=True)
+        e = torch.exp(s32 - m)
+        lv = e.sum(dim=-1, keepdim=True)
+        if a.dim() >= 3:  # dense fibre (xcarrier.py:393-399)
+            d, i = a.shape[-2], a.shape[-1]
+            af = a.reshape(*a.shape[:-2], d * i)
+            tail = (d, i)
+        else:
+            af, tail = a, (a.shape[-1],)
+        V = torch.cat([af.float(), b.float().expand(*af.shape[:-1], b.shape[-1])], dim=-1)
+        num = K.matmul(e, V) if e.dim() >= 2 and V.dim() >= 2 else e @ V
+        return m, lv, num, af.shape[-1], tail
+
+    def _forward_impl(self, *xs: Any) -> Any:
+        p = self._plan
+        if p is None:
+            return self.eval_mod(*xs)
+        x, env = self._input_env(xs)
+        memo: dict = {}
+        ev = self.ev_factory(env, x, memo)
+        try:
+            return self._run(ev, memo)
+        except (L.HipKernelError, L.HipExtensionMissing):
+            raise
+        except (ValueError, IndexError, TypeError, RuntimeError, _Decline):
+            self.fallbacks += 1
+            return self.eval_mod(*xs)
+
+    def _run(self, ev, memo: dict) -> torch.Tensor:
+        p = self._plan
+        dtypes = []
+        seeded: set = set()
+        if p["map_mode"] == "chain":
+            A, B = self._chain_parts(ev)
+            if not (_kernel_dtype(A) and _kernel_dtype(B)):
+                raise _Decline()
+            Pa, Pb = self._prefix_maps(A, B)
+            self._seed(memo, Pa, Pb)
+            # the result's dtype follows the chain's operands, not the fp32 prefix maps
+            dtypes += [A.dtype, B.dtype]
+            seeded = {id(node) for node, *_ in p["proj_seeds"] + p["stack_seeds"]}
+        state = None
+        width = tail = None
+        for lf in p["leaves"]:
+            if lf.op == "omd_elem":
+                s, a, b = ev(lf.args[0]), ev(lf.args[1]), ev(lf.args[2])
+                if not all(_kernel_dtype(t) for t in (s, a, b)):
+                    raise _Decline()
+                dtypes.append(s.dtype)
+                dtypes += [t.dtype for t, arg in ((a, lf.args[1]), (b, lf.args[2])) if id(arg) not in seeded]
+                m, lv, num, wa, tl = self._leaf_carrier(s, a, b)
+            else:
+                m, lv, fa, fb = (ev(t) for t in lf.args)
+                if not all(_kernel_dtype(t) for t in (m, lv, fa, fb)):
+                    raise _Decline()
+                dtypes += [fa.dtype, fb.dtype]
+                lead = m.dim()
+                tl = tuple(fa.shape[lead - 1:])
+                fa_f = fa.reshape(*fa.shape[:lead - 1], -1).float()
+                wa = fa_f.shape[-1]
+                num = torch.cat([fa_f, fb.float()], dim=-1)
+                m, lv = m.float(), lv.float()
+            if width is None:
+                width, tail = wa, tl
+            elif (wa, tl) != (width, tail):
+                raise _Decline()
+            e = (m, lv, num)
+            if state is not None and (state[0].shape != m.shape or state[2].shape != num.shape):
+                raise _Decline()
+            state = e if state is None else _om_compose(state, e)
+        m, lv, num = state
+        fa = num[..., :width].reshape(*num.shape[:-1], *tail)
+        fb = num[..., width:]
+        h = ev(p["h"])
+        if not _kernel_dtype(h):
+            raise _Decline()
+        out_dtype = h.dtype
+        for dt in dtypes:
+            out_dtype = torch.promote_types(out_dtype, dt)
+        hf = h.float()
+        if p["apply"] == "omd_apply":
+            out = (fa * hf + fb) / lv
+        else:
+            out = (K.matmul(fa, hf) + fb) / lv
+        return out.to(out_dtype)
+
+
+class _Decline(Exception):
+    """The batched path does not take these operands (the generic module runs)."""
+
+
+def to_batched_omd_module(ir: IR, param_values: dict | None = None, **kw) -> HipOmdModule:
+    """Always a :class:`HipOmdModule` (check ``is_batched``), ``omd_lower.py:1022-1033``."""
+    return HipOmdModule(ir, param_values, **kw)

@@ -23,7 +23,9 @@ can feed this package's sink exactly what the orchestrator would route:
 * :func:`linear_recurrence_form` / :func:`dense_scan_form` /
   :func:`dense_scan_prefix_form` — the dense affine monoid: ``apply`` over a
   balanced ``aff_compose`` tree (the depth-extracted ``LinearRecurrence``
-  term) and the stacked all-prefix form (``xcarrier.py:2276-2293``).
+  term) and the stacked all-prefix form (``xcarrier.py:2276-2293``);
+* :func:`omd_scan_attention_form` — softmax attention over a scan's states
+  as the deferred-affine ``omd_apply`` term (``omd_lower.py:1-12``).
 
 Each returns ``(IR, param_shapes)``; parameter values come from the caller.
 """
@@ -45,6 +47,7 @@ __all__ = [
     "linear_recurrence_form",
     "dense_scan_form",
     "dense_scan_prefix_form",
+    "omd_scan_attention_form",
 ]
 
 mk = Op.make
@@ -241,3 +244,36 @@ def dense_scan_prefix_form(T: int, d: int, *, time_varying: bool = True, dim: in
     SA = mk("stack", *[mk("aff_A", f) for f in fs], dim=dim)
     SB = mk("stack", *[mk("aff_b", f) for f in fs], dim=dim)
     return IR(mk("apply", mk("aff", SA, SB), h), [A, b, h]), {}
+
+
+def omd_scan_attention_form(T: int, d: int, Tq: int, blocks: int, dk: int = 16, *,
+                            dense: bool = False) -> tuple[IR, dict]:
+    """Softmax attention over the states of a scan, as the cross-carrier lift
+    delivers it (omd_lower.py:1-12, the ``_ScanAttn`` model of
+    tests/test_omd_lower.py:72-124): ``omd_apply(<balanced omd_compose tree
+    of omd_elem(s_i, stack(affd_a f_j), stack(affd_b f_j))>, h)`` over key
+    blocks ``i``, with ``s_i = q · chunk(k, i)ᵀ`` and the prefix chain
+    ``f_j = affd_compose(aff_diag(a[j], x[j]), f_{j-1})``.  ``dense`` uses
+    ``aff`` maps ``A (T, d, d)`` and ``omd_applym``."""
+    if T % blocks:
+        raise ValueError("blocks must divide T")
+    q = Var("q", TensorType((Tq, dk)))
+    k = Var("k", TensorType((T, dk)))
+    a = Var("a", TensorType((T, d, d) if dense else (T, d)))
+    x = Var("x", TensorType((T, d)))
+    h = Var("h", TensorType((d,)))
+    leaf_op, comp, pa, pb = ("aff", "aff_compose", "aff_A", "aff_b") if dense else \
+        ("aff_diag", "affd_compose", "affd_a", "affd_b")
+    fs = []
+    for j in range(T):
+        leaf = mk(leaf_op, mk("select", a, dim=0, index=j), mk("select", x, dim=0, index=j))
+        fs.append(leaf if j == 0 else mk(comp, leaf, fs[-1]))
+    C = T // blocks
+    elems = []
+    for i in range(blocks):
+        blk = fs[i * C:(i + 1) * C]
+        s = mk("matmul", q, mk("transpose", mk("chunk", k, chunks=blocks, dim=0, index=i), dim0=0, dim1=1))
+        elems.append(mk("omd_elem", s, mk("stack", *[mk(pa, f) for f in blk], dim=0),
+                        mk("stack", *[mk(pb, f) for f in blk], dim=0)))
+    root = mk("omd_applym" if dense else "omd_apply", _balanced(elems, "omd_compose"), h)
+    return IR(root, [q, k, a, x, h]), {}

@@ -9,8 +9,8 @@ It presents the reference's ``Sink`` port (luisfuturist/catopt
 * ``ops`` — the binding registry (:class:`~catopt_amd.bindings.HipOpTable`);
 * ``executors`` — the ordered ``ExecutorSpec`` table; mapping order is
   routing order and carrier executors precede the generic one
-  (adapters.py:197-283 orders ``om_decayed_chunked, scan, om_batched, …,
-  generic``);
+  (adapters.py:197-283 orders ``om_decayed_chunked, scan, om_batched,
+  omd_batched, om_streaming, …, generic``);
 * ``lower(ir, params)`` — the generic executor;
 * ``verify(ref, opt, inputs, rtol, atol)`` — the global relative-error gate
   ``max|ref − out| / (max|ref| + 1e-8) < rtol`` (``report.py:128-207``).
@@ -38,9 +38,12 @@ from .evaluator import HipIRModule
 from .executors import (
     HipChunkedDecayModule,
     HipOMModule,
+    HipOmdModule,
     HipScanModule,
+    HipStreamingOMModule,
     is_decayed_term,
     is_om_term,
+    is_omd_term,
     is_scan_term,
 )
 from .ir import IR
@@ -140,7 +143,18 @@ class HipSink:
             ("om_batched", ExecutorSpec(
                 "om_batched", planned(HipOMModule), is_om_term,
                 lambda m: bool(getattr(m, "is_batched", False)),
-                (frozenset({"om_apply"}), frozenset({"om_compose"}), frozenset({"om_elem"})))),
+                (frozenset({"om_apply"}), frozenset({"om_compose"}), frozenset({"om", "om_elem"})))),
+            ("omd_batched", ExecutorSpec(
+                "omd_batched", planned(HipOmdModule), is_omd_term,
+                lambda m: bool(getattr(m, "is_batched", False)),
+                (frozenset({"omd_apply", "omd_applym"}), frozenset({"omd_compose"}),
+                 frozenset({"omd", "omd_elem"})))),
+            # after om_batched with the same acceptance, as in the reference:
+            # never the routed choice, selectable by name
+            ("om_streaming", ExecutorSpec(
+                "om_streaming", planned(HipStreamingOMModule), is_om_term,
+                lambda m: bool(getattr(m, "is_streaming", False)),
+                (frozenset({"om_apply"}), frozenset({"om_compose"}), frozenset({"om", "om_elem"})))),
             ("generic", ExecutorSpec(
                 "generic", lambda ir, params=None: self.lower(ir, params), lambda t: True,
                 lambda m: True, None)),

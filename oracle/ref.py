@@ -48,6 +48,10 @@ __all__ = [
     "fused_dense_levels",
     "serial_aff_scan",
     "aff_chunked_scan",
+    "omd_elem",
+    "omd_compose",
+    "omd_apply",
+    "omd_applym",
 ]
 
 _REL_FLOOR = 1e-8
@@ -605,3 +609,55 @@ def aff_chunked_scan(A, b, h0, table):
             hh = At(t) @ hh + b[t][..., None]
             out[t] = hh
     return out, h
+
+
+# ---------------------------------------------------------------- deferred-affine om (omd)
+
+
+def omd_elem(s, a, b):
+    """``_omd_elem`` (xcarrier.py:380-400): the om triple of the scores ``s``
+    over values affine in a symbolic state, ``v_k = a_k ⊙ h + b_k`` (diagonal
+    fibre, ``a (K,d)``) or ``v_k = A_k @ h + b_k`` (dense fibre, any ``a`` of
+    3 or more axes, ``(…,K,d,i)``): ``(m, l, e@a, e@b)`` with
+    ``e = exp(s − m)``; the dense ``e@A`` contracts the key axis of ``A``."""
+    s, a, b = np.asarray(s), np.asarray(a), np.asarray(b)
+    m = s.max(axis=-1, keepdims=True)
+    e = np.exp(s - m)
+    l_ = e.sum(axis=-1, keepdims=True)
+    if a.ndim >= 3:  # the reference's fibre test: a 3-D+ coefficient is dense
+        d, i = a.shape[-2], a.shape[-1]
+        ea = (e @ a.reshape(*a.shape[:-2], d * i)).reshape(*e.shape[:-1], d, i)
+        return m, l_, ea, e @ b
+    return m, l_, e @ a, e @ b
+
+
+def omd_compose(f, g):
+    """``_omd_compose`` (xcarrier.py:407-440): both numerator parts rescale
+    like om's ``a``, with the same ``isfinite`` guard (a block whose max is
+    −inf contributes nothing)."""
+    m1, l1, fa1, fb1 = (np.asarray(t) for t in f)
+    m2, l2, fa2, fb2 = (np.asarray(t) for t in g)
+    mx = np.maximum(m1, m2)
+    fin1, fin2 = np.isfinite(m1), np.isfinite(m2)
+    with np.errstate(invalid="ignore", over="ignore"):
+        e1 = np.where(fin1, np.exp(np.where(fin1, m1 - mx, 0.0)), 0.0)
+        e2 = np.where(fin2, np.exp(np.where(fin2, m2 - mx, 0.0)), 0.0)
+
+    def lift(e, x):  # row weight (…,Tq,1) onto a numerator with trailing axes
+        return e.reshape(*e.shape, *([1] * (x.ndim - e.ndim)))
+
+    l_ = np.where(fin1, l1 * e1, 0.0) + np.where(fin2, l2 * e2, 0.0)
+    fa = np.where(lift(fin1, fa1), fa1 * lift(e1, fa1), 0.0) + np.where(lift(fin2, fa2), fa2 * lift(e2, fa2), 0.0)
+    fb = np.where(fin1, fb1 * e1, 0.0) + np.where(fin2, fb2 * e2, 0.0)
+    return mx, l_, fa, fb
+
+
+def omd_apply(f, h):
+    """``_omd_apply`` (xcarrier.py:443-445): ``(fa ⊙ h + fb) / l``."""
+    return (np.asarray(f[2]) * h + f[3]) / f[1]
+
+
+def omd_applym(f, h):
+    """``_omd_applym`` (xcarrier.py:448-454): ``(fa @ h + fb) / l``, the
+    dense fibre's map input axis contracted with ``h``."""
+    return (np.asarray(f[2]) @ h + f[3]) / f[1]

@@ -65,6 +65,27 @@ def _om_elem(s, v, *a, **kw):
     return m, e.sum(dim=-1, keepdim=True), e @ v
 
 
+def _omd_elem(s, a, b, *x, **kw):
+    m = s.amax(dim=-1, keepdim=True)
+    e = torch.exp(s - m)
+    if a.dim() >= 3:
+        d, i = a.shape[-2], a.shape[-1]
+        ea = (e @ a.reshape(*a.shape[:-2], d * i)).reshape(*e.shape[:-1], d, i)
+        return m, e.sum(dim=-1, keepdim=True), ea, e @ b
+    return m, e.sum(dim=-1, keepdim=True), e @ a, e @ b
+
+
+def _omd_compose(f, g, *a, **kw):
+    m1, l1, fa1, fb1 = f
+    m2, l2, fa2, fb2 = g
+    lead = m1.dim()
+    n1 = torch.cat([fa1.reshape(*fa1.shape[:lead - 1], -1), fb1], -1)
+    n2 = torch.cat([fa2.reshape(*fa2.shape[:lead - 1], -1), fb2], -1)
+    m, lv, acc = _om_compose((m1, l1, n1), (m2, l2, n2))
+    wa = n1.shape[-1] - fb1.shape[-1]
+    return m, lv, acc[..., :wa].reshape(fa1.shape), acc[..., wa:]
+
+
 def cpu_table() -> HipOpTable:
     t = HipOpTable(HIP_BINDINGS)
     t.register(torch_bindings={
@@ -82,5 +103,8 @@ def cpu_table() -> HipOpTable:
         "hip_glu": _glu,
         "aff_compose": lambda f, g, *a, **kw: (f[0] @ g[0], f[0] @ g[1] + f[1]),
         "apply": lambda f, h, *a, **kw: f[0] @ h + f[1],
+        "omd_elem": _omd_elem,
+        "omd_compose": _omd_compose,
+        "omd_applym": lambda f, h, *a, **kw: (f[2] @ h + f[3]) / f[1],
     })
     return t

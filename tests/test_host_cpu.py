@@ -323,7 +323,7 @@ def test_scan_module_fallback_matches_the_serial_recurrence():
 def test_sink_surface_routing_and_verify():
     sink = HipSink(device="cpu", ops=cpu_table())
     names = list(sink.executors)
-    assert names == ["om_decayed_chunked", "scan", "om_batched", "generic"]
+    assert names == ["om_decayed_chunked", "scan", "om_batched", "omd_batched", "om_streaming", "generic"]
     assert sink.executors["generic"].carrier is None
     assert {"linear", "matmul", "rms_norm", "om_elem", "om_compose", "om_apply", "om_decayed",
             "decay", "decay_vec", "aff_diag", "affd_compose", "applyd", "aff", "aff_compose",
@@ -434,3 +434,55 @@ def test_dense_scan_module_fallback_matches_the_recurrence():
     At = torch.randn(T, d, d, dtype=torch.float64) * 0.3
     refp = oracle.serial_aff_scan(_np(At), _np(x), _np(h0)[:, None])[..., 0]
     assert oracle.verify_equiv(refp, _np(modp(At, x, h0)), rtol=1e-12)["passed"]
+
+
+# ------------------------------------------------------------------ omd plan
+
+
+def test_omd_plan_chain_and_seeds():
+    from catopt_amd.executors import build_omd_plan, is_omd_term
+
+    T, d, Tq, nb = 12, 3, 5, 3
+    ir, _ = forms.omd_scan_attention_form(T, d, Tq, nb)
+    assert is_omd_term(ir.root)
+    p = build_omd_plan(ir.root)
+    assert p["map_mode"] == "chain" and p["chain_domain"] == "diag" and len(p["chain_leaves"]) == T
+    assert p["chain_a_gather"][2] == list(range(T)) and p["chain_b_gather"][2] == list(range(T))
+    assert len(p["stack_seeds"]) == 2 * nb and len(p["leaves"]) == nb
+    # each block's stack reads prefix positions i·C … i·C + C - 1
+    C = T // nb
+    assert sorted(tuple(s[2]) for s in p["stack_seeds"]) == sorted(
+        [tuple(range(i * C, (i + 1) * C)) for i in range(nb)] * 2)
+    pd = build_omd_plan(forms.omd_scan_attention_form(8, 2, 3, 2, dense=True)[0].root)
+    assert pd["map_mode"] == "chain" and pd["chain_domain"] == "dense" and pd["apply"] == "omd_applym"
+    # two unrelated compose trees: forest (generic map evaluation)
+    a = [Var(f"a{i}", TensorType((2,))) for i in range(4)]
+    t1 = mk("affd_compose", mk("aff_diag", a[1], a[1]), mk("aff_diag", a[0], a[0]))
+    t2 = mk("affd_compose", mk("aff_diag", a[3], a[3]), mk("aff_diag", a[2], a[2]))
+    s = Var("s", TensorType((2, 2)))
+    leaf = mk("omd_elem", s, mk("stack", mk("affd_a", t1), mk("affd_a", t2), dim=0),
+              mk("stack", mk("affd_b", t1), mk("affd_b", t2), dim=0))
+    pf = build_omd_plan(mk("omd_apply", leaf, a[0]))
+    assert pf["map_mode"] == "forest"
+    # not omd-shaped
+    assert build_omd_plan(mk("om_apply", mk("om_elem", s, s))) is None
+    assert not is_omd_term(mk("omd_apply", mk("omd_compose", leaf, s), a[0]))
+
+
+def test_omd_module_fallback_matches_attention_over_states():
+    from catopt_amd.executors import HipOmdModule
+
+    T, d, Tq, nb, dk = 12, 3, 5, 3, 4
+    ir, _ = forms.omd_scan_attention_form(T, d, Tq, nb, dk)
+    mod = HipOmdModule(ir, {}, ops=cpu_table())
+    g = torch.Generator().manual_seed(0)
+    q, k = torch.randn(Tq, dk, generator=g, dtype=torch.float64), torch.randn(T, dk, generator=g, dtype=torch.float64)
+    a, x, h = (torch.rand(T, d, generator=g, dtype=torch.float64), torch.randn(T, d, generator=g, dtype=torch.float64),
+               torch.randn(d, generator=g, dtype=torch.float64))
+    out = mod(q, k, a, x, h)  # host fp64: the generic module runs
+    assert mod.fallbacks == 1
+    states = oracle.serial_affd_scan(_np(a), _np(x), _np(h))
+    sc = _np(q) @ _np(k).T
+    w = np.exp(sc - sc.max(-1, keepdims=True))
+    ref = (w / w.sum(-1, keepdims=True)) @ states
+    assert oracle.verify_equiv(ref, _np(out), rtol=1e-12)["passed"]

@@ -1,0 +1,156 @@
+"""Deferred-affine attention (omd) on the GPU (``HipOmdModule``).
+
+The counterpart of the reference's ``tests/test_omd_lower.py`` /
+``test_omd_lower_edges.py``: ``omd_apply(<omd_compose tree>, h)`` over key
+blocks whose coefficients are stacked projections of one scan's prefix maps
+equals softmax attention over that scan's states (diagonal and dense
+carriers); a fully masked row of one block contributes nothing; packaged
+``omd`` leaves fold in; hipGraph replays follow new inputs; fp64 runs the
+generic module.  References: the float64 serial recurrence of the numpy
+oracle (pinned by closed forms) under a dense softmax computed here — a
+different formulation from the carrier algebra the executor uses.  Gates:
+fp32 ≤ 1e-5, bf16 ≤ 2e-2 (verify metric).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from catopt_amd import forms
+from catopt_amd.executors import HipOmdModule
+from catopt_amd.ir import IR, Const, Op, TensorType, Var
+from catopt_amd.runner import HipGraphRunner
+from catopt_amd.sink import HipSink, deliver
+
+pytestmark = pytest.mark.gpu
+mk = Op.make
+TOL_F32 = 1e-5
+TOL_BF16 = 2e-2
+
+
+def _np(t):
+    return t.detach().float().cpu().double().numpy()
+
+
+def _gate(ref, out, tol):
+    rep = oracle.verify_equiv(ref, _np(out), rtol=tol)
+    assert rep["passed"], rep
+    return rep
+
+
+def _softmax_rows(sc):
+    w = np.exp(sc - sc.max(-1, keepdims=True))
+    return w / w.sum(-1, keepdims=True)
+
+
+def _inputs(T, d, Tq, dk, dense, seed, dtype=torch.float32):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((Tq, dk)) * 0.5
+    k = rng.standard_normal((T, dk)) * 0.5
+    a = (rng.standard_normal((T, d, d)) * (0.9 / np.sqrt(d))) if dense else rng.uniform(0.6, 1.0, (T, d))
+    x = rng.standard_normal((T, d))
+    h = rng.standard_normal(d)
+    return [torch.from_numpy(z.astype(np.float32)).to(dtype) for z in (q, k, a, x, h)]
+
+
+def _reference(q, k, a, x, h, dense):
+    qn, kn, an, xn, hn = (_np(t) for t in (q, k, a, x, h))
+    if dense:
+        states = oracle.serial_aff_scan(an, xn, hn[:, None])[..., 0]
+    else:
+        states = oracle.serial_affd_scan(an, xn, hn)
+    return _softmax_rows(qn @ kn.T) @ states
+
+
+@pytest.fixture(scope="module")
+def sink():
+    return HipSink()
+
+
+@pytest.mark.parametrize("dense", [False, True])
+def test_omd_attention_over_scan_states(sink, dev, dense):
+    T, d, Tq, nb, dk = (128, 16, 48, 4, 16) if dense else (512, 32, 64, 8, 16)
+    ir, _ = forms.omd_scan_attention_form(T, d, Tq, nb, dk, dense=dense)
+    ins = _inputs(T, d, Tq, dk, dense, 1)
+    res = deliver(ir, {}, sink, tuple(t.to(dev) for t in ins))
+    assert res.stats["executor"] == "omd_batched" and res.stats["hip_kernel"]
+    mod = res.module
+    assert mod.map_mode == "chain"
+    out = mod(*(t.to(dev) for t in ins))
+    assert mod.fallbacks == 0 and out.shape == (Tq, d) and out.dtype == torch.float32
+    _gate(_reference(*ins, dense), out, TOL_F32)
+
+
+def test_omd_bf16_operands(dev):
+    T, d, Tq, nb, dk = 256, 32, 32, 4, 16
+    ir, _ = forms.omd_scan_attention_form(T, d, Tq, nb, dk)
+    ins = _inputs(T, d, Tq, dk, False, 2, torch.bfloat16)
+    mod = HipOmdModule(ir, {})
+    out = mod(*(t.to(dev) for t in ins))
+    assert mod.fallbacks == 0 and out.dtype == torch.bfloat16
+    _gate(_reference(*ins, False), out, TOL_BF16)
+
+
+def test_omd_masked_block_rows_and_packaged_leaf(dev):
+    """Block 0 hides every key from query row 1 (a -inf row: that block's
+    carrier row is the empty one), and a packaged omd(m, l, fa, fb) leaf
+    built from the oracle folds in with the kernel-made ones."""
+    T, d, Tq, dk = 64, 8, 6, 8
+    C = T // 2
+    ins = _inputs(T, d, Tq, dk, False, 3)
+    q_, k_, a_, x_, h_ = (Var(n, TensorType(tuple(t.shape))) for n, t in zip("qkaxh", ins))
+    mask = Var("mask", TensorType((Tq, C)))
+    fs = []
+    for j in range(T):
+        lf = mk("aff_diag", mk("select", a_, dim=0, index=j), mk("select", x_, dim=0, index=j))
+        fs.append(lf if j == 0 else mk("affd_compose", lf, fs[-1]))
+
+    def stacks(lo, hi):
+        return (mk("stack", *[mk("affd_a", f) for f in fs[lo:hi]], dim=0),
+                mk("stack", *[mk("affd_b", f) for f in fs[lo:hi]], dim=0))
+
+    s0 = mk("masked_fill", mk("matmul", q_, mk("transpose", mk("chunk", k_, chunks=2, dim=0, index=0), dim0=0, dim1=1)),
+            mask, Const(float("-inf")))
+    e0 = mk("omd_elem", s0, *stacks(0, C))
+    pm, pl, pa, pb = (Var(n, TensorType(sh)) for n, sh in
+                      (("pm", (Tq, 1)), ("pl", (Tq, 1)), ("pa", (Tq, d)), ("pb", (Tq, d))))
+    root = mk("omd_apply", mk("omd_compose", e0, mk("omd", pm, pl, pa, pb)), h_)
+    mod = HipOmdModule(IR(root, [q_, k_, a_, x_, h_, mask, pm, pl, pa, pb]), {})
+    assert mod.is_batched and mod.map_mode == "chain"
+    mk_np = np.zeros((Tq, C), dtype=bool)
+    mk_np[1] = True
+    mk_np[3, ::2] = True
+    # the second key block as a packaged carrier, from the oracle on the true prefix maps
+    qn, kn, an, xn = (_np(t) for t in ins[:4])
+    Pa, Pb = np.cumprod(an, axis=0), oracle.serial_affd_scan(an, xn, np.zeros(d))
+    s1 = qn @ kn[C:].T
+    pkg = oracle.omd_elem(s1, Pa[C:], Pb[C:])
+    dev_ins = [t.to(dev) for t in ins] + [torch.from_numpy(mk_np).to(dev)] + \
+        [torch.from_numpy(np.asarray(z, dtype=np.float32)).to(dev) for z in pkg]
+    out = mod(*dev_ins)
+    assert mod.fallbacks == 0
+    states = oracle.serial_affd_scan(an, xn, _np(ins[4]))
+    sc = qn @ kn.T
+    sc[:, :C][mk_np] = -np.inf
+    _gate(_softmax_rows(sc) @ states, out, TOL_F32)
+
+
+def test_omd_graph_replay_and_fp64_fallback(sink, dev):
+    T, d, Tq, nb, dk = 128, 16, 16, 4, 8
+    ir, _ = forms.omd_scan_attention_form(T, d, Tq, nb, dk)
+    ins = [t.to(dev) for t in _inputs(T, d, Tq, dk, False, 4)]
+    res = deliver(ir, {}, sink, tuple(ins), runner=HipGraphRunner())
+    assert res.module.is_graph_captured
+    out = res.module(*ins).clone()
+    _gate(_reference(*ins, False), out, TOL_F32)
+    ins2 = [t.to(dev) for t in _inputs(T, d, Tq, dk, False, 5)]
+    out2 = res.module(*ins2).clone()
+    _gate(_reference(*ins2, False), out2, TOL_F32)
+    mod = HipOmdModule(ir, {})
+    out64 = mod(*(t.double() for t in ins))
+    assert mod.fallbacks == 1 and out64.dtype == torch.float64
+    rep = oracle.verify_equiv(_reference(*ins, False), out64.cpu().numpy(), rtol=1e-10)
+    assert rep["passed"], rep

@@ -445,3 +445,76 @@ def test_aff_chunked_scan_matches_serial(T, per_slot):
         out, hT = oracle.aff_chunked_scan(A, b, h0, np.asarray(table))
         _close(out, ser, 1e-10)
         _close(hT, ser[-1], 1e-10)
+
+
+# ------------------------------------------------------------------ deferred-affine om
+
+
+def test_omd_elem_is_om_elem_of_the_affine_values():
+    """The defining identity: applying the deferred carrier to h equals
+    softmax attention over the materialised values a⊙h + b (diagonal) or
+    A@h + b (dense)."""
+    Tq, K, d = 5, 7, 4
+    s = rng.standard_normal((2, Tq, K))  # two heads over shared per-key coefficients
+    a, b, h = rng.standard_normal((K, d)), rng.standard_normal((K, d)), rng.standard_normal(d)
+    f = oracle.omd_elem(s, a, b)
+    dense = np.exp(s - s.max(-1, keepdims=True))
+    dense = dense / dense.sum(-1, keepdims=True)
+    _close(oracle.omd_apply(f, h), dense @ (a * h + b), 1e-12)
+    _close(oracle.omd_apply(f, h), oracle.om_apply(oracle.om_elem(s, a * h + b)), 1e-12)
+    A = rng.standard_normal((2, K, d, 3))
+    hm = rng.standard_normal(3)
+    fm = oracle.omd_elem(s, A, b)
+    assert fm[2].shape == (2, Tq, d, 3)
+    _close(oracle.omd_applym(fm, hm), dense @ (A @ hm + b), 1e-12)
+    # a transposed map or a dropped offset would not pass
+    Asq = rng.standard_normal((2, K, d, d))
+    hs = rng.standard_normal(d)
+    fsq = oracle.omd_elem(s, Asq, b)
+    assert np.max(np.abs(oracle.omd_applym(fsq, hs) - dense @ (np.swapaxes(Asq, -1, -2) @ hs + b))) > 1e-6
+    assert np.max(np.abs(oracle.omd_applym(fsq, hs) - dense @ (Asq @ hs))) > 1e-6
+
+
+def test_omd_compose_is_om_compose_on_concatenated_numerators():
+    Tq, K, d = 4, 6, 3
+    s1, s2 = rng.standard_normal((Tq, K)), rng.standard_normal((Tq, K)) + 3.0
+    a1, b1, a2, b2 = (rng.standard_normal((K, d)) for _ in range(4))
+    f, g = oracle.omd_elem(s1, a1, b1), oracle.omd_elem(s2, a2, b2)
+    c = oracle.omd_compose(f, g)
+    om = oracle.om_compose((f[0], f[1], np.concatenate([f[2], f[3]], -1)),
+                           (g[0], g[1], np.concatenate([g[2], g[3]], -1)))
+    _close(c[0], om[0], 1e-12)
+    _close(c[1], om[1], 1e-12)
+    _close(np.concatenate([c[2], c[3]], -1), om[2], 1e-12)
+    # = one leaf over the concatenated keys (the softmax is over all keys)
+    whole = oracle.omd_elem(np.concatenate([s1, s2], -1), np.concatenate([a1, a2]), np.concatenate([b1, b2]))
+    h = rng.standard_normal(d)
+    _close(oracle.omd_apply(c, h), oracle.omd_apply(whole, h), 1e-12)
+    # associativity, and order matters only through rounding
+    e3 = oracle.omd_elem(rng.standard_normal((Tq, K)), rng.standard_normal((K, d)), rng.standard_normal((K, d)))
+    l1 = oracle.omd_compose(oracle.omd_compose(f, g), e3)
+    l2 = oracle.omd_compose(f, oracle.omd_compose(g, e3))
+    _close(oracle.omd_apply(l1, h), oracle.omd_apply(l2, h), 1e-12)
+
+
+def test_omd_compose_masked_block_and_dense_fibre():
+    Tq, K, d, i = 3, 4, 2, 5
+    s = rng.standard_normal((Tq, K))
+    s_masked = s.copy()
+    s_masked[1] = -np.inf  # row 1 of this block fully masked
+    A, b = rng.standard_normal((K, d, i)), rng.standard_normal((K, d))
+    f = oracle.omd_elem(s, A, b)
+    with np.errstate(invalid="ignore"):
+        g = oracle.omd_elem(s_masked, A, b)
+    c = oracle.omd_compose(f, g)
+    assert np.all(np.isfinite(c[2])) and np.all(np.isfinite(c[3]))
+    # row 1: only f contributes
+    _close(c[1][1], f[1][1], 1e-12)
+    _close(c[2][1], f[2][1], 1e-12)
+    # other rows: the two blocks of the same keys weigh equally
+    _close(c[2][0] / c[1][0], f[2][0] / f[1][0], 1e-12)
+    # both fully masked: the empty carrier (0/0 on apply, as dense softmax)
+    with np.errstate(invalid="ignore"):
+        z = oracle.omd_compose(g, g)
+        out = oracle.omd_applym(z, rng.standard_normal(i))
+    assert np.isneginf(z[0][1]).all() and z[1][1] == 0 and np.isnan(out[1]).all()
