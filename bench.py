@@ -1,6 +1,6 @@
 """Delivered-form throughput of the HIP executor on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--forms c1,c2,c3,c4,c5,aff,copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--forms c1,c2,c3,c4,c5,aff,omd,copy]
                     [--cpu-budget SECONDS] [--no-cpu]
 
 One "step" is one forward of a delivered form over one batch of synthetic
@@ -8,9 +8,10 @@ input that is already resident in HBM (BASELINE.json's five configs, seeded
 with ``torch.manual_seed(0)``).  The headline workload is config 2 (the
 SwiGLU MLP block with RMSNorm: rms_norm -> gate/up GEMM with the silu*mul
 epilogue -> down GEMM); its whole-step TFLOP/s is ``value``.  Every other
-config is measured the same way and reported under ``forms``, and so is the
-dense affine scan (``aff``: a batched LTI recurrence delivered as
-``apply(<aff_compose tree>, h)``; not one of the BASELINE configs).
+config is measured the same way and reported under ``forms``, and so are
+the dense affine scan (``aff``: a batched LTI recurrence delivered as
+``apply(<aff_compose tree>, h)``) and the deferred-affine attention over a
+scan's states (``omd``), which are not BASELINE configs.
 
 Per form:
   * ``ms_per_step``  — HIP events on torch's current stream (the stream the
@@ -553,6 +554,75 @@ class DenseScan(Form):
                 "parity_max_rel": rel}
 
 
+class OmdScanAttention(Form):
+    """Deferred-affine attention (not a BASELINE config): softmax attention of
+    Tq queries over the T states of a diagonal scan, delivered as
+    ``omd_apply(<omd_compose tree of omd_elem(q·k_iᵀ, stack(affd_a f_j),
+    stack(affd_b f_j))>, h)`` over 16 key blocks of the prefix chain f_j."""
+
+    name, dtype, unit, bound = "omd", "f32", "TFLOP/s", "mfma"
+    T, d, Tq, blocks, dk = 4096, 64, 4096, 16, 64
+    workload = ("omd attention over scan states: T=4096 keys/steps, state d=64, Tq=4096 queries, dk=64, "
+                "16 key blocks, diagonal scan a_t,x_t (T,64), fp32")
+    peak = PEAK["fp32_tflops"]
+    work = 2.0 * Tq * T * (dk + 2 * d)  # scores + the two numerator parts
+    dom_name = "e @ [a|b] leaf GEMM (gemm_generic<float,false,false,0>)"
+    dom_key = "gemm_generic<float, false, false, 0>"
+    dom_work = 2.0 * Tq * (T // blocks) * 2 * d
+
+    def setup(self, dev):
+        import torch
+
+        from catopt_amd import forms
+        from catopt_amd import kernels as K
+        from catopt_amd.sink import deliver
+
+        g = _gen(0)
+        self.q = torch.randn((self.Tq, self.dk), device=dev, generator=g) * 0.125
+        self.k = torch.randn((self.T, self.dk), device=dev, generator=g) * 0.125
+        self.a = torch.rand((self.T, self.d), device=dev, generator=g) * 0.4 + 0.6
+        self.x = torch.randn((self.T, self.d), device=dev, generator=g)
+        self.h = torch.randn((self.d,), device=dev, generator=g)
+        ir, _ = forms.omd_scan_attention_form(self.T, self.d, self.Tq, self.blocks, self.dk)
+        self.ins = (self.q, self.k, self.a, self.x, self.h)
+        res = deliver(ir, {}, _sink(dev), self.ins)
+        self.mod, self.stats = res.module, res.stats
+        assert self.mod.map_mode == "chain"
+        C = self.T // self.blocks
+        self.e = torch.rand((self.Tq, C), device=dev, generator=g)
+        self.V = torch.randn((C, 2 * self.d), device=dev, generator=g)
+        self.K = K
+
+    def step(self):
+        self.out = self.mod(*self.ins)
+
+    def dominant(self):
+        self.K.matmul(self.e, self.V)
+
+    def cpu(self, budget):
+        import numpy as np
+
+        import oracle
+
+        Tq = 256  # 256 of the 4096 queries (rows are independent), all T keys
+        q, k, a, x, h = (t.cpu().double().numpy() for t in self.ins)
+        q = q[:Tq]
+
+        def run():
+            states = oracle.serial_affd_scan(a, x, h)
+            sc = q @ k.T
+            w = np.exp(sc - sc.max(-1, keepdims=True))
+            return (w / w.sum(-1, keepdims=True)) @ states
+
+        sec, reps, ref = time_cpu(run, budget)
+        self.step()
+        rel = oracle.verify_equiv(ref, self.out[:Tq].double().cpu().numpy())["max_rel"]
+        flops = 2.0 * Tq * self.T * (self.dk + self.d)
+        return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": cpu_threads(), "kind": "port",
+                "sample": f"{Tq} of {self.Tq} queries over all {self.T} scan states (numpy fp64: serial scan, "
+                          f"dense softmax), {reps} reps", "parity_max_rel": rel}
+
+
 class CopyStream(Form):
     """STREAM-style device copy of 2 GiB fp32: the measured-achievable HBM
     figure reported beside the vendor peak, and the known-size kernel the
@@ -578,7 +648,8 @@ class CopyStream(Form):
     dominant = step
 
 
-FORMS = {f.name: f for f in (C1WeightChain, C2SwiGLU, C3Attention, C4Retention, C5SSM, DenseScan, CopyStream)}
+FORMS = {f.name: f for f in (C1WeightChain, C2SwiGLU, C3Attention, C4Retention, C5SSM, DenseScan,
+                                OmdScanAttention, CopyStream)}
 HEADLINE = "c2"
 
 
@@ -638,7 +709,7 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--forms", default="c1,c2,c3,c4,c5,aff,copy")
+    ap.add_argument("--forms", default="c1,c2,c3,c4,c5,aff,omd,copy")
     ap.add_argument("--cpu-budget", type=float, default=10.0,
                     help="seconds of CPU oracle work for the headline form (others get a third)")
     ap.add_argument("--no-cpu", action="store_true")

@@ -124,15 +124,49 @@ def _part_gather(leaves: list, slot: int) -> tuple | None:
     return base, dim, [i[2] for i in idx]
 
 
+def _spine_positions(maps: dict, leaf_op: str, comp_op: str) -> tuple | None:
+    """O(T) recognition of the common chain: every map lies on one spine
+    ``f_j = compose(leaf_j, f_{j-1})`` (``f_0`` a leaf).  Returns
+    ``(positions, leaves)`` or ``None`` (the general comparison then runs)."""
+    depth: dict = {}
+    for mp in maps:
+        path, u = [], mp
+        while u not in depth:
+            if is_op(u, leaf_op, 2):
+                depth[u] = 0
+                break
+            if is_op(u, comp_op, 2) and is_op(u.args[0], leaf_op, 2):
+                path.append(u)
+                u = u.args[1]
+                continue
+            return None
+        dpt = depth[u]
+        for n in reversed(path):
+            dpt += 1
+            depth[n] = dpt
+    top = max(maps, key=lambda m: depth[m])
+    spine, u = [], top
+    while not is_op(u, leaf_op, 2):
+        spine.append(u)
+        u = u.args[1]
+    spine.append(u)
+    spine.reverse()  # spine[j] = f_j
+    if any(not (spine[depth[m]] is m or spine[depth[m]] == m) for m in maps):
+        return None
+    leaves = [spine[0]] + [f.args[0] for f in spine[1:]]
+    return {m: depth[m] for m in maps}, leaves
+
+
 def build_omd_plan(root: Any) -> dict | None:
     if not is_omd_term(root):
         return None
     F, h = root.args
     leaves = _omd_leaves(F)
     # ---- projections of maps inside the leaves (and h) -------------------
-    projs: list = []   # (node, component, map)
+    projs: list = []   # (node, component, map): projections outside a stack
     stacks: list = []  # (node, component, [maps], dim)
     maps: dict = {}    # map term -> carrier
+    loose: list = []   # map terms in a tensor position (evaluated as pairs)
     bad = False
     seen: set = set()
 
@@ -157,11 +191,11 @@ def build_omd_plan(root: Any) -> dict | None:
                 ci, dom = next(iter(infos))
                 for c in t.args:
                     register(c.args[0], dom)
-                    projs.append((c, ci, c.args[0]))
                 stacks.append((t, ci, [c.args[0] for c in t.args], int(attr_of(t.attrs, "dim", default=0))))
-                return
+                return  # its projections are reached only through the stack: one seed covers them
         if t.op in _COMPOSE or t.op in _LEAF:
-            return  # map structure in a tensor position stays with the generic module
+            loose.append(t)  # a map in a tensor position: seeded as a pair if it is a chain map
+            return
         for a in t.args:
             scan(a)
 
@@ -176,6 +210,13 @@ def build_omd_plan(root: Any) -> dict | None:
     if not maps:
         return plan
     # ---- chain: every projected map a prefix of one leaf sequence ---------
+    doms = set(maps.values())
+    if len(doms) == 1:
+        dom = next(iter(doms))
+        leaf_op, comp_op = ("aff_diag", "affd_compose") if dom == "diag" else ("aff", "aff_compose")
+        fast = _spine_positions(maps, leaf_op, comp_op)
+        if fast is not None:
+            return _chain_plan(plan, dom, fast[1], fast[0], projs, stacks, [m for m in loose if m in maps])
     seqs = {mp: _app_order(mp) for mp in maps}  # terms are content-keyed (cached hashes)
     base = max(seqs.values(), key=len)
     doms = set(maps.values())
@@ -188,11 +229,18 @@ def build_omd_plan(root: Any) -> dict | None:
         plan["map_mode"] = "forest"
         return plan
     pos = {mp: len(s) - 1 for mp, s in seqs.items()}
+    return _chain_plan(plan, dom, base, pos, projs, stacks, [m for m in loose if m in maps])
+
+
+def _chain_plan(plan: dict, dom: str, base: list, pos: dict, projs: list, stacks: list, loose: list) -> dict:
+    """Seeds for the evaluator's memo: every stack of projections, every
+    projection outside a stack, and every chain map met in a tensor position
+    (``omd_lower.py:528-547``)."""
     plan.update(map_mode="chain", chain_domain=dom, chain_leaves=base,
                 chain_a_gather=_part_gather(base, 0), chain_b_gather=_part_gather(base, 1))
     plan["proj_seeds"] = [(node, ci, pos[mp]) for node, ci, mp in projs]
     plan["stack_seeds"] = [(node, ci, [pos[mp] for mp in mps], dim) for node, ci, mps, dim in stacks]
-    plan["map_seeds"] = [(mp, pos[mp]) for mp in maps]
+    plan["map_seeds"] = [(mp, pos[mp]) for mp in dict.fromkeys(loose)]
     return plan
 
 
@@ -211,6 +259,8 @@ class HipOmdModule(HipExecutorBase, nn.Module):
         self._const_cache: dict = {}
         self.fallbacks = 0
         self._plan = build_omd_plan(self.eval_mod._root)
+        self._seeded_ids = set() if self._plan is None else \
+            {id(node) for node, *_ in self._plan["proj_seeds"] + self._plan["stack_seeds"]}
         self._init_graph_state()
 
     @property
@@ -330,7 +380,7 @@ class HipOmdModule(HipExecutorBase, nn.Module):
             self._seed(memo, Pa, Pb)
             # the result's dtype follows the chain's operands, not the fp32 prefix maps
             dtypes += [A.dtype, B.dtype]
-            seeded = {id(node) for node, *_ in p["proj_seeds"] + p["stack_seeds"]}
+            seeded = self._seeded_ids
         state = None
         width = tail = None
         for lf in p["leaves"]:

@@ -486,3 +486,20 @@ def test_omd_module_fallback_matches_attention_over_states():
     w = np.exp(sc - sc.max(-1, keepdims=True))
     ref = (w / w.sum(-1, keepdims=True)) @ states
     assert oracle.verify_equiv(ref, _np(out), rtol=1e-12)["passed"]
+
+
+def test_omd_plan_chain_with_other_bracketing():
+    """A prefix bracketed differently (compose(compose(l3, l2), f1)) is still a
+    prefix of the same leaf sequence: the general check keeps the chain."""
+    from catopt_amd.executors import build_omd_plan
+
+    a = Var("a", TensorType((4, 2)))
+    lv = [mk("aff_diag", mk("select", a, dim=0, index=j), mk("select", a, dim=0, index=j)) for j in range(4)]
+    f1 = mk("affd_compose", lv[1], lv[0])
+    f3 = mk("affd_compose", mk("affd_compose", lv[3], lv[2]), f1)
+    s, h = Var("s", TensorType((3, 2))), Var("h", TensorType((2,)))
+    leaf = mk("omd_elem", s, mk("stack", mk("affd_a", f1), mk("affd_a", f3), dim=0),
+              mk("stack", mk("affd_b", f1), mk("affd_b", f3), dim=0))
+    p = build_omd_plan(mk("omd_apply", leaf, h))
+    assert p["map_mode"] == "chain" and len(p["chain_leaves"]) == 4
+    assert [tuple(x[2]) for x in p["stack_seeds"]] == [(1, 3), (1, 3)]
