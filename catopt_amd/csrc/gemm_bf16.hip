@@ -81,6 +81,9 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
   __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | ((n >> 4) << 14));
 }
 
+// s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt not waited on).
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (3 << 14)); }
+
 struct TileMap {
   int tm, tn;
 };
@@ -239,11 +242,18 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_nt(
     const int nxt = cur + 1 == NSTAGE ? 0 : cur + 1;
 #pragma unroll
     for (int ks = 0; ks + 1 < KS; ++ks) {
+      // k-step ks's fragments (read one step earlier) have landed before the
+      // next step's reads go out: the MFMAs below then wait on nothing, where
+      // the compiler's own wait before them would also cover the new reads.
+      wait_lgkm0();
       read_frags(cur, ks + 1, (ks + 1) & 1);
       __builtin_amdgcn_sched_barrier(0);
       mfmas(ks & 1);
       __builtin_amdgcn_sched_barrier(0);
     }
+    // the last k-step's fragments have landed on both paths below, so the
+    // MFMAs after the branch do not wait for the next tile's first reads
+    wait_lgkm0();
     if (kt + 1 < ktiles) {
       // loads land in issue order: all but the newest NSTAGE-2 tiles means
       // tile kt+1 is in place
