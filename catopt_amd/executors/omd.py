@@ -29,7 +29,10 @@ Execution on the device:
   lanes from ``[1 | 0]`` with offsets ``[0 | b]`` gives
   ``[∏a | prefix b]``; dense: two ``catopt_hip_aff_scan`` launches
   (``I`` under the maps alone, ``0`` under the maps and offsets);
-* leaves — ``m``, ``l`` and one HIP GEMM ``e @ [a | b]`` per leaf (the two
+* leaves — a score ``scale · q kᵀ`` (unmasked) runs the fused fp32 carrier
+  kernel ``catopt_hip_attn_carrier_f32`` over the values ``[a | b]``: the
+  scores, exponentials and numerators stay on chip; any other score is
+  evaluated, then ``m``, ``l`` and one HIP GEMM ``e @ [a | b]`` (the two
   numerator parts share the exponentials);
 * the compose tree — left-folded in product order by the HIP ``om_compose``
   kernel over the concatenated numerator ``[fa | fb]`` (the omd combine is
@@ -56,6 +59,7 @@ from ..bindings import _om_compose, attr_of
 from ..evaluator import HipIRModule
 from ..ir import IR, Op, is_op
 from .base import HipExecutorBase
+from .om import _peel_scale, parse_score
 from .scan import prefix_chunk_table
 
 __all__ = ["HipOmdModule", "build_omd_plan", "is_omd_term", "to_batched_omd_module"]
@@ -157,6 +161,26 @@ def _spine_positions(maps: dict, leaf_op: str, comp_op: str) -> tuple | None:
     return {m: depth[m] for m in maps}, leaves
 
 
+def _plain_score(leaf: Any) -> dict | None:
+    """``q``, ``k`` and ``scale`` of an unmasked ``scale · q kᵀ`` leaf score.
+    A transpose with absolute axes (``transpose(x, 0, 1)``) of a term whose
+    rank is not known here is accepted with those axes recorded; the call
+    checks them against the evaluated operand's rank."""
+    if leaf.op != "omd_elem":
+        return None
+    sc = parse_score(leaf.args[0])
+    if sc is not None:
+        return dict(sc, axes=None) if sc["mask"] is None else None
+    s, scale = _peel_scale(leaf.args[0])
+    if not is_op(s, "matmul", 2) or not is_op(s.args[1], "transpose", 1):
+        return None
+    d0, d1 = attr_of(s.args[1].attrs, "dim0", default=None), attr_of(s.args[1].attrs, "dim1", default=None)
+    if d0 is None or d1 is None:
+        return None
+    return {"q": s.args[0], "k": s.args[1].args[0], "scale": scale, "mask": None,
+            "axes": frozenset((int(d0), int(d1)))}
+
+
 def build_omd_plan(root: Any) -> dict | None:
     if not is_omd_term(root):
         return None
@@ -206,7 +230,10 @@ def build_omd_plan(root: Any) -> dict | None:
     if bad:
         return None
     plan: dict = {"apply": root.op, "h": h, "leaves": leaves, "map_mode": None,
-                  "proj_seeds": [], "stack_seeds": [], "map_seeds": []}
+                  "proj_seeds": [], "stack_seeds": [], "map_seeds": [],
+                  # unmasked scale·q kᵀ scores: the leaf runs the fused carrier kernel
+                  "scores": [_plain_score(lf) for lf in leaves], "blocks": None}
+    plan["k_chunks"] = _chunk_keys(plan["scores"])
     if not maps:
         return plan
     # ---- chain: every projected map a prefix of one leaf sequence ---------
@@ -235,13 +262,53 @@ def build_omd_plan(root: Any) -> dict | None:
 def _chain_plan(plan: dict, dom: str, base: list, pos: dict, projs: list, stacks: list, loose: list) -> dict:
     """Seeds for the evaluator's memo: every stack of projections, every
     projection outside a stack, and every chain map met in a tensor position
-    (``omd_lower.py:528-547``)."""
+    (``omd_lower.py:528-547``); and, when every leaf's coefficients are the
+    stacks of one contiguous run of prefix positions, those runs."""
     plan.update(map_mode="chain", chain_domain=dom, chain_leaves=base,
                 chain_a_gather=_part_gather(base, 0), chain_b_gather=_part_gather(base, 1))
     plan["proj_seeds"] = [(node, ci, pos[mp]) for node, ci, mp in projs]
     plan["stack_seeds"] = [(node, ci, [pos[mp] for mp in mps], dim) for node, ci, mps, dim in stacks]
     plan["map_seeds"] = [(mp, pos[mp]) for mp in dict.fromkeys(loose)]
+    plan["blocks"] = _leaf_blocks(plan)
     return plan
+
+
+def _leaf_blocks(plan: dict) -> list | None:
+    """``[(start, length)]`` per leaf when its ``a`` and ``b`` arguments stack
+    the same contiguous prefix positions along axis 0; else ``None``."""
+    by_node = {id(node): (ci, idx, dim) for node, ci, idx, dim in plan["stack_seeds"]}
+    out = []
+    for lf in plan["leaves"]:
+        if lf.op != "omd_elem":
+            return None
+        sa, sb = by_node.get(id(lf.args[1])), by_node.get(id(lf.args[2]))
+        if sa is None or sb is None or sa[0] != 0 or sb[0] != 1 or sa[2] != 0 or sb[2] != 0 or sa[1] != sb[1]:
+            return None
+        idx = sa[1]
+        if idx != list(range(idx[0], idx[0] + len(idx))):
+            return None
+        out.append((idx[0], len(idx)))
+    return out
+
+
+def _chunk_keys(scores: list) -> tuple | None:
+    """``(base, dim)`` when leaf ``i``'s key operand is ``chunk(base, chunks=L,
+    dim, index=i)`` of one base over the L leaves."""
+    if not scores or any(sc is None for sc in scores):
+        return None
+    L = len(scores)
+    base = dim = None
+    for i, sc in enumerate(scores):
+        kt = sc["k"]
+        if not is_op(kt, "chunk", 1) or int(attr_of(kt.attrs, "index", default=-1)) != i or \
+                int(attr_of(kt.attrs, "chunks", default=0)) != L:
+            return None
+        d = int(attr_of(kt.attrs, "dim", default=0))
+        if base is None:
+            base, dim = kt.args[0], d
+        elif not (kt.args[0] is base or kt.args[0] == base) or d != dim:
+            return None
+    return base, dim
 
 
 def _kernel_dtype(t: Any) -> bool:
@@ -259,6 +326,7 @@ class HipOmdModule(HipExecutorBase, nn.Module):
         self._const_cache: dict = {}
         self.fallbacks = 0
         self._plan = build_omd_plan(self.eval_mod._root)
+        self.fused_leaves = 0  # leaves run by the fused carrier kernel on the last call
         self._seeded_ids = set() if self._plan is None else \
             {id(node) for node, *_ in self._plan["proj_seeds"] + self._plan["stack_seeds"]}
         self._init_graph_state()
@@ -343,15 +411,125 @@ class HipOmdModule(HipExecutorBase, nn.Module):
         m = s32.amax(dim=-1, keepdim=True)
         e = torch.exp(s32 - m)
         lv = e.sum(dim=-1, keepdim=True)
+        V, wa, tail = HipOmdModule._values(a, b)
+        num = K.matmul(e, V) if e.dim() >= 2 and V.dim() >= 2 else e @ V
+        return m, lv, num, wa, tail
+
+    @staticmethod
+    def _values(a: torch.Tensor, b: torch.Tensor) -> tuple:
+        """``[a | b]`` along the value axis (the dense ``a`` flattened), its
+        ``fa`` width and trailing shape."""
         if a.dim() >= 3:  # dense fibre (xcarrier.py:393-399)
             d, i = a.shape[-2], a.shape[-1]
-            af = a.reshape(*a.shape[:-2], d * i)
-            tail = (d, i)
+            af, tail = a.reshape(*a.shape[:-2], d * i), (d, i)
         else:
             af, tail = a, (a.shape[-1],)
         V = torch.cat([af.float(), b.float().expand(*af.shape[:-1], b.shape[-1])], dim=-1)
-        num = K.matmul(e, V) if e.dim() >= 2 and V.dim() >= 2 else e @ V
-        return m, lv, num, af.shape[-1], tail
+        return V, af.shape[-1], tail
+
+    def _fused_leaf(self, sc: dict, a: torch.Tensor, b: torch.Tensor, ev) -> tuple | None:
+        """The leaf's carrier from ``catopt_hip_attn_carrier_f32`` when its
+        score is ``scale·q kᵀ`` over device fp32/bf16 operands in the kernel's
+        envelope; ``None`` otherwise (the unfused path runs)."""
+        q, k = ev(sc["q"]), ev(sc["k"])
+        if not all(_kernel_dtype(t) for t in (q, k, a, b)) or q.dim() < 2 or k.dim() != q.dim():
+            return None
+        n = k.dim()
+        if sc["axes"] is not None and {x % n for x in sc["axes"]} != {n - 2, n - 1}:
+            return None  # not a transpose of the last two axes: the evaluated score is used
+        if q.shape[-1] != k.shape[-1] or q.shape[-1] > 128 or tuple(q.shape[:-2]) != tuple(k.shape[:-2]):
+            return None
+        V, wa, tail = self._values(a, b)
+        if V.shape[-1] > 256 or V.shape[-2] != k.shape[-2] or (V.dim() > 2 and tuple(V.shape[:-2]) != tuple(q.shape[:-2])):
+            return None
+        m, lv, num = K.attn_carrier_f32(q, k, V, float(sc["scale"]))
+        return m, lv, num, wa, tail, [q.dtype, k.dtype]
+
+    def _shared_q(self, ev) -> torch.Tensor | None:
+        scs = self._plan["scores"]
+        if len(scs) < 2 or any(sc is None for sc in scs):
+            return None
+        if any(not (sc["q"] is scs[0]["q"] or sc["q"] == scs[0]["q"]) or sc["scale"] != scs[0]["scale"]
+               for sc in scs):
+            return None
+        q = ev(scs[0]["q"])
+        if not _kernel_dtype(q) or q.dim() != 2 or q.shape[-1] > 128:
+            return None
+        return q
+
+    @staticmethod
+    def _fold(m: torch.Tensor, lv: torch.Tensor, num: torch.Tensor) -> tuple:
+        """The om combine of every carrier along axis 0 at once: weights
+        ``exp(m_i − M)``, a carrier with no finite score weighing 0."""
+        M = m.amax(dim=0)
+        fin = torch.isfinite(m)
+        w = torch.where(fin, torch.exp(torch.where(fin, m, M) - M), torch.zeros_like(m))
+        return M, (lv * w).sum(dim=0), (num * w).sum(dim=0)
+
+    def _batched_blocks(self, ev, Pa: torch.Tensor, Pb: torch.Tensor) -> tuple | None:
+        """The chain plan's fast path: every leaf's coefficients are one
+        contiguous run of prefix positions, so the value blocks are rows of
+        ``[Pa | Pb]`` (built once) and the key blocks chunks of one key array —
+        one carrier launch over all leaves, no per-leaf gathers."""
+        p = self._plan
+        blocks = p["blocks"]
+        if not blocks or p["k_chunks"] is None:
+            return None
+        q = self._shared_q(ev)
+        if q is None:
+            return None
+        L, C = len(blocks), blocks[0][1]
+        if any(n != C for _, n in blocks):
+            return None
+        base, dim = p["k_chunks"]
+        kall = ev(base)
+        if not _kernel_dtype(kall) or kall.dim() != 2 or dim % 2 != 0 or kall.shape[0] != L * C or \
+                kall.shape[1] != q.shape[1]:
+            return None
+        T = Pa.shape[0]
+        tail = tuple(Pa.shape[1:]) if Pa.dim() >= 3 else (Pa.shape[-1],)  # the fibre test of _omd_elem
+        wa = Pa[0].numel()
+        Vall = torch.cat([Pa.reshape(T, -1), Pb.reshape(T, -1)], dim=1)
+        if Vall.shape[1] > 256:
+            return None
+        if blocks == [(i * C, C) for i in range(L)]:
+            V = Vall[:L * C].view(L, C, -1)
+        else:
+            V = torch.stack([Vall[s:s + C] for s, _ in blocks])
+        m, lv, num = K.attn_carrier_f32(q, kall.reshape(L, C, -1), V, float(p["scores"][0]["scale"]))
+        return self._fold(m, lv, num), wa, tail, [q.dtype, kall.dtype]
+
+    def _batched_leaves(self, ev) -> tuple | None:
+        """Every leaf a ``scale · q k_iᵀ`` score over one shared ``q`` with key
+        and value blocks of one shape: one carrier launch over (query tiles x
+        leaves), then one weighted fold over the leaf axis (the om combine of
+        all blocks at once, with the ``isfinite`` guard).  ``None`` when the
+        leaves do not line up (each leaf then runs on its own)."""
+        p = self._plan
+        scs = p["scores"]
+        q = self._shared_q(ev)
+        if q is None:
+            return None
+        ks, Vs, shape = [], [], None
+        for lf, sc in zip(p["leaves"], scs):
+            k, a, b = ev(sc["k"]), ev(lf.args[1]), ev(lf.args[2])
+            if not all(_kernel_dtype(t) for t in (k, a, b)) or k.dim() != 2 or k.shape[-1] != q.shape[-1]:
+                return None
+            if sc["axes"] is not None and set(sc["axes"]) - {0, 1, -1, -2}:
+                return None
+            V, wa, tail = self._values(a, b)
+            if V.dim() != 2 or V.shape[0] != k.shape[0]:
+                return None
+            if shape is None:
+                shape = (k.shape, V.shape, wa, tail)
+            elif (k.shape, V.shape, wa, tail) != shape:
+                return None
+            ks.append(k)
+            Vs.append(V)
+        if shape[1][-1] > 256:
+            return None
+        m, lv, num = K.attn_carrier_f32(q, torch.stack(ks), torch.stack(Vs), float(scs[0]["scale"]))
+        return self._fold(m, lv, num), shape[2], shape[3], [q.dtype] + [k.dtype for k in ks[:1]]
 
     def _forward_impl(self, *xs: Any) -> Any:
         p = self._plan
@@ -372,25 +550,42 @@ class HipOmdModule(HipExecutorBase, nn.Module):
         p = self._plan
         dtypes = []
         seeded: set = set()
+        Pa = Pb = None
         if p["map_mode"] == "chain":
             A, B = self._chain_parts(ev)
             if not (_kernel_dtype(A) and _kernel_dtype(B)):
                 raise _Decline()
             Pa, Pb = self._prefix_maps(A, B)
-            self._seed(memo, Pa, Pb)
             # the result's dtype follows the chain's operands, not the fp32 prefix maps
             dtypes += [A.dtype, B.dtype]
             seeded = self._seeded_ids
         state = None
         width = tail = None
-        for lf in p["leaves"]:
+        self.fused_leaves = 0
+        batched = self._batched_blocks(ev, Pa, Pb) if Pa is not None else None
+        if batched is None:
+            if Pa is not None:
+                self._seed(memo, Pa, Pb)  # the leaves read their coefficient stacks through the memo
+            batched = self._batched_leaves(ev)
+        if batched is not None:
+            state, width, tail, sdts = batched
+            dtypes += sdts
+            self.fused_leaves = len(p["leaves"])
+        for lf, sc in zip(() if batched is not None else p["leaves"], p["scores"]):
             if lf.op == "omd_elem":
-                s, a, b = ev(lf.args[0]), ev(lf.args[1]), ev(lf.args[2])
-                if not all(_kernel_dtype(t) for t in (s, a, b)):
-                    raise _Decline()
-                dtypes.append(s.dtype)
+                a, b = ev(lf.args[1]), ev(lf.args[2])
+                fused = self._fused_leaf(sc, a, b, ev) if sc is not None else None
+                if fused is not None:
+                    m, lv, num, wa, tl, sdts = fused
+                    self.fused_leaves += 1
+                else:
+                    s = ev(lf.args[0])
+                    if not all(_kernel_dtype(t) for t in (s, a, b)):
+                        raise _Decline()
+                    sdts = [s.dtype]
+                    m, lv, num, wa, tl = self._leaf_carrier(s, a, b)
+                dtypes += sdts
                 dtypes += [t.dtype for t, arg in ((a, lf.args[1]), (b, lf.args[2])) if id(arg) not in seeded]
-                m, lv, num, wa, tl = self._leaf_carrier(s, a, b)
             else:
                 m, lv, fa, fb = (ev(t) for t in lf.args)
                 if not all(_kernel_dtype(t) for t in (m, lv, fa, fb)):

@@ -404,6 +404,40 @@ def affd_scan(a: torch.Tensor, u: torch.Tensor, h0: torch.Tensor | None,
     return (out.reshape(T, *sshape) if out is not None else None), hf.reshape(sshape)
 
 
+def attn_carrier_f32(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float = 1.0) -> tuple:
+    """The om element of ``s = scale · q kᵀ`` over values ``v`` in fp32:
+    ``(m (…,Tq,1), l (…,Tq,1), a (…,Tq,dv))``, ``dk ≤ 128``, ``dv ≤ 256``.
+    ``k (…,Tk,dk)``; ``q (…,Tq,dk)`` or ``(Tq,dk)`` and ``v (…,Tk,dv)`` or
+    ``(Tk,dv)``, a 2-D operand shared over the leading axes."""
+    _need_device(q, k, v)
+    lib = L.load()
+    lead = tuple(k.shape[:-2])
+    Tq, dk = q.shape[-2], q.shape[-1]
+    Tk, dv = k.shape[-2], v.shape[-1]
+    if k.shape[-1] != dk or v.shape[-2] != Tk or (q.dim() > 2 and tuple(q.shape[:-2]) != lead) or \
+            (v.dim() > 2 and tuple(v.shape[:-2]) != lead):
+        raise ValueError(f"attn_carrier_f32: q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)} do not fit")
+    nb = math.prod(lead) if lead else 1
+    if q.dim() == 2:  # one query block shared by every key block
+        q3, q_sb = q.to(torch.float32).contiguous(), 0
+    else:
+        q3, q_sb = q.to(torch.float32).reshape(nb, Tq, dk).contiguous(), Tq * dk
+    k3 = k.to(torch.float32).reshape(nb, Tk, dk).contiguous()
+    if v.dim() == 2:
+        v3, v_sb = v.to(torch.float32).contiguous(), 0
+    else:
+        v3 = v.to(torch.float32).reshape(nb, Tk, dv).contiguous()
+        v_sb = Tk * dv
+    m = torch.empty((nb, Tq), dtype=torch.float32, device=q.device)
+    lv = torch.empty((nb, Tq), dtype=torch.float32, device=q.device)
+    a = torch.empty((nb, Tq, dv), dtype=torch.float32, device=q.device)
+    st = lib.catopt_hip_attn_carrier_f32(nb, Tq, Tk, dk, dv, _ptr(q3), q_sb, dk, _ptr(k3), Tk * dk, dk,
+                                         _ptr(v3), v_sb, dv, float(scale), _ptr(m), _ptr(lv), _ptr(a), Tq * dv, dv,
+                                         _stream(q))
+    L.check("catopt_hip_attn_carrier_f32", st)
+    return m.reshape(*lead, Tq, 1), lv.reshape(*lead, Tq, 1), a.reshape(*lead, Tq, dv)
+
+
 def aff_scan(A: torch.Tensor, b: torch.Tensor, h0: torch.Tensor, chunk_starts, *,
              schedule: int = L.SCAN_AUTO, states: bool = True):
     """Dense affine scan over the leading axis: ``X_t = A_t X_{t-1} + b_t 1ᵀ``.

@@ -259,6 +259,28 @@ int32_t catopt_hip_ssm_scan(int64_t B, int64_t T, int64_t D, int64_t N,
                             int64_t workspace_bytes, void* stream);
 
 /*
+ * fp32 attention carrier: the om element of the score block s = scale·q kᵀ
+ * over values v whose width dv is independent of the key width dk,
+ *   m = rowmax(s),  l = Σ_k exp(s − m),  a = Σ_k exp(s − m) v_k
+ * per query row (the (m, l, a) triple of _om_elem, torch_bridge.py:1974-1981;
+ * the deferred-affine omd_elem, xcarrier.py:380-400, with v = [fa | fb]).
+ * q: [batch, Tq, dk] with batch stride q_sb and row stride ldq; k: [batch,
+ * Tk, dk] (k_sb, ldk); v: [batch, Tk, dv] (v_sb, ldv; a stride of 0 shares
+ * one block); m_out, l_out: [batch, Tq] contiguous; num: [batch, Tq, dv]
+ * (num_sb, ldn).  A row with no finite score gets the empty carrier
+ * (m = −∞, l = 0, a = 0).  dk ≤ 128, dv ≤ 256 (else CATOPT_E_UNSUPPORTED).
+ * Replaces the score-block leaf of BatchedOmdModule's level loop
+ * (omd_lower.py:885-898): the scores and exponentials stay on chip.
+ */
+int32_t catopt_hip_attn_carrier_f32(int64_t batch, int64_t Tq, int64_t Tk,
+                                    int64_t dk, int64_t dv, const float* q,
+                                    int64_t q_sb, int64_t ldq, const float* k,
+                                    int64_t k_sb, int64_t ldk, const float* v,
+                                    int64_t v_sb, int64_t ldv, float scale,
+                                    float* m_out, float* l_out, float* num,
+                                    int64_t num_sb, int64_t ldn, void* stream);
+
+/*
  * Dense affine scan over T steps of P slots, each carrying a d x k state
  * (fp32, 1 ≤ d ≤ 64, k ≥ 1):
  *   X_t[p] = A_t[p] · X_{t-1}[p] + b_t[p] 1ᵀ,   X_{-1} = h0 (NULL = 0)

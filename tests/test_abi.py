@@ -99,3 +99,10 @@ def test_host_argument_checks(lib):
     assert lib.catopt_hip_aff_scan(4, 2, 16, 0, *args, 0, None, None, None, 0, None) == L.E_INVAL
     assert lib.catopt_hip_aff_scan(4, 2, 16, 1, None, -1, 0, None, 16, 0, None, table, 1, 0, None, None,
                                    None, 0, None) == L.E_INVAL
+    # fp32 carrier: dk / dv beyond the templates, bad leading dimension
+    assert lib.catopt_hip_attn_carrier_f32(1, 4, 4, 129, 8, None, 0, 129, None, 0, 129, None, 0, 8, 1.0,
+                                           None, None, None, 0, 8, None) == L.E_UNSUPPORTED
+    assert lib.catopt_hip_attn_carrier_f32(1, 4, 4, 16, 300, None, 0, 16, None, 0, 16, None, 0, 300, 1.0,
+                                           None, None, None, 0, 300, None) == L.E_UNSUPPORTED
+    assert lib.catopt_hip_attn_carrier_f32(1, 4, 4, 16, 8, None, 0, 8, None, 0, 16, None, 0, 8, 1.0,
+                                           None, None, None, 0, 8, None) == L.E_INVAL

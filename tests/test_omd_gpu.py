@@ -154,3 +154,42 @@ def test_omd_graph_replay_and_fp64_fallback(sink, dev):
     assert mod.fallbacks == 1 and out64.dtype == torch.float64
     rep = oracle.verify_equiv(_reference(*ins, False), out64.cpu().numpy(), rtol=1e-10)
     assert rep["passed"], rep
+
+
+@pytest.mark.parametrize("dk,dv,Tq,Tk", [(64, 128, 300, 256), (5, 33, 17, 45), (128, 256, 130, 97),
+                                         (16, 1, 64, 32), (32, 64, 1, 1)])
+def test_attn_carrier_f32_matches_om_elem(dev, dk, dv, Tq, Tk):
+    """The fused carrier kernel against the oracle's om_elem on the same
+    fp32 scores: ragged query / key counts, widths that pad the templates,
+    a batch with per-batch values, and a negative scale (whose max is the
+    raw minimum)."""
+    from catopt_amd import kernels as K
+
+    rng = np.random.default_rng(dk * 7 + dv)
+    for lead, shared_v, scale in (((), True, 0.3), ((2,), False, -0.7), ((3,), True, 1.0)):
+        # attention-scaled queries: scores of order one, as in softmax attention (unscaled
+        # unit-normal q·k at dk = 128 reach |s| ~ 40, where the fp32 rounding of the dot
+        # product alone is 1e-5 of exp(s))
+        q = (rng.standard_normal((*lead, Tq, dk)) / np.sqrt(dk)).astype(np.float32)
+        k = rng.standard_normal((*lead, Tk, dk)).astype(np.float32)
+        v = rng.standard_normal((Tk, dv) if shared_v else (*lead, Tk, dv)).astype(np.float32)
+        m, lv, a = K.attn_carrier_f32(*(torch.from_numpy(z).to(dev) for z in (q, k, v)), scale)
+        s = scale * (q.astype(np.float64) @ np.swapaxes(k.astype(np.float64), -1, -2))
+        rm, rl, ra = oracle.om_elem(s, v.astype(np.float64))
+        _gate(rm, m, TOL_F32)
+        _gate(rl, lv, TOL_F32)
+        _gate(ra, a, TOL_F32)
+    # no keys: the empty carrier
+    m, lv, a = K.attn_carrier_f32(torch.zeros(4, dk, device=dev), torch.zeros(0, dk, device=dev),
+                                  torch.zeros(0, dv, device=dev))
+    assert torch.isneginf(m).all() and not lv.any() and not a.any()
+
+
+def test_omd_leaves_run_the_fused_kernel(dev):
+    T, d, Tq, nb, dk = 256, 32, 40, 4, 16
+    ir, _ = forms.omd_scan_attention_form(T, d, Tq, nb, dk)
+    ins = _inputs(T, d, Tq, dk, False, 6)
+    mod = HipOmdModule(ir, {})
+    out = mod(*(t.to(dev) for t in ins))
+    assert mod.fallbacks == 0 and mod.fused_leaves == nb
+    _gate(_reference(*ins, False), out, TOL_F32)
