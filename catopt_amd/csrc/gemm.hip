@@ -124,7 +124,11 @@ __global__ __launch_bounds__(NTH) void gemm_generic(
 // (4*(l/16) + r, l%16).  The k index of the MFMA is only a summation order,
 // so each lane loads 4 consecutive k with one 16-byte load and feeds them to
 // 4 consecutive MFMA steps (the same permutation on both operands).
-constexpr int SK_CHUNK = 64;  // k per wave per pass: 16 per lane group
+#ifndef CATOPT_SK_CHUNK
+#define CATOPT_SK_CHUNK 64
+#endif
+constexpr int SK_CHUNK = CATOPT_SK_CHUNK;  // k per wave per pass (one load round trip)
+constexpr int SK_STEPS = SK_CHUNK / 16;    // 16-k steps per pass: 4 per lane group each
 
 __device__ __forceinline__ f32x4 mfma16x16x4f32(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -142,20 +146,20 @@ __global__ __launch_bounds__(256) void gemm_f32_skinny(
   const int am = min(m0 + r16, M - 1), wn = min(n0 + r16, N - 1);  // clamped rows are never stored
   const float* arow = A + (int64_t)am * lda;
   const float* wrow = W + (int64_t)wn * ldw;
-  const int kper = ((K + 4 * SK_CHUNK - 1) / (4 * SK_CHUNK)) * SK_CHUNK;  // k per wave, multiple of 64
+  const int kper = ((K + 4 * SK_CHUNK - 1) / (4 * SK_CHUNK)) * SK_CHUNK;  // k per wave, multiple of SK_CHUNK
   const int kbeg = wave * kper, kend = min(K, kbeg + kper);
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int kb = kbeg; kb < kend; kb += SK_CHUNK) {
-    f32x4 av[4], bv[4];
+    f32x4 av[SK_STEPS], bv[SK_STEPS];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < SK_STEPS; ++s) {
       const int k = kb + 16 * s + 4 * kq;  // K % 4 == 0: a group is wholly in or out
       const bool ok = k < kend;
       av[s] = ok ? *reinterpret_cast<const f32x4*>(arow + k) : f32x4{0.f, 0.f, 0.f, 0.f};
       bv[s] = ok ? *reinterpret_cast<const f32x4*>(wrow + k) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+    for (int s = 0; s < SK_STEPS; ++s)
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc = mfma16x16x4f32(av[s][e], bv[s][e], acc);
   }
