@@ -23,6 +23,14 @@ for both affine carriers:
   where each ``f_i = compose(leaf_i, f_{i-1})`` extends the previous prefix by
   one step (checked structurally, not assumed).
 
+A third root extends the reference's (which routes it to the generic
+executor): a read-out ``sum(mul(S, c), dim)`` of either root ``S``, the
+selective SSM's ``y_t = Σ_n c_t[n]·h_t[…, n]``.  It is planned as the inner
+scan followed by ``mul`` / ``sum``; when the leaf offsets are the outer
+product ``x_t ⊗ bx_t`` of two gathered step reads and the states stack along
+axis 1 of a ``(B, D, N)`` state, scan and read-out run as one SSM kernel
+launch and the ``(B, T, D, N)`` states are never written.
+
 As in the reference's plan builder, nested applications are folded into the
 compose spine first (``apply(f, apply(g, h)) → apply(compose(f, g), h)``,
 ``scan_lower.py:131-165``) and pure view wrappers around the root are peeled
@@ -222,11 +230,21 @@ def _same_term(x: Any, y: Any) -> bool:
 def build_scan_plan(root: Any) -> dict | None:
     root = fold_nested_apply(root)
     root, post = strip_output_views(root)
+    ro = _readout(root)
+    if ro is not None:
+        # a read-out contraction of the states: planned as the inner scan plus
+        # ``mul`` / ``sum`` after its own view wrappers
+        inner = build_scan_plan(ro[0])
+        if inner is None:
+            return None
+        factors = _offset_factors(inner["leaves"]) if inner["domain"] == "diag" else None
+        return {**inner, "post": post, "inner_post": inner["post"], "factors": factors,
+                "readout": {"c": ro[1], "dim": ro[2]}}
     if not isinstance(root, Op) or root.op not in _CARRIERS or len(root.args) != 2:
         return None
     leaf_op, comp_op, proj_a, proj_b, domain = _CARRIERS[root.op]
     F, h = root.args
-    base = {"domain": domain, "h": h, "post": post}
+    base = {"domain": domain, "h": h, "post": post, "inner_post": [], "readout": None, "factors": None}
     if is_op(F, leaf_op, 2):
         pa, pb = _proj_list(F.args[0], proj_a), _proj_list(F.args[1], proj_b)
         if pa is not None and pb is not None:
@@ -266,20 +284,68 @@ def _step_index(t: Any) -> tuple | None:
     return None
 
 
+def _step_view(t: Any) -> tuple | None:
+    """``(base, dim, index, unsqueezes)`` of a step read wrapped in
+    ``unsqueeze`` ops (``unsqueezes`` innermost first)."""
+    unsq: list = []
+    while is_op(t, "unsqueeze", 1):
+        unsq.append(int(attr_of(t.attrs, "dim", default=0)))
+        t = t.args[0]
+    s = _step_index(t)
+    return None if s is None else (*s, tuple(reversed(unsq)))
+
+
+def _gather_spec(terms: list) -> tuple | None:
+    """``(base, dim, indices, unsqueezes)`` when every term reads one step of
+    one shared base along one axis, with the same view wrappers."""
+    views = [_step_view(t) for t in terms]
+    if not views or any(v is None for v in views):
+        return None
+    base, dim, _, unsq = views[0]
+    if any(not _same_term(v[0], base) or v[1] != dim or v[3] != unsq for v in views):
+        return None
+    return base, dim, [v[2] for v in views], unsq
+
+
 def _shared_gather(leaves: list) -> dict:
     """Per leaf slot (0: linear part, 1: offset) whose operands all index one
-    base term along one axis: ``(base, dim, indices)`` in time order
-    (``_leaf_b_gather``, scan_lower.py:308-337, extended to the linear part)."""
+    base term along one axis: ``(base, dim, indices, unsqueezes)`` in time
+    order (``_leaf_b_gather``, scan_lower.py:308-337, extended to the linear
+    part and to ``unsqueeze``-wrapped reads)."""
     out = {}
     for slot in (0, 1):
-        idx = [_step_index(lf.args[slot]) for lf in leaves]
-        if any(i is None for i in idx):
-            continue
-        base, dim = idx[0][0], idx[0][1]
-        if any(not _same_term(i[0], base) for i in idx) or any(i[1] != dim for i in idx):
-            continue
-        out[slot] = (base, dim, [i[2] for i in idx])
+        g = _gather_spec([lf.args[slot] for lf in leaves])
+        if g is not None:
+            out[slot] = g
     return out
+
+
+def _offset_factors(leaves: list) -> list | None:
+    """When every leaf offset is ``mul(f_t, g_t)`` of two gathered step
+    reads (the input term ``x_t ⊗ bx_t`` of a selective SSM): the two gather
+    specs, else None."""
+    if not all(is_op(lf.args[1], "mul", 2) for lf in leaves):
+        return None
+    out = [_gather_spec([lf.args[1].args[k] for lf in leaves]) for k in (0, 1)]
+    return None if any(g is None for g in out) else out
+
+
+def _readout(t: Any) -> tuple | None:
+    """``(states, c, dim)`` of ``sum(mul(states, c), dim)`` (either operand
+    order) whose ``states`` operand is an affine-scan root."""
+    if not is_op(t, "sum", 1) or bool(attr_of(t.attrs, "keepdim", default=False)):
+        return None
+    dim = attr_of(t.attrs, "dim", "axis", default=None)
+    if isinstance(dim, (list, tuple)):
+        dim = dim[0] if len(dim) == 1 else None
+    if dim is None or not is_op(t.args[0], "mul", 2):
+        return None
+    m = t.args[0]
+    for s, c in ((m.args[0], m.args[1]), (m.args[1], m.args[0])):
+        core, _ = strip_output_views(fold_nested_apply(s))
+        if isinstance(core, Op) and core.op in _CARRIERS and len(core.args) == 2:
+            return s, c, int(dim)
+    return None
 
 
 def is_scan_term(term: Any) -> bool:
@@ -300,6 +366,7 @@ class HipScanModule(HipExecutorBase, nn.Module):
         self._inputs = list(ir.inputs)
         self._const_cache: dict = {}
         self.fallbacks = 0
+        self.fused_readouts = 0  # calls whose read-out ran inside the SSM kernel
         self.schedule = L.SCAN_AUTO if schedule is None else schedule
         self._plan = build_scan_plan(self.eval_mod._root)
         self._init_graph_state()
@@ -314,22 +381,44 @@ class HipScanModule(HipExecutorBase, nn.Module):
         stacked prefix form, whose map is one leaf in the reference's plan)."""
         return 0 if self._plan is None else self._plan["levels"]
 
+    def _gathered(self, ev, key: Any, spec: tuple) -> torch.Tensor | None:
+        """Step-major stack (a step-0 axis) of the reads ``spec`` describes:
+        the base itself when it holds the steps in order along ``dim``,
+        else one ``index_select``; the per-step ``unsqueeze`` wrappers are
+        re-applied with their axes shifted past the step axis."""
+        base_t, dim, idx, unsq = spec
+        T = len(idx)
+        base = ev(base_t)
+        if not isinstance(base, torch.Tensor) or not -base.dim() <= dim < base.dim():
+            return None
+        if idx == list(range(T)) and base.shape[dim] == T:
+            out = base.movedim(dim, 0)
+        elif all(-base.shape[dim] <= i < base.shape[dim] for i in idx):
+            ix = self._cached(("idx", key, tuple(idx)), base,
+                              lambda t: torch.tensor(idx, dtype=torch.long, device=t.device),
+                              dtype=torch.long)
+            out = base.index_select(dim, ix).movedim(dim, 0)
+        else:
+            return None
+        for d in unsq:
+            out = out.unsqueeze(d + 1 if d >= 0 else d)
+        return out
+
     def _slot_values(self, ev, slot: int) -> torch.Tensor | None:
         """Step-major stack of leaf operand ``slot`` (a step-0 axis)."""
         p = self._plan
-        T = len(p["leaves"])
         g = p["gather"].get(slot)
         if g is not None:
-            base_t, dim, idx = g
-            base = ev(base_t)
-            if isinstance(base, torch.Tensor) and -base.dim() <= dim < base.dim():
-                if idx == list(range(T)) and base.shape[dim] == T:
-                    return base.movedim(dim, 0)
-                if all(-base.shape[dim] <= i < base.shape[dim] for i in idx):
-                    ix = self._cached(("idx", slot, tuple(idx)), base,
-                                      lambda t: torch.tensor(idx, dtype=torch.long, device=t.device),
-                                      dtype=torch.long)
-                    return base.index_select(dim, ix).movedim(dim, 0)
+            out = self._gathered(ev, slot, g)
+            if out is not None:
+                return out
+        if slot == 1 and p["factors"] is not None:
+            f0, f1 = (self._gathered(ev, ("f", k), p["factors"][k]) for k in (0, 1))
+            if f0 is not None and f1 is not None:
+                try:
+                    return torch.mul(f0, f1)
+                except RuntimeError:
+                    pass
         vals = [torch.as_tensor(ev(lf.args[slot])) for lf in p["leaves"]]
         try:
             tgt = torch.broadcast_shapes(*[v.shape for v in vals])
@@ -337,11 +426,20 @@ class HipScanModule(HipExecutorBase, nn.Module):
             return None
         return torch.stack([v.expand(tgt) for v in vals])
 
-    def _apply_post(self, out: Any) -> Any:
+    def _apply_views(self, out: Any, post: list) -> Any:
         tab = self.eval_mod._bindings().torch_bindings
-        for op, attrs in reversed(self._plan["post"]):
+        for op, attrs in reversed(post):
             out = tab[op](out, **attrs)
         return out
+
+    def _apply_post(self, out: Any) -> Any:
+        return self._apply_views(out, self._plan["post"])
+
+    def _apply_readout(self, ev, states: Any) -> Any:
+        """``sum(mul(states, c), dim)`` through the op table."""
+        ro = self._plan["readout"]
+        tab = self.eval_mod._bindings().torch_bindings
+        return tab["sum"](tab["mul"](states, ev(ro["c"])), dim=ro["dim"])
 
     def _forward_impl(self, *xs: Any) -> Any:
         p = self._plan
@@ -349,7 +447,13 @@ class HipScanModule(HipExecutorBase, nn.Module):
             return self.eval_mod(*xs)
         x, env = self._input_env(xs)
         ev = self.ev_factory(env, x)
-        out = self._forward_diag(ev) if p["domain"] == "diag" else self._forward_dense(ev)
+        out = self._forward_ssm(ev) if p["readout"] is not None else None
+        if out is not None:
+            self.fused_readouts += 1
+        else:
+            out = self._forward_diag(ev) if p["domain"] == "diag" else self._forward_dense(ev)
+            if out is not None and p["readout"] is not None:
+                out = self._apply_readout(ev, self._apply_views(out, p["inner_post"]))
         if out is None:
             self.fallbacks += 1
             return self.eval_mod(*xs)
@@ -377,10 +481,26 @@ class HipScanModule(HipExecutorBase, nn.Module):
         if not shared and a.shape[0] != T:
             return None
         out_dtype = torch.promote_types(torch.promote_types(a.dtype, u.dtype), h.dtype)
+        sa, su = (a.shape if shared else a.shape[1:]), u.shape[1:]
+        if p["mode"] == "prefix":
+            # stack(a-prefixes, dim) ⊙ h + stack(b-prefixes, dim): both stacks
+            # must line up, and h must be one state for every step
+            R = len(su) + 1
+            if len(sa) != len(su) or not -R <= p["dim"] < R or h.dim() > R:
+                return None
+            ax = h.dim() - R + p["dim"] % R  # the axis of h aligned with the stacked one
+            if ax >= 0:
+                if h.shape[ax] != 1:
+                    return None
+                h = h.squeeze(ax)
         try:
-            sshape = torch.broadcast_shapes(a.shape if shared else a.shape[1:], u.shape[1:], h.shape)
+            sshape = torch.broadcast_shapes(sa, su, h.shape)
         except RuntimeError:
             return None
+        if len(sa) < len(sshape):
+            a = a.reshape(a.shape[:0 if shared else 1] + (1,) * (len(sshape) - len(sa)) + tuple(sa))
+        if len(su) < len(sshape):
+            u = u.reshape((T,) + (1,) * (len(sshape) - len(su)) + tuple(su))
         a_ = a.expand(sshape) if shared else a.expand(T, *sshape)
         u_ = u.expand(T, *sshape)
         h_ = h.expand(sshape)
@@ -388,7 +508,56 @@ class HipScanModule(HipExecutorBase, nn.Module):
                                  states=p["mode"] == "prefix")
         if p["mode"] == "final":
             return hf.to(out_dtype)
-        return states.to(out_dtype).movedim(0, p["dim"])
+        return states.to(out_dtype).movedim(0, p["dim"] % (len(sshape) + 1))
+
+    def _forward_ssm(self, ev) -> torch.Tensor | None:
+        """Every prefix state read out in the kernel: the selective SSM
+        ``h_t = a_t ⊙ h_{t-1} + x_t ⊗ bx_t`` over a ``(B, D, N)`` state, stacked
+        along axis 1, contracted with ``c (B, T, 1, N)`` over ``N``, so the
+        ``(B, T, D, N)`` states never reach HBM.  None when the operands do
+        not have that layout (the caller then scans and reads out apart)."""
+        p = self._plan
+        fac = p["factors"]
+        if fac is None or p["mode"] != "prefix" or p["inner_post"] or p["domain"] != "diag":
+            return None
+        T = len(p["leaves"])
+        f0, f1 = (self._gathered(ev, ("f", k), fac[k]) for k in (0, 1))
+        if f0 is None or f1 is None or f0.dim() != 4 or f1.dim() != 4 or T == 0:
+            return None
+        # the input term: one factor (T, B, D, 1), the other (T, B, 1, N)
+        xs, bs = (f0, f1) if f0.shape[-1] == 1 and f1.shape[-2] == 1 else (f1, f0)
+        if xs.shape[-1] != 1 or bs.shape[-2] != 1 or xs.shape[:2] != (T, bs.shape[1]) or bs.shape[0] != T:
+            return None
+        B, D, N = xs.shape[1], xs.shape[2], bs.shape[3]
+        if N not in (4, 8, 16, 32, 64) or p["dim"] % 4 != 1 or p["readout"]["dim"] % 4 != 3:
+            return None
+        if p["a_shared"] and p["gather"].get(0) is None:
+            a1 = torch.as_tensor(ev(p["leaves"][0].args[0]))
+            A = a1.unsqueeze(0).expand(T, *a1.shape) if a1.dim() == 3 else None
+        else:
+            A = self._slot_values(ev, 0)
+        h, c = ev(p["h"]), ev(p["readout"]["c"])
+        if A is None or A.dim() != 4 or A.shape[0] != T or not self._kernel_ok(A, xs, bs, h, c):
+            return None
+        try:
+            if torch.broadcast_shapes(A.shape[1:], (B, D, N)) != (B, D, N):
+                return None
+            if torch.broadcast_shapes(h.shape, (B, 1, D, N)) != (B, 1, D, N):
+                return None  # h varies along the stacked axis: not one scan
+            if torch.broadcast_shapes(c.shape, (B, T, 1, N)) != (B, T, 1, N):
+                return None  # c varies along D: not a read-out over N
+        except RuntimeError:
+            return None
+        # a per channel (…, D, 1) runs the kernel's broadcast-over-N form
+        a = A.movedim(0, 1)
+        a = a.squeeze(-1).expand(B, T, D) if A.shape[-1] == 1 and N > 1 else a.expand(B, T, D, N)
+        out_dtype = A.dtype
+        for t in (xs, bs, h, c):
+            out_dtype = torch.promote_types(out_dtype, t.dtype)
+        y = K.ssm_scan(a, bs[:, :, 0, :].movedim(0, 1), c.expand(B, T, 1, N)[:, :, 0, :],
+                       xs[..., 0].movedim(0, 1), h.expand(B, 1, D, N)[:, 0], p["table"],
+                       schedule=self.schedule)
+        return y.to(out_dtype)
 
     # ---------------------------------------------------------------- dense
 

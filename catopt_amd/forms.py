@@ -47,6 +47,7 @@ __all__ = [
     "linear_recurrence_form",
     "dense_scan_form",
     "dense_scan_prefix_form",
+    "diag_ssm_form",
     "omd_scan_attention_form",
 ]
 
@@ -244,6 +245,35 @@ def dense_scan_prefix_form(T: int, d: int, *, time_varying: bool = True, dim: in
     SA = mk("stack", *[mk("aff_A", f) for f in fs], dim=dim)
     SB = mk("stack", *[mk("aff_b", f) for f in fs], dim=dim)
     return IR(mk("apply", mk("aff", SA, SB), h), [A, b, h]), {}
+
+
+def diag_ssm_form(B: int, T: int, D: int, N: int, *, a_per_state: bool = True) -> tuple[IR, dict]:
+    """The selective diagonal SSM with every output: the ``DiagonalSSM`` step
+    (models/ssm.py:121-160) over a ``(B, D, N)`` state,
+    ``h_t = a_t ⊙ h_{t-1} + x_t ⊗ bx_t``, read out as
+    ``y_t = Σ_n c_t[n]·h_t[…, n]``.  Delivered as the stacked all-prefix form
+    (xcarrier.py:2252-2273) inside the contraction:
+    ``sum(mul(applyd(aff_diag(stack(affd_a f_t, dim=1), stack(affd_b f_t,
+    dim=1)), unsqueeze(h, 1)), unsqueeze(c, 2)), dim=-1)`` with
+    ``f_t = affd_compose(aff_diag(a_t, x_t ⊗ bx_t), f_{t-1})``.
+    ``a_per_state=False`` takes ``a (B, T, D)``, broadcast over ``N``."""
+    a = Var("a", TensorType((B, T, D, N) if a_per_state else (B, T, D)))
+    bx, c = Var("bx", TensorType((B, T, N))), Var("c", TensorType((B, T, N)))
+    x, h = Var("x", TensorType((B, T, D))), Var("h", TensorType((B, D, N)))
+    fs = []
+    for t in range(T):
+        at = mk("select", a, dim=1, index=t)
+        if not a_per_state:
+            at = mk("unsqueeze", at, dim=-1)
+        ut = mk("mul", mk("unsqueeze", mk("select", x, dim=1, index=t), dim=-1),
+                mk("unsqueeze", mk("select", bx, dim=1, index=t), dim=-2))
+        leaf = mk("aff_diag", at, ut)
+        fs.append(leaf if t == 0 else mk("affd_compose", leaf, fs[-1]))
+    states = mk("applyd", mk("aff_diag", mk("stack", *[mk("affd_a", f) for f in fs], dim=1),
+                             mk("stack", *[mk("affd_b", f) for f in fs], dim=1)),
+                mk("unsqueeze", h, dim=1))
+    y = mk("sum", mk("mul", states, mk("unsqueeze", c, dim=2)), dim=-1)
+    return IR(y, [a, bx, c, x, h]), {}
 
 
 def omd_scan_attention_form(T: int, d: int, Tq: int, blocks: int, dk: int = 16, *,

@@ -317,6 +317,38 @@ def test_scan_module_fallback_matches_the_serial_recurrence():
     assert oracle.verify_equiv(refp, _np(modp(a, u, h)), rtol=1e-12)["passed"]
 
 
+def test_ssm_readout_plan_and_fallback():
+    """The selective SSM delivered as a read-out of the stacked prefix
+    states: planned as a prefix scan with its input factors and read-out
+    recognised, routed to the scan executor, and (on host tensors, outside
+    the kernels' envelope) run by the generic module to the serial
+    recurrence's values."""
+    B, T, D, N = 2, 9, 3, 4
+    for per_state in (True, False):
+        ir, _ = forms.diag_ssm_form(B, T, D, N, a_per_state=per_state)
+        p = build_scan_plan(ir.root)
+        assert p is not None and p["mode"] == "prefix" and p["dim"] == 1 and p["domain"] == "diag"
+        assert p["readout"]["dim"] == -1 and p["inner_post"] == [] and p["post"] == []
+        (fx, fb) = p["factors"]
+        assert fx[1] == 1 and fx[2] == list(range(T)) and fx[3] == (-1,)
+        assert fb[1] == 1 and fb[2] == list(range(T)) and fb[3] == (-2,)
+        assert p["gather"][0][2] == list(range(T)) and p["gather"][0][3] == (() if per_state else (-1,))
+        assert route_spec(ir.root, HipSink(device="cpu", ops=cpu_table())).name == "scan"
+        g = torch.Generator().manual_seed(3)
+        a = torch.rand((B, T, D, N) if per_state else (B, T, D), generator=g, dtype=torch.float64)
+        bx, c = (torch.randn(B, T, N, generator=g, dtype=torch.float64) for _ in range(2))
+        x = torch.randn(B, T, D, generator=g, dtype=torch.float64)
+        h = torch.randn(B, D, N, generator=g, dtype=torch.float64)
+        mod = HipScanModule(ir, {}, ops=cpu_table())
+        out = mod(a, bx, c, x, h)
+        assert mod.fallbacks == 1 and out.shape == (B, T, D)
+        ref, _ = oracle.ssm_serial(*(_np(t) for t in (a, bx, c, x, h)))
+        assert oracle.verify_equiv(ref, _np(out), rtol=1e-12)["passed"]
+    # a contraction whose operand is not a scan root is not a read-out
+    v = Var("v", TensorType((3, 4)))
+    assert build_scan_plan(mk("sum", mk("mul", v, v), dim=-1)) is None
+
+
 # ---------------------------------------------------------------------- sink
 
 

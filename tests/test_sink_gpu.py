@@ -204,3 +204,34 @@ def test_scan_executor(sink, dev, form):
     out2 = res.module(torch.from_numpy(a2).to(dev), ins[1], ins[2]).clone()
     ref2 = oracle.serial_affd_scan(a2.astype(np.float64), u.astype(np.float64), h.astype(np.float64))
     _gate(ref2[-1] if form == "final" else ref2, out2, 1e-5)
+
+
+@pytest.mark.parametrize("N,per_state,dtype", [(16, True, torch.float32), (8, False, torch.float32),
+                                               (3, True, torch.float32), (16, True, torch.bfloat16)])
+def test_ssm_readout_executor(sink, dev, N, per_state, dtype):
+    """The selective SSM delivered as sum(mul(<stacked prefix states>, c), -1):
+    N in the kernel's set runs the fused scan + read-out (the states never
+    reach HBM); N = 3 scans every prefix state along the stacked axis and
+    reads out through the op table.  Replays follow new inputs."""
+    B, T, D = 2, 300, 24
+    ir, _ = forms.diag_ssm_form(B, T, D, N, a_per_state=per_state)
+    rng = np.random.default_rng(8 + N)
+
+    def inputs():
+        z = rng.standard_normal((B, T, D, N) if per_state else (B, T, D))
+        vals = (1.0 / (1.0 + np.exp(z)), rng.standard_normal((B, T, N)), rng.standard_normal((B, T, N)),
+                rng.standard_normal((B, T, D)), rng.standard_normal((B, D, N)))  # a = exp(-softplus(z))
+        return tuple(torch.from_numpy(v.astype(np.float32)).to(dtype).to(dev) for v in vals)
+
+    ins = inputs()
+    res = deliver(ir, {}, sink, ins, runner=HipGraphRunner())
+    assert res.stats["executor"] == "scan" and res.stats["hip_kernel"] and res.stats["cuda_graph"] is True
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    for _ in range(2):
+        out = res.module(*ins).clone()
+        assert out.dtype == dtype and out.shape == (B, T, D)
+        ref, _ = oracle.ssm_serial(*(_np(t) for t in ins))
+        _gate(ref, out, tol)
+        ins = inputs()
+    mod = res.module
+    assert mod.fallbacks == 0 and (mod.fused_readouts > 0) == (N != 3)
