@@ -9,8 +9,10 @@
 //
 // Tiling: 256x256 block tile, BK = 64, 8 waves in a 2x4 grid (two per
 // SIMD), each wave a 128x64 sub-tile = 4x2 MFMA blocks.  Tiles reach LDS by
-// direct global->LDS loads (global_load_lds_dwordx4): no register staging,
-// no LDS store instructions.  A ring of LDS stages (two of 64 KB): the loads
+// direct buffer->LDS loads (buffer_load_dwordx4 ... lds) through buffer
+// resources over the tile's rows: one precomputed 32-bit offset per load slot
+// plus the K offset, so a tile's loads cost no 64-bit address arithmetic; no
+// register staging, no LDS store instructions.  A ring of LDS stages (two of 64 KB): the loads
 // of K tile t+1 are issued before the MFMAs of tile t, one barrier per K
 // tile.  Within a tile the fragments of k-step s+1 are read before the MFMAs
 // of k-step s, and the last k-step's MFMAs are issued after the barrier,
@@ -21,8 +23,10 @@
 // XOR-swizzled so a fragment read's 16 rows per pass hit 16 bank groups.
 //
 // Edges: rows past M (A) or N (B) load a clamped, valid row and are never
-// stored; a K tail (K % 64 != 0, K % 8 == 0) loads clamped chunks and then
-// zeroes the chunks past K in LDS before they are read.
+// stored; in a K tail (K % 64 != 0, K % 8 == 0) the chunks past K read the
+// next row's head or, past the operand's end, the buffer range check's zero,
+// and are zeroed in LDS before they are read.  Every offset within a tile's
+// rows must fit in 31 bits (checked on the host).
 //
 // Paired epilogues (SILU_MUL / GLU): the B tile holds 128 rows of the first
 // projection and the 128 matching rows of the second (row n and row n + N of
@@ -131,40 +135,46 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_nt(
 
   // This thread's load slots: slot s = i*NT + wave*64 + lane of a tile is
   // (row s/8, swizzled chunk s%8); the global row is clamped to a valid one.
-  int64_t a_off[SLOTS_PER_THREAD], b_off[SLOTS_PER_THREAD];
-  int s_chunk[SLOTS_PER_THREAD];
+  // Buffer resources over this tile's rows: 32-bit offsets from the tile's
+  // first row (rows past M / N clamp to the last valid one); a paired tile
+  // reads its up rows through a second resource N rows further on.  The K
+  // offset rides in the per-lane offset, which the range check covers: a
+  // chunk past K of the tail tile reads the next row's head (in bounds) or,
+  // past the operand's last element, zero; zero_k_tail clears those chunks.
+  const uint16_t* Ab = A + (int64_t)m0 * lda;
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)Ab, (short)0, (int)((((int64_t)(M - 1 - m0)) * lda + K) * 2), 0x00020000);
+  const uint16_t* Bb0 = B + (int64_t)n0 * ldb;
+  const int b_rec = (int)((((int64_t)(N - 1 - n0)) * ldb + K) * 2);
+  const __amdgpu_buffer_rsrc_t rb0 = __builtin_amdgcn_make_buffer_rsrc((void*)Bb0, (short)0, b_rec, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb1 = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(Bb0 + (PAIRED ? (int64_t)N * ldb : 0)), (short)0, b_rec, 0x00020000);
+  uint32_t a_vo[SLOTS_PER_THREAD], b_vo[SLOTS_PER_THREAD];
+  bool b_hi[SLOTS_PER_THREAD];
 #pragma unroll
   for (int i = 0; i < SLOTS_PER_THREAD; ++i) {
     const int s = i * NT + wave * 64 + lane;
     const int r = s / CPR, cp = s % CPR;
     const int chunk = cp ^ chunk_swizzle(r);
-    s_chunk[i] = chunk;
-    const int am = min(m0 + r, M - 1);
-    int bn;
-    if (PAIRED) {
-      const int half = r >> 7, rr = r & 127;
-      bn = min(n0 + rr, N - 1) + half * N;
-    } else {
-      bn = min(n0 + r, N - 1);
-    }
-    a_off[i] = (int64_t)am * lda + chunk * 8;
-    b_off[i] = (int64_t)bn * ldb + chunk * 8;
+    const int am = min(r, M - 1 - m0);
+    const int bn = PAIRED ? min(r & 127, N - 1 - n0) : min(r, N - 1 - n0);
+    b_hi[i] = PAIRED && r >= 128;
+    a_vo[i] = (uint32_t)(((int64_t)am * lda + chunk * 8) * 2);
+    b_vo[i] = (uint32_t)(((int64_t)bn * ldb + chunk * 8) * 2);
   }
 
   const int ktiles = (K + BK - 1) / BK;
   const bool k_tail = (K % BK) != 0;
 
   auto issue = [&](int kt, int stage) {
-    const int k0 = kt * BK;
+    const uint32_t koff = (uint32_t)kt * (BK * 2);
     char* sa = lds + stage * STAGE_BYTES;
-    const bool full = !k_tail || kt + 1 < ktiles;
 #pragma unroll
     for (int i = 0; i < SLOTS_PER_THREAD; ++i) {
-      // a chunk past K reads chunk 0 of the tile instead (zeroed below)
-      const int kk = (full || k0 + s_chunk[i] * 8 < K) ? k0 : k0 - s_chunk[i] * 8;
       char* dst = sa + (i * NT + wave * 64) * 16;
-      __builtin_amdgcn_global_load_lds(A + a_off[i] + kk, (lds_ptr)dst, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(B + b_off[i] + kk, (lds_ptr)(dst + TILE_BYTES), 16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr)dst, 16, a_vo[i] + koff, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(b_hi[i] ? rb1 : rb0, (lds_ptr)(dst + TILE_BYTES), 16,
+                                               b_vo[i] + koff, 0, 0, 0);
     }
   };
   // zero the chunks past K of the tail tile (after its loads landed)
@@ -342,9 +352,11 @@ int32_t launch(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb,
 // Fast-path predicate shared with the dispatcher in gemm.hip.
 bool gemm_bf16_nt_fast_ok(int64_t M, int64_t N, int64_t K, const void* x, int64_t ldx,
                           const void* w, int64_t ldw, const void* y, int64_t ldy) {
+  // buffer offsets within one tile's rows: (255 * ld + K) * 2 bytes < 2^31
+  const bool offsets_fit = (256 * (ldx > ldw ? ldx : ldw) + K) * 2 < (1LL << 31);
   return M > 0 && N > 0 && K > 0 && M < (1LL << 31) && N < (1LL << 30) && K < (1LL << 31) &&
-         K % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0 && aligned16(x) && aligned16(w) &&
-         ldy >= 1 && y != nullptr;
+         K % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0 && ldx >= K && ldw >= K && offsets_fit &&
+         aligned16(x) && aligned16(w) && ldy >= 1 && y != nullptr;
 }
 
 int32_t gemm_bf16_nt_launch(int32_t epi, int64_t M, int64_t N, int64_t K, const void* x,
