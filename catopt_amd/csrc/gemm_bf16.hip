@@ -150,7 +150,9 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_nt(
   const __amdgpu_buffer_rsrc_t rb1 = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(Bb0 + (PAIRED ? (int64_t)N * ldb : 0)), (short)0, b_rec, 0x00020000);
   uint32_t a_vo[SLOTS_PER_THREAD], b_vo[SLOTS_PER_THREAD];
-  bool b_hi[SLOTS_PER_THREAD];
+  // slot i covers tile rows [i * NT / CPR, (i + 1) * NT / CPR): whether it
+  // reads up rows is known at compile time, so the resource stays uniform
+  static_assert(128 % (NT / CPR) == 0, "a load slot straddles the gate / up halves");
 #pragma unroll
   for (int i = 0; i < SLOTS_PER_THREAD; ++i) {
     const int s = i * NT + wave * 64 + lane;
@@ -158,7 +160,6 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_nt(
     const int chunk = cp ^ chunk_swizzle(r);
     const int am = min(r, M - 1 - m0);
     const int bn = PAIRED ? min(r & 127, N - 1 - n0) : min(r, N - 1 - n0);
-    b_hi[i] = PAIRED && r >= 128;
     a_vo[i] = (uint32_t)(((int64_t)am * lda + chunk * 8) * 2);
     b_vo[i] = (uint32_t)(((int64_t)bn * ldb + chunk * 8) * 2);
   }
@@ -173,7 +174,8 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_nt(
     for (int i = 0; i < SLOTS_PER_THREAD; ++i) {
       char* dst = sa + (i * NT + wave * 64) * 16;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr)dst, 16, a_vo[i] + koff, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(b_hi[i] ? rb1 : rb0, (lds_ptr)(dst + TILE_BYTES), 16,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds((PAIRED && i * (NT / CPR) >= 128) ? rb1 : rb0,
+                                               (lds_ptr)(dst + TILE_BYTES), 16,
                                                b_vo[i] + koff, 0, 0, 0);
     }
   };
