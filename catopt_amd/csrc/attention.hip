@@ -450,7 +450,8 @@ extern "C" int32_t catopt_hip_attn_fwd(int32_t dtype, int64_t B, int64_t H, int6
   if (d != dv || (d != 128 && d != 64)) return CATOPT_E_UNSUPPORTED;
   if (!(scale > 0.f) || !__builtin_isfinite(scale)) return CATOPT_E_UNSUPPORTED;
   if (B == 0 || H == 0 || Tq == 0) return CATOPT_OK;
-  if (!q || !k || !v || !o) return CATOPT_E_INVAL;
+  // no keys: k and v may be empty (null) buffers; every row is the empty carrier
+  if (!q || !o || (Tk > 0 && (!k || !v))) return CATOPT_E_INVAL;
   if (!strides_ok(q_strides) || !strides_ok(k_strides) || !strides_ok(v_strides) ||
       !strides_ok(o_strides))
     return CATOPT_E_INVAL;

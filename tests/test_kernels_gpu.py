@@ -296,3 +296,39 @@ def test_silu_kernels(dev):
     u = _rand((1000,), torch.bfloat16, 8)
     _gate(oracle.silu(_np(x)), K.silu(x.to(dev)), TOL_BF16)
     _gate(oracle.silu(_np(x)) * _np(u), K.silu_mul(x.to(dev), u.to(dev)), TOL_BF16)
+
+
+def test_empty_inputs(dev):
+    """Zero rows, steps, queries or keys at every entry point: empty outputs,
+    the initial state passed through, and the empty carrier (m = -inf, l = 0,
+    a / l = NaN) when there are no keys."""
+    t = lambda *s, dt=torch.bfloat16: torch.randn(*s, device=dev).to(dt)  # noqa: E731
+    for dt in (torch.bfloat16, torch.float32):
+        assert K.linear(t(0, 64, dt=dt), t(32, 64, dt=dt)).shape == (0, 32)
+    assert K.linear(t(0, 64), t(64, 64), epilogue=L.EPI_SILU_MUL).shape == (0, 32)
+    assert K.matmul(t(0, 8, dt=torch.float32), t(8, 16, dt=torch.float32)).shape == (0, 16)
+    assert K.rmsnorm(t(0, 256), t(256), 1e-6).shape == (0, 256)
+    assert K.silu(t(0)).shape == (0,)
+    # no queries / no steps
+    assert K.attention(t(1, 2, 0, 64), t(1, 2, 0, 64), t(1, 2, 0, 64), 0.125, causal=True).shape == (1, 2, 0, 64)
+    assert K.retention(t(1, 2, 0, 128), t(1, 2, 0, 128), t(1, 2, 0, 128),
+                       torch.tensor([0.9, 0.95], device=dev)).shape == (1, 2, 0, 128)
+    # no keys: om_apply of the empty carrier is 0 / 0
+    q = t(1, 1, 5, 64)
+    out = K.attention(q, t(1, 1, 0, 64), t(1, 1, 0, 64), 0.125)
+    assert out.shape == (1, 1, 5, 64) and torch.isnan(out.float()).all()
+    o2, m, lv = K.attention(q, t(1, 1, 0, 64), t(1, 1, 0, 64), 0.125, normalize=False, return_ml=True)
+    assert torch.isneginf(m).all() and not lv.any() and not o2.float().any()
+    # zero steps: the state passes through
+    h0 = torch.randn(10, device=dev)
+    st, hf = K.affd_scan(torch.zeros(0, 10, device=dev), torch.zeros(0, 10, device=dev), h0, [0, 0])
+    assert st.shape == (0, 10) and torch.equal(hf, h0)
+    hs = torch.randn(1, 8, 16, device=dev)
+    y, hsf = K.ssm_scan(torch.zeros(1, 0, 8, 16, device=dev), torch.zeros(1, 0, 16, device=dev),
+                        torch.zeros(1, 0, 16, device=dev), torch.zeros(1, 0, 8, device=dev), hs, [0, 0],
+                        return_state=True)
+    assert y.shape == (1, 0, 8) and torch.equal(hsf, hs)
+    assert K.decay(torch.tensor([0.9, 0.8], device=dev), 0).shape == (2, 0, 0)
+    e = torch.zeros(0, 1, device=dev)
+    mc, lc, ac = K.om_compose((e, e, torch.zeros(0, 4, device=dev)), (e, e, torch.zeros(0, 4, device=dev)))
+    assert mc.shape == (0, 1) and ac.shape == (0, 4)
