@@ -34,6 +34,8 @@
 // by more than kLazy/c; between moves p ≤ 2^kLazy, exact in fp32 and
 // bf16's exponent range, and a / l is unchanged.  The true row max is
 // tracked separately so the emitted (m, l, a) carrier is the om_elem one.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace catopt {
@@ -222,8 +224,11 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
     }
   }
 
-  for (int kvt = 0; kvt < nkv; ++kvt) {
-    const int cur = kvt & 1;
+  // one KV tile; the stage is a compile-time constant (the loop below runs
+  // the tiles in pairs), so every LDS fragment address is a loop-invariant
+  // lane offset plus an immediate
+  auto tile = [&](int kvt, auto stage_tag) {
+    constexpr int cur = decltype(stage_tag)::value;
     if (kvt + 1 < nkv) issue_tile(kvt + 1, cur ^ 1);
     const char* Ks = lds + cur * L::STAGE_BYTES;
     const char* Vs = Ks + L::TILE_BYTES;
@@ -351,6 +356,10 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
         __syncthreads();
       }
     }
+  };
+  for (int kvt = 0; kvt < nkv; kvt += 2) {
+    tile(kvt, std::integral_constant<int, 0>{});
+    if (kvt + 1 < nkv) tile(kvt + 1, std::integral_constant<int, 1>{});
   }
 
   // ---- epilogue: back to the true max, normalise, store
