@@ -38,6 +38,8 @@
 // stages: chunk i + NSTAGE - 1's loads are issued before chunk i's arithmetic,
 // which keeps several chunks of loads in flight per workgroup (one workgroup
 // per CU leaves nothing else to hide the memory latency behind).
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace catopt {
@@ -170,11 +172,13 @@ __global__ __launch_bounds__(NT, 1) void retention_scan(
   wait_vm_lgkm0<LOADS_PER_CHUNK * (NSTAGE - 2)>();
   __syncthreads();
 
-  int cur = 0;
-  for (int ci = 0; ci < nchunks; ++ci) {
+  // one chunk; its stage is a compile-time constant (the loop below runs
+  // the chunks NSTAGE at a time), so LDS addresses fold to immediates
+  auto chunk = [&](int ci, auto stage_tag) {
+    constexpr int cur = decltype(stage_tag)::value;
     {
       const int ahead = ci + NSTAGE - 1;
-      const int st = cur == 0 ? NSTAGE - 1 : cur - 1;  // the stage chunk ci - 1 used
+      constexpr int st = cur == 0 ? NSTAGE - 1 : cur - 1;  // the stage chunk ci - 1 used
       issue(min(ahead, nchunks - 1), st);
     }
     const char* Ks = lds + cur * STAGE;
@@ -299,13 +303,18 @@ __global__ __launch_bounds__(NT, 1) void retention_scan(
     // chunk ci+1's tiles have landed (earlier stores were issued before them)
     wait_vm_lgkm0<LOADS_PER_CHUNK * (NSTAGE - 2)>();
     __syncthreads();  // next chunk's tiles and S fragments in place; exchange, decayed v free
-    cur = cur + 1 == NSTAGE ? 0 : cur + 1;
     if (kb == 0) {
       // o[ci*C + qrow][sl*32 + 8 r4 + 4g .. +3]
       uint16_t* orow = o + ((int64_t)ci * CH + qrow) * HD + sl * SL + 4 * g;
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) *reinterpret_cast<u32x2*>(orow + 8 * r4) = ow[r4];
     }
+  };
+  static_assert(NSTAGE == 3, "the chunk loop below runs three stages");
+  for (int ci = 0; ci < nchunks; ci += 3) {
+    chunk(ci, std::integral_constant<int, 0>{});
+    if (ci + 1 < nchunks) chunk(ci + 1, std::integral_constant<int, 1>{});
+    if (ci + 2 < nchunks) chunk(ci + 2, std::integral_constant<int, 2>{});
   }
 }
 
