@@ -54,7 +54,7 @@ constexpr int NSL = HD / SL;
 typedef __attribute__((ext_vector_type(4))) short s16x4;
 
 // LDS layout (bytes).  Per stage: k and q tiles [64][128] bf16 whose 16-byte
-// chunks are XOR-swizzled by (row & 15), then the v slice [64][32] bf16.
+// chunks are XOR-swizzled by kq_swz(row), then the v slice [64][32] bf16.
 constexpr int KQ_BYTES = CH * HD * 2;             // 16 KB
 constexpr int V_BYTES = CH * SL * 2;              // 4 KB
 constexpr int STAGE = 2 * KQ_BYTES + V_BYTES;
@@ -76,8 +76,15 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
   __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | ((n >> 4) << 14));
 }
 
+// The 16-byte chunk index of a k / q row is XOR-ed with a bijection of the
+// row's position among 16 consecutive rows (low two bits to bits 2-3, bits
+// 2-3 to bits 0-1).  A plain row read (16 consecutive rows, one chunk) hits
+// 16 distinct chunk slots; a transposing read of k (4 consecutive keys x 4
+// adjacent chunks per 32 lanes, rows a whole bank window apart) does too,
+// where XOR-ing with (row & 15) folded those 16 pieces onto 4 slots.
+__device__ __forceinline__ int kq_swz(int row) { return ((row & 3) << 2) | ((row >> 2) & 3); }
 __device__ __forceinline__ int kq_off(int row, int chunk) {  // byte offset in a k / q tile
-  return row * (HD * 2) + ((chunk ^ (row & 15)) << 4);
+  return row * (HD * 2) + ((chunk ^ kq_swz(row)) << 4);
 }
 
 // Transposing LDS read (ds_read_b64_tr_b16).  Within each 16-lane group, when
@@ -136,7 +143,7 @@ __global__ __launch_bounds__(NT, 1) void retention_scan(
   for (int i = 0; i < 4; ++i) {
     const int s = i * NT + wave * 64 + lane;
     const int row = s >> 4, cp = s & 15;
-    kq_goff[i] = row * HD + ((cp ^ (row & 15)) << 3);
+    kq_goff[i] = row * HD + ((cp ^ kq_swz(row)) << 3);
   }
   const int v_goff = (tid >> 2) * HD + sl * SL + (tid & 3) * 8;
   const uint32_t lds_base = lds_u32(lds);
