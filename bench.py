@@ -70,6 +70,42 @@ def time_events(fn, steps: int, warmup: int) -> float:
     return t0.elapsed_time(t1) / steps
 
 
+def time_graph_replays(fn, n: int = 30, warmup: int = 5) -> dict:
+    """One call of ``fn`` recorded into a hipGraph and replayed: median and
+    interquartile range (ms) of ``n`` replays timed one by one with HIP
+    events after ``warmup`` untimed replays (the reference's timing contract,
+    timing.py:54-80: warmup >= 5, n >= 30, median / IQR)."""
+    import statistics
+
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(n):
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        g.replay()
+        t1.record()
+        t1.synchronize()
+        ts.append(t0.elapsed_time(t1))
+    q = statistics.quantiles(ts, n=4)
+    del g
+    return {"median_ms": round(statistics.median(ts), 5), "iqr_ms": round(q[2] - q[0], 5), "n": n,
+            "warmup": warmup}
+
+
 def time_graph(fn, reps: int = 50) -> float:
     """Average ms per call of ``fn`` recorded ``reps`` times into one hipGraph
     (launches back to back on the GPU, no host gap between them)."""
@@ -696,6 +732,11 @@ def measure(form: Form, dev, steps: int, warmup: int, cpu_budget: float | None) 
         },
         "wall_ms_incl_warmup": round(wall_ms, 2),
     }
+    # the step replayed from a hipGraph (median / IQR over 30 replays)
+    try:
+        rec["graph_replay"] = time_graph_replays(form.step)
+    except Exception as exc:  # a step that cannot be captured is reported, not fatal
+        rec["graph_replay"] = {"error": f"{type(exc).__name__}: {exc}"[:200]}
     if getattr(form, "stats", None) is not None:
         rec["delivery"] = {k: (v.value if hasattr(v, "value") else v) for k, v in form.stats.items()}
     if isinstance(form, C4Retention):
