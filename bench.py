@@ -4,14 +4,15 @@
                     [--cpu-budget SECONDS] [--no-cpu]
 
 One "step" is one forward of a delivered form over one batch of synthetic
-input that is already resident in HBM (BASELINE.json's five configs, seeded
-with ``torch.manual_seed(0)``).  The headline workload is config 2 (the
+input that is already resident in HBM (the five benchmark configurations
+C1-C5 at their full shapes, seeded with ``torch.manual_seed(0)``).  The
+headline workload is C2 (the
 SwiGLU MLP block with RMSNorm: rms_norm -> gate/up GEMM with the silu*mul
 epilogue -> down GEMM); its whole-step TFLOP/s is ``value``.  Every other
 config is measured the same way and reported under ``forms``, and so are
 the dense affine scan (``aff``: a batched LTI recurrence delivered as
 ``apply(<aff_compose tree>, h)``) and the deferred-affine attention over a
-scan's states (``omd``), which are not BASELINE configs.
+scan's states (``omd``), which are not among C1-C5.
 
 Per form:
   * ``ms_per_step``  — HIP events on torch's current stream (the stream the
@@ -185,7 +186,7 @@ def traffic_bytes(kernel_key: str) -> float | None:
 
 
 class Form:
-    """One BASELINE config: inputs, one delivered step, its dominant kernel."""
+    """One benchmark configuration: inputs, one delivered step, its dominant kernel."""
 
     name = ""
     workload = ""
@@ -543,7 +544,7 @@ class C5SSM(Form):
 
 
 class DenseScan(Form):
-    """The dense affine monoid (not a BASELINE config): a batched LTI
+    """The dense affine monoid (not one of C1-C5): a batched LTI
     ``LinearRecurrence`` h_t = A h_{t-1} + x_t over many independent
     sequences, delivered as ``apply(<balanced aff_compose tree>, h)`` with one
     shared map; the kernel runs each step as one fp32 MFMA product over all
@@ -595,7 +596,7 @@ class DenseScan(Form):
 
 
 class OmdScanAttention(Form):
-    """Deferred-affine attention (not a BASELINE config): softmax attention of
+    """Deferred-affine attention (not one of C1-C5): softmax attention of
     Tq queries over the T states of a diagonal scan, delivered as
     ``omd_apply(<omd_compose tree of omd_elem(q·k_iᵀ, stack(affd_a f_j),
     stack(affd_b f_j))>, h)`` over 16 key blocks of the prefix chain f_j."""

@@ -100,7 +100,7 @@ def linear(x, W, b=None):
 
 def linear_chain(x, Ws, bs):
     """The un-optimised weight chain: ``linear(…linear(x, W1, b1)…, WL, bL)``
-    (8 stacked nn.Linear)."""
+    (8 stacked nn.Linear: the C1 weight-chain workload)."""
     h = x
     for W, b in zip(Ws, bs):
         h = linear(h, W, b)
@@ -469,7 +469,7 @@ def serial_affd_scan(a, u, h0=None):
 
 
 def ssm_serial(a, bx, c, x, h0=None):
-    """The selective diagonal SSM of BASELINE config 5, serially:
+    """The selective diagonal SSM of the C5 workload, serially:
     ``h[b,t,d,n] = a[b,t,d,n]·h[b,t-1,d,n] + bx[b,t,n]·x[b,t,d]``,
     ``y[b,t,d] = Σ_n c[b,t,n]·h[b,t,d,n]`` (DiagonalSSM's step,
     models/ssm.py:121-160, with the stacked read-out of all prefix states,
