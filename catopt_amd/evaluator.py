@@ -183,11 +183,15 @@ class HipIRModule(nn.Module):
 
     @property
     def _param_map(self) -> dict:
-        return {name: getattr(self, attr) for name, attr in self._buf_names.items()}
+        # re-read per call (the reference's contract: a replaced buffer is
+        # picked up), straight from the buffer dict rather than through
+        # nn.Module.__getattr__, which costs microseconds per name
+        bufs = self._buffers
+        return {name: bufs[attr] for name, attr in self._buf_names.items()}
 
     def _pv(self, t: Any) -> torch.Tensor | None:
         if _is_param(t) and t.name in self._buf_names:
-            return getattr(self, self._buf_names[t.name])
+            return self._buffers[self._buf_names[t.name]]
         return None
 
     def _new_param(self, value: torch.Tensor) -> Param:
