@@ -142,10 +142,13 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_nt(
   // chunk past K of the tail tile reads the next row's head (in bounds) or,
   // past the operand's last element, zero; zero_k_tail clears those chunks.
   const uint16_t* Ab = A + (int64_t)m0 * lda;
+  // num_records covers this tile's rows only (at most BM rows from the
+  // first): the host check that every in-tile offset fits 31 bits then
+  // bounds it too, however large the rest of the operand is
   const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)Ab, (short)0, (int)((((int64_t)(M - 1 - m0)) * lda + K) * 2), 0x00020000);
+      (void*)Ab, (short)0, (int)(((int64_t)min(M - 1 - m0, BM - 1) * lda + K) * 2), 0x00020000);
   const uint16_t* Bb0 = B + (int64_t)n0 * ldb;
-  const int b_rec = (int)((((int64_t)(N - 1 - n0)) * ldb + K) * 2);
+  const int b_rec = (int)(((int64_t)min(N - 1 - n0, (PAIRED ? BN / 2 : BN) - 1) * ldb + K) * 2);
   const __amdgpu_buffer_rsrc_t rb0 = __builtin_amdgcn_make_buffer_rsrc((void*)Bb0, (short)0, b_rec, 0x00020000);
   const __amdgpu_buffer_rsrc_t rb1 = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(Bb0 + (PAIRED ? (int64_t)N * ldb : 0)), (short)0, b_rec, 0x00020000);

@@ -390,6 +390,25 @@ __global__ __launch_bounds__(kThreads, 2) void ssm_stream_lds(
 // Lanes that fill the GPU: 256 CUs x 8 waves x 64 lanes.
 constexpr int64_t kFillThreads = 256LL * 8 * 64;
 
+// The schedule a launch runs: the automatic choice streams when the lanes
+// fill the GPU and goes chunk-parallel otherwise.  The workspace queries use
+// the same functions, so a caller sizes exactly what the launch will read.
+bool affd_chunked(int64_t S, int64_t nc, int32_t schedule) {
+  if (schedule == CATOPT_SCAN_CHUNKED) return true;
+  return schedule == CATOPT_SCAN_AUTO && nc > 1 && S < kFillThreads;
+}
+
+int64_t ssm_threads(int64_t B, int64_t D, int64_t N) {
+  const int64_t tpd = N / 4;  // threads per channel (4 states per thread)
+  const int64_t dpw = kThreads / tpd;
+  return (D + dpw - 1) / dpw * kThreads * B;
+}
+
+bool ssm_chunked(int64_t B, int64_t D, int64_t N, int64_t nc, int32_t schedule) {
+  if (schedule == CATOPT_SCAN_CHUNKED) return true;
+  return schedule == CATOPT_SCAN_AUTO && nc > 1 && ssm_threads(B, D, N) < kFillThreads;
+}
+
 template <int N, bool APS>
 int32_t ssm_launch(int64_t B, int64_t T, int64_t D, const float* a, const float* bx,
                    const float* c, const float* x, const float* h0, const int64_t* cs,
@@ -397,9 +416,8 @@ int32_t ssm_launch(int64_t B, int64_t T, int64_t D, const float* a, const float*
                    hipStream_t s) {
   const int64_t gx = (D + SsmLayout<N>::DPW - 1) / SsmLayout<N>::DPW;
   const int64_t S = B * D * N;
-  const int64_t threads = gx * kThreads * B;
-  bool chunked = schedule == CATOPT_SCAN_CHUNKED;
-  if (schedule == CATOPT_SCAN_AUTO) chunked = nc > 1 && threads < kFillThreads;
+  static_assert(SsmLayout<N>::TPD == N / 4, "ssm_threads assumes four states per thread");
+  const bool chunked = ssm_chunked(B, D, N, nc, schedule);
   if (gx > 0x7fffffff || B > 65535 || nc > 65535) return CATOPT_E_UNSUPPORTED;
   if (!chunked && APS) {
     static bool attr_done = false;
@@ -445,30 +463,42 @@ extern "C" int64_t catopt_hip_scan_workspace_bytes(int64_t S, int64_t n_chunks) 
   return 2 * S * n_chunks * (int64_t)sizeof(float);
 }
 
-extern "C" int32_t catopt_hip_affd_scan(int64_t T, int64_t S, const float* a, int64_t lda,
-                                        const float* u, int64_t ldu, const float* h0,
-                                        const int64_t* chunk_starts, int64_t n_chunks,
-                                        int32_t schedule, float* states, float* h_final,
-                                        void* workspace, int64_t workspace_bytes, void* stream) {
-  if (T < 0 || S < 0 || n_chunks < 1 || lda < 0 || ldu < S) return CATOPT_E_INVAL;
-  if (lda != 0 && lda < S) return CATOPT_E_INVAL;
-  if (schedule < CATOPT_SCAN_AUTO || schedule > CATOPT_SCAN_CHUNKED) return CATOPT_E_INVAL;
-  if (S == 0) return CATOPT_OK;
-  if (!chunk_starts || (T > 0 && (!a || !u))) return CATOPT_E_INVAL;
+extern "C" int64_t catopt_hip_affd_scan_workspace_bytes(int64_t T, int64_t S, int64_t n_chunks,
+                                                         int32_t schedule) {
+  if (T < 0 || S < 0 || n_chunks < 1) return -1;
+  if (schedule < CATOPT_SCAN_AUTO || schedule > CATOPT_SCAN_CHUNKED) return -1;
+  return affd_chunked(S, n_chunks, schedule) ? catopt_hip_scan_workspace_bytes(S, n_chunks) : 0;
+}
+
+extern "C" int64_t catopt_hip_ssm_scan_workspace_bytes(int64_t B, int64_t T, int64_t D, int64_t N,
+                                                        int64_t n_chunks, int32_t schedule) {
+  if (B < 0 || T < 0 || D < 0 || n_chunks < 1) return -1;
+  if (schedule < CATOPT_SCAN_AUTO || schedule > CATOPT_SCAN_CHUNKED) return -1;
+  if (N != 4 && N != 8 && N != 16 && N != 32 && N != 64) return -1;
+  return ssm_chunked(B, D, N, n_chunks, schedule) ? catopt_hip_scan_workspace_bytes(B * D * N, n_chunks)
+                                                  : 0;
+}
+
+namespace catopt {
+namespace {
+
+// Argument checks and launches of catopt_hip_affd_scan, with the workspace
+// resolved by the caller: `ws_cap` is the bytes available at `ws`.
+int32_t affd_scan_body(int64_t T, int64_t S, const float* a, int64_t lda, const float* u,
+                       int64_t ldu, const float* h0, const int64_t* chunk_starts,
+                       int64_t n_chunks, int32_t schedule, float* states, float* h_final,
+                       void* ws, int64_t ws_cap, hipStream_t s) {
   if (S > 0x7fffffffLL * kThreads || n_chunks > 65535) return CATOPT_E_UNSUPPORTED;
-  hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t gx = (S + kThreads - 1) / kThreads;
-  bool chunked = schedule == CATOPT_SCAN_CHUNKED;
-  if (schedule == CATOPT_SCAN_AUTO) chunked = n_chunks > 1 && S < kFillThreads;
+  const bool chunked = affd_chunked(S, n_chunks, schedule);
   if (!chunked) {
     affd_stream<<<dim3((uint32_t)gx), dim3(kThreads), 0, s>>>(a, lda, u, ldu, h0, chunk_starts,
                                                               n_chunks, T, S, states, h_final);
     CATOPT_LAUNCH_CHECK();
     return CATOPT_OK;
   }
-  if (!workspace || workspace_bytes < catopt_hip_scan_workspace_bytes(S, n_chunks))
-    return CATOPT_E_WORKSPACE;
-  float* ws_p = static_cast<float*>(workspace);
+  if (!ws || ws_cap < catopt_hip_scan_workspace_bytes(S, n_chunks)) return CATOPT_E_WORKSPACE;
+  float* ws_p = static_cast<float*>(ws);
   float* ws_h = ws_p + n_chunks * S;
   affd_chunk_local<<<dim3((uint32_t)gx, (uint32_t)n_chunks), dim3(kThreads), 0, s>>>(
       a, lda, u, ldu, chunk_starts, T, S, ws_p, ws_h);
@@ -481,6 +511,31 @@ extern "C" int32_t catopt_hip_affd_scan(int64_t T, int64_t S, const float* a, in
     CATOPT_LAUNCH_CHECK();
   }
   return CATOPT_OK;
+}
+
+int32_t affd_scan_args_ok(int64_t T, int64_t S, const float* a, int64_t lda, const float* u,
+                          int64_t ldu, const int64_t* chunk_starts, int64_t n_chunks,
+                          int32_t schedule) {
+  if (T < 0 || S < 0 || n_chunks < 1 || lda < 0 || ldu < S) return CATOPT_E_INVAL;
+  if (lda != 0 && lda < S) return CATOPT_E_INVAL;
+  if (schedule < CATOPT_SCAN_AUTO || schedule > CATOPT_SCAN_CHUNKED) return CATOPT_E_INVAL;
+  if (S > 0 && (!chunk_starts || (T > 0 && (!a || !u)))) return CATOPT_E_INVAL;
+  return CATOPT_OK;
+}
+
+}  // namespace
+}  // namespace catopt
+
+extern "C" int32_t catopt_hip_affd_scan(int64_t T, int64_t S, const float* a, int64_t lda,
+                                        const float* u, int64_t ldu, const float* h0,
+                                        const int64_t* chunk_starts, int64_t n_chunks,
+                                        int32_t schedule, float* states, float* h_final,
+                                        void* workspace, int64_t workspace_bytes, void* stream) {
+  const int32_t st = affd_scan_args_ok(T, S, a, lda, u, ldu, chunk_starts, n_chunks, schedule);
+  if (st != CATOPT_OK) return st;
+  if (S == 0) return CATOPT_OK;
+  return affd_scan_body(T, S, a, lda, u, ldu, h0, chunk_starts, n_chunks, schedule, states, h_final,
+                        workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int32_t catopt_hip_ssm_scan(int64_t B, int64_t T, int64_t D, int64_t N,

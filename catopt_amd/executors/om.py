@@ -269,6 +269,10 @@ def build_om_plan(root: Any, eval_mod: HipIRModule) -> dict | None:
         sc = parse_score(s)
         if sc is None:
             return None
+        if not (math.isfinite(sc["scale"]) and sc["scale"] > 0):
+            # the kernel tracks the row max of q·k and scales it, which is the
+            # max of the scaled scores only for a positive scale
+            return None
         lf = {"q": sc["q"], "k": sc["k"], "v": v, "scale": sc["scale"], "mask": sc["mask"]}
         if not _classify_mask(lf, eval_mod):
             return None

@@ -324,6 +324,7 @@ class HipOmdModule(HipExecutorBase, nn.Module):
         self.eval_mod = eval_mod if eval_mod is not None else HipIRModule(ir, param_values, device=device, ops=ops)
         self._inputs = list(ir.inputs)
         self._const_cache: dict = {}
+        self._tables: dict = {}
         self.fallbacks = 0
         self._plan = build_omd_plan(self.eval_mod._root)
         self.fused_leaves = 0  # leaves run by the fused carrier kernel on the last call
@@ -362,7 +363,11 @@ class HipOmdModule(HipExecutorBase, nn.Module):
     def _prefix_maps(self, A: torch.Tensor, B: torch.Tensor) -> tuple:
         """Every prefix map ``f_t = leaf_t ∘ … ∘ leaf_0`` of the chain (fp32)."""
         T = A.shape[0]
-        table = prefix_chunk_table(T)  # lets the kernels go chunk-parallel when the lanes are few
+        # the blocked plan lets the kernels go chunk-parallel when the lanes
+        # are few; the table object (and its device copy) lives with the module
+        table = self._tables.get(T)
+        if table is None:
+            table = self._tables[T] = K.ChunkTable(prefix_chunk_table(T), T)
         if self._plan["chain_domain"] == "diag":
             if A.shape != B.shape:
                 raise ValueError("diagonal chain parts differ in shape")

@@ -257,14 +257,14 @@ def build_scan_plan(root: Any) -> dict | None:
                 return None
             return {**base, "mode": "prefix", "leaves": leaves, "dim": dim_a, "levels": 0,
                     "gather": _shared_gather(leaves), "a_shared": _a_shared(leaves),
-                    "table": prefix_chunk_table(len(leaves))}
+                    "table": K.ChunkTable(prefix_chunk_table(len(leaves)), len(leaves))}
     leaves = map_leaves(F, leaf_op, comp_op)
     if leaves is None:
         return None
     leaves = leaves[::-1]  # time order: the innermost map runs first
     return {**base, "mode": "final", "leaves": leaves, "levels": _compose_levels(F, comp_op),
             "gather": _shared_gather(leaves), "a_shared": _a_shared(leaves),
-            "table": prefix_chunk_table(len(leaves))}
+            "table": K.ChunkTable(prefix_chunk_table(len(leaves)), len(leaves))}
 
 
 def _a_shared(leaves: list) -> bool:

@@ -347,30 +347,75 @@ def decay_vec(gamma: torch.Tensor, t: int, offset: int = 0, sign: int = 1) -> to
 # ---------------------------------------------------------------------- scans
 
 
-_TABLES: dict = {}
-
-
-def _chunk_table(chunk_starts: Sequence[int] | torch.Tensor, T: int, device) -> tuple[torch.Tensor, int]:
-    """The validated int64 chunk table on ``device``.
-
-    Validated on the host every call (the kernels index with it); the
-    device copy is cached per (table, device), so a forward recorded into a
-    hipGraph after a warm-up call makes no host-to-device copy."""
+def _validate_starts(chunk_starts, T: int) -> tuple[int, ...]:
     if isinstance(chunk_starts, torch.Tensor):
         chunk_starts = chunk_starts.detach().cpu().tolist()
-    key_vals = tuple(int(c) for c in chunk_starts)
-    if len(key_vals) < 2:
+    vals = tuple(int(c) for c in chunk_starts)
+    if len(vals) < 2:
         raise ValueError("chunk table needs at least [0, T]")
-    if key_vals[0] != 0 or key_vals[-1] != T or (T > 0 and any(b <= a for a, b in zip(key_vals, key_vals[1:]))):
+    if vals[0] != 0 or vals[-1] != T or (T > 0 and any(b <= a for a, b in zip(vals, vals[1:]))):
         raise ValueError(f"chunk table must rise strictly from 0 to T={T}")
+    return vals
+
+
+class ChunkTable:
+    """A chunk table validated once, holding one int64 device copy per device.
+
+    The kernels index the steps with it, so it is checked on the host when
+    built.  The device copies live as long as this object: an executor keeps
+    its table in its plan, so a hipGraph that recorded a launch reading a
+    copy can never outlive it."""
+
+    __slots__ = ("starts", "T", "_dev")
+
+    def __init__(self, chunk_starts, T: int) -> None:
+        self.starts = _validate_starts(chunk_starts, T)
+        self.T = int(T)
+        self._dev: dict = {}
+
+    @property
+    def n_chunks(self) -> int:
+        return len(self.starts) - 1
+
+    def on(self, device) -> torch.Tensor:
+        key = str(device)
+        cs = self._dev.get(key)
+        if cs is None:
+            cs = torch.tensor(self.starts, dtype=torch.int64).to(device)
+            self._dev[key] = cs
+        return cs
+
+
+# Tables passed as plain sequences: cached per (table, device) and never
+# evicted, since a graph recorded around such a call holds the device
+# pointer.  Past the cap, a new table is uploaded per call (and a graph
+# capture of that call fails loudly on the host-to-device copy instead of
+# replaying a freed table).
+_TABLES: dict = {}
+_TABLES_CAP = 4096
+
+
+def _chunk_table(chunk_starts, T: int, device) -> tuple[torch.Tensor, int]:
+    """The validated int64 chunk table on ``device`` and its chunk count."""
+    if isinstance(chunk_starts, ChunkTable):
+        if chunk_starts.T != T:
+            raise ValueError(f"chunk table spans {chunk_starts.T} steps, the scan has {T}")
+        return chunk_starts.on(device), chunk_starts.n_chunks
+    key_vals = _validate_starts(chunk_starts, T)
     key = (key_vals, str(device))
     cs = _TABLES.get(key)
     if cs is None:
-        if len(_TABLES) > 256:
-            _TABLES.clear()
         cs = torch.tensor(key_vals, dtype=torch.int64).to(device)
-        _TABLES[key] = cs
+        if len(_TABLES) < _TABLES_CAP:
+            _TABLES[key] = cs
     return cs, len(key_vals) - 1
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor | None:
+    """Caller workspace for a launch that reads ``nbytes`` (none when 0)."""
+    if nbytes == 0:
+        return None
+    return torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=device)
 
 
 def affd_scan(a: torch.Tensor, u: torch.Tensor, h0: torch.Tensor | None,
@@ -396,8 +441,10 @@ def affd_scan(a: torch.Tensor, u: torch.Tensor, h0: torch.Tensor | None,
     cs, nc = _chunk_table(chunk_starts, T, u.device)
     out = torch.empty((T, S), dtype=torch.float32, device=u.device) if states else None
     hf = torch.empty((S,), dtype=torch.float32, device=u.device)
-    wsb = lib.catopt_hip_scan_workspace_bytes(S, nc)
-    ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=u.device)
+    wsb = lib.catopt_hip_affd_scan_workspace_bytes(T, S, nc, int(schedule))
+    if wsb < 0:
+        raise ValueError("affd scan workspace query rejected the call")
+    ws = _workspace(wsb, u.device)
     st = lib.catopt_hip_affd_scan(T, S, _ptr(a2), lda, _ptr(u2), S, _ptr(h), _ptr(cs), nc,
                                   int(schedule), _ptr(out), _ptr(hf), _ptr(ws), wsb, _stream(u))
     L.check("catopt_hip_affd_scan", st)
@@ -503,8 +550,10 @@ def ssm_scan(a: torch.Tensor, bx: torch.Tensor, c: torch.Tensor, x: torch.Tensor
     cs, nc = _chunk_table(chunk_starts, T, x.device)
     y = torch.empty((B, T, D), dtype=torch.float32, device=x.device)
     hf = torch.empty((B, D, N), dtype=torch.float32, device=x.device) if return_state else None
-    wsb = lib.catopt_hip_scan_workspace_bytes(B * D * N, nc)
-    ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=x.device)
+    wsb = lib.catopt_hip_ssm_scan_workspace_bytes(B, T, D, N, nc, int(schedule))
+    if wsb < 0:
+        raise ValueError("SSM scan workspace query rejected the call")
+    ws = _workspace(wsb, x.device)
     st = lib.catopt_hip_ssm_scan(B, T, D, N, _ptr(a), aps, _ptr(bx), _ptr(c), _ptr(x), _ptr(h0),
                                  _ptr(cs), nc, int(schedule), _ptr(y), _ptr(hf), _ptr(ws), wsb,
                                  _stream(x))

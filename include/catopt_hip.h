@@ -230,6 +230,14 @@ enum catopt_scan_schedule {
  * level loop (scan_lower.py:652-674).
  */
 int64_t catopt_hip_scan_workspace_bytes(int64_t S, int64_t n_chunks);
+/*
+ * The bytes a catopt_hip_affd_scan call with these sizes and this schedule
+ * reads from its workspace: the chunk-parallel size when that schedule runs
+ * (CATOPT_SCAN_AUTO resolved exactly as the launch resolves it), else 0.
+ * -1 for a bad size or schedule.
+ */
+int64_t catopt_hip_affd_scan_workspace_bytes(int64_t T, int64_t S, int64_t n_chunks,
+                                             int32_t schedule);
 int32_t catopt_hip_affd_scan(int64_t T, int64_t S, const float* a,
                              int64_t lda, const float* u, int64_t ldu,
                              const float* h0, const int64_t* chunk_starts,
@@ -250,6 +258,13 @@ int32_t catopt_hip_affd_scan(int64_t T, int64_t S, const float* a,
  * and schedule as for catopt_hip_affd_scan; workspace for the
  * chunk-parallel schedule: catopt_hip_scan_workspace_bytes(B*D*N, n_chunks).
  */
+/*
+ * The bytes a catopt_hip_ssm_scan call with these sizes and this schedule
+ * reads from its workspace (0 when it streams); -1 for a bad size, N or
+ * schedule.
+ */
+int64_t catopt_hip_ssm_scan_workspace_bytes(int64_t B, int64_t T, int64_t D, int64_t N,
+                                            int64_t n_chunks, int32_t schedule);
 int32_t catopt_hip_ssm_scan(int64_t B, int64_t T, int64_t D, int64_t N,
                             const float* a, int32_t a_per_state,
                             const float* bx, const float* c, const float* x,

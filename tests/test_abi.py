@@ -68,6 +68,20 @@ def test_workspace_queries(lib):
     assert lib.catopt_hip_retention_workspace_bytes(1, 1, 64, 128, 32) == -1
     assert lib.catopt_hip_scan_workspace_bytes(10, 3) == 2 * 10 * 3 * 4
     assert lib.catopt_hip_scan_workspace_bytes(-1, 3) == -1
+    # schedule-resolved queries: streaming reads no workspace; AUTO goes
+    # chunk-parallel only when the lanes do not fill the GPU (131072 lanes)
+    assert lib.catopt_hip_affd_scan_workspace_bytes(100, 10, 3, L.SCAN_STREAM) == 0
+    assert lib.catopt_hip_affd_scan_workspace_bytes(100, 10, 3, L.SCAN_CHUNKED) == 2 * 10 * 3 * 4
+    assert lib.catopt_hip_affd_scan_workspace_bytes(100, 10, 3, L.SCAN_AUTO) == 2 * 10 * 3 * 4
+    assert lib.catopt_hip_affd_scan_workspace_bytes(100, 10, 1, L.SCAN_AUTO) == 0
+    assert lib.catopt_hip_affd_scan_workspace_bytes(100, 1 << 20, 3, L.SCAN_AUTO) == 0
+    assert lib.catopt_hip_affd_scan_workspace_bytes(100, 10, 3, 7) == -1
+    # C5 (B=16, D=2048, N=16, 128 chunks) streams: no 512 MiB workspace
+    assert lib.catopt_hip_ssm_scan_workspace_bytes(16, 16384, 2048, 16, 128, L.SCAN_AUTO) == 0
+    assert lib.catopt_hip_ssm_scan_workspace_bytes(16, 16384, 2048, 16, 128, L.SCAN_CHUNKED) == \
+        2 * 16 * 2048 * 16 * 128 * 4
+    assert lib.catopt_hip_ssm_scan_workspace_bytes(1, 512, 64, 16, 23, L.SCAN_AUTO) == 2 * 64 * 16 * 23 * 4
+    assert lib.catopt_hip_ssm_scan_workspace_bytes(1, 512, 64, 12, 23, L.SCAN_AUTO) == -1
     # dense scan: chunk maps (G·d², 256-byte rounded) + offsets (P·d) + carries (P·d·k), per chunk
     up = lambda n: -(-n // 64) * 64  # noqa: E731
     assert lib.catopt_hip_aff_scan_workspace_bytes(4, 16, 2, 1, 3) == 4 * (up(3 * 256) + up(3 * 64) + up(3 * 128))

@@ -201,6 +201,21 @@ def test_om_parse_declines_a_finite_fill_and_an_untransposed_key():
     assert math.isclose(sc["scale"], 0.75)
 
 
+@pytest.mark.parametrize("c", [0.0, -2.0])
+def test_om_plan_declines_a_non_positive_scale(c):
+    # the kernel scales the row max of q·k, which is the max of the scaled
+    # scores only for a positive scale: such a leaf runs the generic module
+    q, k, v = (Var(n, TensorType((1, 2, 16, 64))) for n in "qkv")
+    s = mk("mul", mk("matmul", q, mk("transpose", k, dim0=-2, dim1=-1)), Const(c))
+    root = mk("om_apply", mk("om_elem", s, v))
+    mod = HipOMModule(IR(root, [q, k, v]), {}, ops=cpu_table())
+    assert mod._plan is None
+    qs, ks, vs = (torch.randn(1, 2, 16, 64, dtype=torch.float64) for _ in range(3))
+    out = mod(qs, ks, vs)
+    ref = torch.softmax(c * (qs @ ks.transpose(-2, -1)), -1) @ vs
+    assert oracle.verify_equiv(_np(ref), _np(out), rtol=1e-12)["passed"]
+
+
 def test_om_module_falls_back_on_host_inputs():
     ir, _ = forms.causal_attention_form(1, 2, 16, 64, mask="param")
     vals = {"mask": torch.ones(16, 16, dtype=torch.bool).tril()}
