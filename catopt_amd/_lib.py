@@ -58,6 +58,11 @@ SIGNATURES: dict[str, tuple] = {
         _i32,
         [_i64, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _i32, _p, _p, _p, _i64, _p],
     ),
+    "catopt_hip_affd_scan_noalloc_max_bytes": (_i64, []),
+    "catopt_hip_affd_scan_noalloc": (
+        _i32,
+        [_i64, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _i32, _p, _p, _p],
+    ),
     "catopt_hip_ssm_scan": (
         _i32,
         [_i64, _i64, _i64, _i64, _p, _i32, _p, _p, _p, _p, _p, _i64, _i32, _p, _p, _p, _i64, _p],

@@ -16,6 +16,8 @@
 //             This is the two-level blocked scan of the reference's
 //             all-prefix path; it trades a second read of the inputs for
 //             chunk-level parallelism when B*D*N alone cannot fill the GPU.
+#include <mutex>
+
 #include "common.hpp"
 
 namespace catopt {
@@ -483,7 +485,8 @@ namespace catopt {
 namespace {
 
 // Argument checks and launches of catopt_hip_affd_scan, with the workspace
-// resolved by the caller: `ws_cap` is the bytes available at `ws`.
+// resolved by the caller: `ws_cap` is the bytes available at `ws` (a caller
+// buffer, or the static scratch array of the no-allocation entry point).
 int32_t affd_scan_body(int64_t T, int64_t S, const float* a, int64_t lda, const float* u,
                        int64_t ldu, const float* h0, const int64_t* chunk_starts,
                        int64_t n_chunks, int32_t schedule, float* states, float* h_final,
@@ -523,6 +526,38 @@ int32_t affd_scan_args_ok(int64_t T, int64_t S, const float* a, int64_t lda, con
   return CATOPT_OK;
 }
 
+// Scratch of the no-allocation entry point: a file-scope device array that
+// each GPU holds from the library's load to the end of the process.  Its
+// name is a host-side stand-in, not a device address: host code uses only
+// the per-device address that hipGetSymbolAddress returns for it.  The
+// chunk-parallel schedule writes every word it later reads (chunk maps and
+// local states, then the carries), so nothing in it has to start at zero.
+constexpr int64_t kAffdScratchBytes = CATOPT_AFFD_SCAN_SCRATCH_BYTES;
+static __device__ __align__(256) float scratch[kAffdScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's address of `scratch`, looked up once per device with that
+// device current (the caller's current device: the stream's).
+int32_t affd_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_hip_error(e);
+  if (dev < 0 || dev >= kMaxDevices) return CATOPT_E_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return set_hip_error(e);
+    if (!p) return CATOPT_E_HIP;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return CATOPT_OK;
+}
+
 }  // namespace
 }  // namespace catopt
 
@@ -536,6 +571,27 @@ extern "C" int32_t catopt_hip_affd_scan(int64_t T, int64_t S, const float* a, in
   if (S == 0) return CATOPT_OK;
   return affd_scan_body(T, S, a, lda, u, ldu, h0, chunk_starts, n_chunks, schedule, states, h_final,
                         workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t catopt_hip_affd_scan_noalloc_max_bytes(void) { return kAffdScratchBytes; }
+
+extern "C" int32_t catopt_hip_affd_scan_noalloc(int64_t T, int64_t S, const float* a, int64_t lda,
+                                                const float* u, int64_t ldu, const float* h0,
+                                                const int64_t* chunk_starts, int64_t n_chunks,
+                                                int32_t schedule, float* states, float* h_final,
+                                                void* stream) {
+  int32_t st = affd_scan_args_ok(T, S, a, lda, u, ldu, chunk_starts, n_chunks, schedule);
+  if (st != CATOPT_OK) return st;
+  if (S == 0) return CATOPT_OK;
+  void* ws = nullptr;
+  if (affd_chunked(S, n_chunks, schedule)) {
+    // reject before touching the device: the chunked workspace must fit
+    if (catopt_hip_scan_workspace_bytes(S, n_chunks) > kAffdScratchBytes) return CATOPT_E_WORKSPACE;
+    st = affd_scratch(&ws);
+    if (st != CATOPT_OK) return st;
+  }
+  return affd_scan_body(T, S, a, lda, u, ldu, h0, chunk_starts, n_chunks, schedule, states, h_final,
+                        ws, ws ? kAffdScratchBytes : 0, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int32_t catopt_hip_ssm_scan(int64_t B, int64_t T, int64_t D, int64_t N,

@@ -246,6 +246,35 @@ int32_t catopt_hip_affd_scan(int64_t T, int64_t S, const float* a,
                              int64_t workspace_bytes, void* stream);
 
 /*
+ * catopt_hip_affd_scan without a workspace argument: the one entry point
+ * that allocates nothing and takes no caller workspace.  It has no
+ * counterpart in the reference.  It is for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops, and
+ * harnesses that forbid hipMalloc.
+ * Arguments, results and schedules are those of catopt_hip_affd_scan (the
+ * same kernels run).  The chunk-parallel schedule keeps its chunk maps and
+ * carries in a static device array of CATOPT_AFFD_SCAN_SCRATCH_BYTES
+ * (16 MiB) that every GPU the library runs on holds until the process
+ * ends; a call whose chunk-parallel workspace,
+ * catopt_hip_scan_workspace_bytes(S, n_chunks), exceeds it returns
+ * CATOPT_E_WORKSPACE before any device work.  Streaming calls use no
+ * scratch.  All calls on one GPU share that GPU's array and leave their
+ * contents in it: two calls that overlap on one GPU (streams not ordered
+ * with each other) race, and the result of both is undefined.
+ * The device address of the array is looked up once per device, on the
+ * first call with that device current.
+ */
+#define CATOPT_AFFD_SCAN_SCRATCH_BYTES (16LL * 1024 * 1024)
+int64_t catopt_hip_affd_scan_noalloc_max_bytes(void);
+int32_t catopt_hip_affd_scan_noalloc(int64_t T, int64_t S, const float* a,
+                                     int64_t lda, const float* u, int64_t ldu,
+                                     const float* h0,
+                                     const int64_t* chunk_starts,
+                                     int64_t n_chunks, int32_t schedule,
+                                     float* states, float* h_final,
+                                     void* stream);
+
+/*
  * Diagonal selective-SSM scan with the input and readout contractions
  * fused (the all-prefix stacked form gather_applyd_stack, xcarrier.py:
  * 2252-2273, read out by y_t = Σ_n c_t[n] h_t[·, n]):
