@@ -95,7 +95,9 @@ __device__ __forceinline__ uint32_t lds_u32(const void* p) {
 // with the tile being computed.  Callers wait with s_waitcnt vmcnt before
 // the barrier that publishes the loaded stage.
 __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_wave) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_wave)
+  // one wait state between the SALU write of M0 and the LDS-DMA load that
+  // reads it (a hazard the compiler cannot see inside inline asm)
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_wave)
                : "m0");
 }
 

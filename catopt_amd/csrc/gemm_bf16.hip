@@ -1,335 +1,435 @@
-// bf16 "NT" GEMM on gfx950 MFMA with fused epilogues.
+// bf16 "NT" GEMM on gfx950 MFMA with fused epilogues: a persistent
+// ping-pong kernel.
 //
-//   C[m, n] = epi( sum_k A[m, k] * B[n, k] )
+//   C[m, n] = epi( sum_k X[m, k] * W[n, k] )
 //
-// A is the activation (rows of length K, K contiguous), B the weight in
+// X is the activation (rows of length K, K contiguous), W the weight in
 // nn.Linear layout (out_features x in_features, K contiguous): both operands
-// are K-contiguous, which is the layout the 32x32x16 MFMA consumes directly
-// (each lane supplies 8 consecutive k of one row/column).
+// are K-contiguous, the layout the 16x16x32 bf16 MFMA consumes directly (each
+// lane supplies 8 consecutive k of one row).  W rows feed the MFMA's A
+// operand and X rows its B operand, so a lane's accumulators hold four
+// consecutive output columns n of one row m: the epilogue packs them into
+// one 8-byte store.
 //
-// Tiling: 256x256 block tile, BK = 64, 8 waves in a 2x4 grid (two per
-// SIMD), each wave a 128x64 sub-tile = 4x2 MFMA blocks.  Tiles reach LDS by
-// direct buffer->LDS loads (buffer_load_dwordx4 ... lds) through buffer
-// resources over the tile's rows: one precomputed 32-bit offset per load slot
-// plus the K offset, so a tile's loads cost no 64-bit address arithmetic; no
-// register staging, no LDS store instructions.  A ring of LDS stages (two of 64 KB): the loads
-// of K tile t+1 are issued before the MFMAs of tile t, one barrier per K
-// tile.  Within a tile the fragments of k-step s+1 are read before the MFMAs
-// of k-step s, and the last k-step's MFMAs are issued after the barrier,
-// behind the next tile's first reads.  (Measured on MI355X: shallower K
-// tiles with a deeper ring lose more to the extra barriers than they gain
-// in loads in flight; 128x128 wave tiles at one wave per SIMD lose to the
-// two-waves-per-SIMD layout.)  The 16-byte chunk index of each LDS row is
-// XOR-swizzled so a fragment read's 16 rows per pass hit 16 bank groups.
+// Tiling: a 256 (m) x 256 (n) output tile per workgroup of 8 waves, two per
+// SIMD.  Wave w owns m rows [128 (w / 4), +128) and n columns [64 (w % 4),
+// +64): 8 x 4 MFMA blocks of 16 x 16, 128 accumulator registers.
 //
-// Edges: rows past M (A) or N (B) load a clamped, valid row and are never
-// stored; in a K tail (K % 64 != 0, K % 8 == 0) the chunks past K read the
-// next row's head or, past the operand's end, the buffer range check's zero,
-// and are zeroed in LDS before they are read.  Every offset within a tile's
-// rows must fit in 31 bits (checked on the host).
+// Schedule.  The waves form two groups, 0-3 and 4-7, one wave of each per
+// SIMD.  Phases are separated by workgroup barriers; in each phase one group
+// computes and the other does memory work, and group 1 runs one phase behind
+// group 0, so on every SIMD one wave issues MFMAs back to back while its
+// partner reads its next fragments.  A K stage of 64 is two steps of 32:
+//   memory phase, first step:  read the wave's fragments of the step from LDS
+//     (12 x ds_read_b128) and issue the group's half of the global->LDS loads
+//     of the next stage (group 0 the X tile, group 1 the W tile);
+//   memory phase, second step:  read the fragments, wait for the wave's own
+//     loads of the next stage;
+//   compute phase:  32 MFMAs over the fragment registers, nothing else.
+// Two LDS stages of 64 KB (X then W) alternate: the next stage goes into the
+// one the previous stage used, which both groups finished reading in the
+// phases before, and it lands two phases before its first reader.
 //
-// Paired epilogues (SILU_MUL / GLU): the B tile holds 128 rows of the first
+// Persistent tiles: the grid is one workgroup per CU, and each workgroup
+// walks its tiles in rounds.  The loads run one stage ahead across tile
+// boundaries (the last stage of a tile prefetches the first of the next),
+// and a tile's epilogue is issued in the first memory phase of the next
+// tile, so the stores overlap the next tile's MFMAs instead of all
+// workgroups storing at once.
+//
+// Loads go global->LDS directly (buffer_load_dwordx4 ... lds) through buffer
+// resources over the tile's rows, issued as inline asm: the compiler then
+// places no vmcnt wait of its own in front of the fragment reads (it cannot
+// tell which stage a pending load writes), and the explicit waits are the
+// only ones.  Each load moves 8 rows x 128 bytes, whole cache lines (a
+// 64-byte row per load costs about 10% more time).  Rows past M or N read a
+// clamped, valid row and are never stored; 16-byte chunks past K read out of
+// the resource's range, which returns zeros.  Each 128-byte LDS row is
+// XOR-swizzled by (row / 2) % 8 so that the 16 rows of a fragment read hit
+// 16 distinct 16-byte bank groups.
+//
+// Paired epilogues (SILU_MUL / GLU): the W tile holds 128 rows of the first
 // projection and the 128 matching rows of the second (row n and row n + N of
-// the concatenated weight), so every wave owns both halves of its output
-// columns and the gate is applied in registers — the chunk/silu/mul of the
-// SWIGLU_FUSE form never touch HBM.
+// the concatenated weight), and each wave owns 32 columns of both, so the
+// gate is applied in registers and chunk / silu / mul never touch HBM.
 //
-// Block-to-tile mapping is XCD-aware: the hardware deals workgroups round
-// robin over 8 XCDs, so each XCD is given a contiguous range of logical tiles
-// (grouped 8 M-tiles at a time), which march through K together and share
-// that XCD's L2.
+// Tile order is XCD-aware: the hardware deals workgroups round robin over 8
+// XCDs, so in each round the 32 workgroups of one XCD take a contiguous range
+// of logical tiles (grouped 8 M-tiles at a time), which march through K
+// together and share that XCD's L2.
 #include "common.hpp"
 
 namespace catopt {
 namespace {
 
-#ifndef CATOPT_GEMM_BK
-#define CATOPT_GEMM_BK 64
-#endif
-#ifndef CATOPT_GEMM_STAGES
-#define CATOPT_GEMM_STAGES 2
-#endif
-constexpr int BM = 256, BN = 256, BK = CATOPT_GEMM_BK;
-constexpr int NSTAGE = CATOPT_GEMM_STAGES;
-#ifndef CATOPT_GEMM_NWN
-#define CATOPT_GEMM_NWN 4
-#endif
-constexpr int NWN = CATOPT_GEMM_NWN;    // waves along N (2 along M)
-constexpr int NT = 128 * NWN;           // threads per block
-constexpr int WCOLS = BN / NWN;         // output columns per wave (B rows)
-constexpr int TJ = WCOLS / 32;          // 32-wide MFMA blocks per wave along N
-constexpr int CPR = BK / 8;             // 16-byte chunks per tile row
-constexpr int RPB = 256 / (BK * 2);     // tile rows per 256 bytes (one pass of the LDS banks)
-constexpr int TILE_BYTES = BM * BK * 2;                 // one operand tile (A or B)
-constexpr int STAGE_BYTES = 2 * TILE_BYTES;             // A then B
-constexpr int LDS_BYTES = NSTAGE * STAGE_BYTES;
-constexpr int SLOTS_PER_THREAD = (BM * BK / 8) / NT;    // 16-byte slots per thread per operand
-static_assert(SLOTS_PER_THREAD >= 1 && (BM * BK / 8) % NT == 0, "tile / thread mismatch");
-static_assert(NSTAGE >= 2 && LDS_BYTES <= 160 * 1024, "LDS ring does not fit");
-static_assert(BK % 16 == 0 && RPB >= 1 && CPR * RPB == 16, "row geometry");
+constexpr int BM = 256, BN = 256, BK = 64;     // tile; K per stage (two MFMA steps of 32)
+constexpr int NT = 512;                        // 8 waves
+constexpr int ROW_BYTES = BK * 2;              // 128: one cache line per tile row per stage
+constexpr int SLOT_ROWS = 128;                 // an LDS slot: 128 rows of one stage
+constexpr int SLOT_BYTES = SLOT_ROWS * ROW_BYTES;  // 16 KB
+// LDS slots: X rows 0-127 in a ring of 3 (read by waves 0-3), X rows
+// 128-255 in a ring of 3 (waves 4-7), W rows 0-127 and 128-255 in a ring of
+// 2 stages (read by all waves).
+constexpr int X_RING = 3, W_RING = 2;
+constexpr int W_SLOT0 = 2 * X_RING;
+constexpr int N_SLOTS = 2 * X_RING + 2 * W_RING;
+constexpr int LDS_BYTES = N_SLOTS * SLOT_BYTES;   // 160 KB
+constexpr int DMA_PER_PHASE = 4;               // 1 KB loads per wave per compute phase
+constexpr int FM = 8, FN = 4;                  // 16x16 blocks per wave along m, n
+static_assert(BN == BM && LDS_BYTES <= 160 * 1024, "geometry");
+static_assert(SLOT_BYTES / 1024 == 4 * DMA_PER_PHASE, "a group's 4 waves fill one slot per phase");
 
-typedef __attribute__((address_space(3))) void* lds_ptr;
-
-// The 16-byte chunk index is XOR-swizzled by the row's position among the 16
-// consecutive rows that one 16-lane pass of a fragment read touches, so those
-// 16 rows land on 16 distinct 16-byte bank groups.
-__device__ __forceinline__ int chunk_swizzle(int row) { return (row / RPB) % CPR; }
-__device__ __forceinline__ int swz(int row, int chunk) {  // byte offset of (row, chunk) in a tile
-  return row * (BK * 2) + ((chunk ^ chunk_swizzle(row)) << 4);
+// Byte offset of (row, 16-byte chunk) in a slot.
+__device__ __forceinline__ constexpr int swz(int row, int chunk) {
+  return row * ROW_BYTES + ((chunk ^ ((row >> 1) & 7)) << 4);
 }
 
-// s_waitcnt: vmcnt <= n, lgkmcnt = 0, expcnt not waited on (gfx9 encoding).
+// One 1 KB global->LDS load: lane l's 16 bytes at byte `voff` of the buffer
+// land at LDS byte address lds + 16 l.  The s_nop is the one wait state the
+// hardware needs between an SALU write of M0 and an LDS-DMA load reading it
+// (the compiler cannot insert it inside inline asm; without it the load can
+// take the previous M0 and land in another load's place).
+__device__ __forceinline__ void dma(u32x4 rsrc, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :: "v"(voff), "s"(rsrc), "s"(lds) : "m0", "memory");
+}
+
+// Buffer resource (raw, stride 0) over `bytes` bytes from `base`.
+__device__ __forceinline__ u32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  u32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane((uint32_t)b);
+  r.y = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  r.z = __builtin_amdgcn_readfirstlane(bytes);
+  r.w = 0x00020000;
+  return r;
+}
+
+// s_waitcnt with lgkmcnt(0) and vmcnt <= n (gfx9 encoding; expcnt not waited on).
 template <int n>
 __device__ __forceinline__ void wait_vm_lgkm0() {
   static_assert(n >= 0 && n < 64, "vmcnt field");
   __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | ((n >> 4) << 14));
 }
-
-// s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt not waited on).
 __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (3 << 14)); }
+
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
 
 struct TileMap {
   int tm, tn;
 };
 
-__device__ __forceinline__ TileMap map_tile(int tiles_m, int tiles_n) {
-  int bid = blockIdx.x;
-  const int nb = gridDim.x;
-  if ((nb & 7) == 0) {
-    const int xcd = bid & 7, loc = bid >> 3;
-    bid = xcd * (nb >> 3) + loc;
-  }
+// Logical tile -> (M-tile, N-tile): groups of 8 M-tiles, N-tiles in order.
+__device__ __forceinline__ TileMap tile_of(int lt, int tiles_m, int tiles_n) {
   constexpr int GM = 8;
   const int per_group = GM * tiles_n;
-  const int group = bid / per_group;
+  const int group = lt / per_group;
   const int first_m = group * GM;
   const int gsize = min(tiles_m - first_m, GM);
-  const int in_group = bid - group * per_group;
+  const int in_group = lt - group * per_group;
   TileMap t;
   t.tm = first_m + in_group % gsize;
   t.tn = in_group / gsize;
   return t;
 }
 
+// The kernel's operands, shared by its helpers.
+struct GemmArgs {
+  const uint16_t* X;
+  const uint16_t* W;
+  int64_t lda, ldb;
+  int M, N, K, tiles_m, tiles_n, nblocks, kst, G, slot;
+};
+
+// One load stream of a wave: the 128 rows of one matrix half that the wave's
+// group loads, stage after stage, tile after tile.  `what` is 0 for X rows
+// 128 h .. 128 h + 127 (h = `half`), 1 for W rows of half h (paired: h = 0 the
+// gate rows, h = 1 the up rows).  Wave wq loads 1 KB blocks q = 4 wq + i
+// (i < 4) of the 16 in a slot; block q covers slot rows 8 q .. 8 q + 7, lane
+// l holds row 8 q + l / 8 and stored chunk l % 8, i.e. global chunk
+// (l % 8) ^ ((q % 2) * 4 + l / 16).  Past the last tile the stream repeats
+// its last stage (into a slot nobody reads again), so every wave issues the
+// same loads every phase and the vmcnt bounds below stay exact.
+template <bool PAIRED>
+struct Stream {
+  u32x4 rsrc;
+  uint32_t voff[DMA_PER_PHASE];
+  int what, half;  // 0: X rows 128 half.., 1: W rows of `half`
+  int round, T;    // the stage this stream loads next
+  bool live;       // a tile exists for `round`
+
+  __device__ __forceinline__ void setup(const GemmArgs& g, int wq, int lane, const int* lchunk8) {
+    const int lt = round * g.G + g.slot;
+    live = lt < g.nblocks;
+    if (!live) return;  // keep the last tile's resource and offsets
+    const TileMap t = tile_of(lt, g.tiles_m, g.tiles_n);
+    int64_t ld;
+    int row0, row_lim;  // first tile row of the half; last valid tile row
+    const uint16_t* base;
+    if (what == 0) {
+      const int m0 = t.tm * BM;
+      base = g.X + (int64_t)m0 * g.lda;
+      ld = g.lda;
+      row0 = half * SLOT_ROWS;
+      row_lim = min(g.M - 1 - m0, BM - 1);
+    } else {
+      const int n0 = t.tn * (PAIRED ? BN / 2 : BN);
+      ld = g.ldb;
+      if (PAIRED) {  // gate rows n0.. or up rows N + n0..
+        base = g.W + ((int64_t)n0 + (half ? (int64_t)g.N : 0)) * g.ldb;
+        row0 = 0;
+        row_lim = min(g.N - 1 - n0, BN / 2 - 1);
+      } else {
+        base = g.W + (int64_t)n0 * g.ldb;
+        row0 = half * SLOT_ROWS;
+        row_lim = min(g.N - 1 - n0, BN - 1);
+      }
+    }
+    rsrc = make_rsrc(base, (uint32_t)(((int64_t)row_lim * ld + g.K) * 2));
+#pragma unroll
+    for (int i = 0; i < DMA_PER_PHASE; ++i) {
+      const int r = row0 + 8 * (4 * wq + i) + (lane >> 3);
+      voff[i] = (uint32_t)(((int64_t)min(r, row_lim) * ld + lchunk8[i & 1]) * 2);
+    }
+  }
+  // the offset of load i of the current stage (zero-reading past K)
+  __device__ __forceinline__ uint32_t off(const GemmArgs& g, int i, const int* lchunk8) const {
+    const int klim = g.K - T * BK;
+    return lchunk8[i & 1] < klim ? voff[i] + (uint32_t)T * ROW_BYTES : 0x80000000u;
+  }
+  __device__ __forceinline__ void advance(const GemmArgs& g, int wq, int lane, const int* lchunk8) {
+    if (!live) return;  // repeat the last stage
+    if (++T == g.kst) {
+      T = 0;
+      ++round;
+      setup(g, wq, lane, lchunk8);
+      if (!live) T = g.kst - 1;  // nothing left: repeat the last stage of the last tile
+    }
+  }
+};
+
 template <int EPI>
 __global__ __launch_bounds__(NT, 1) void gemm_bf16_nt(
-    const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb,
+    const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restrict__ W, int64_t ldb,
     const uint16_t* __restrict__ bias, const uint16_t* __restrict__ bias2,
     uint16_t* __restrict__ C, int64_t ldc, int M, int N, int K, int tiles_m, int tiles_n,
-    int64_t sA, int64_t sB, int64_t sC) {
+    int64_t sA, int64_t sB, int64_t sC, int vec_store, int stagger) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
-  A += (int64_t)blockIdx.y * sA;
-  B += (int64_t)blockIdx.y * sB;
-  C += (int64_t)blockIdx.y * sC;
   constexpr bool PAIRED = (EPI == CATOPT_EPI_SILU_MUL || EPI == CATOPT_EPI_GLU);
-  const TileMap tile = map_tile(tiles_m, tiles_n);
-  const int m0 = tile.tm * BM;
-  // n0: first output column of this tile; B rows for the tile start at n0
-  // (and at N + n0 for the second projection of a paired epilogue).
-  const int n0 = tile.tn * (PAIRED ? BN / 2 : BN);
+  constexpr int WROWS = PAIRED ? BN / 2 : BN;  // weight rows per projection in a tile
+  GemmArgs ga;
+  ga.X = X + (int64_t)blockIdx.y * sA;
+  ga.W = W + (int64_t)blockIdx.y * sB;
+  C += (int64_t)blockIdx.y * sC;
+  ga.lda = lda;
+  ga.ldb = ldb;
+  ga.M = M;
+  ga.N = N;
+  ga.K = K;
+  ga.tiles_m = tiles_m;
+  ga.tiles_n = tiles_n;
+  ga.nblocks = tiles_m * tiles_n;
+  ga.kst = (K + BK - 1) / BK;
+  // This workgroup's slot in a round: the workgroups of one XCD (ids
+  // congruent mod 8) take consecutive logical tiles.
+  ga.G = gridDim.x;
+  ga.slot = (ga.G & 7) == 0 ? (blockIdx.x & 7) * (ga.G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+  const int kst = ga.kst;
+  if (ga.slot >= ga.nblocks) return;  // uniform over the workgroup
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / NWN, wn = wave % NWN;
-  const int l32 = lane & 31, g = lane >> 5;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2, wq = wave & 3;
+  const uint32_t lds0 = lds_u32(lds);
+  const int lchunk8[2] = {((lane & 7) ^ (lane >> 4)) * 8, ((lane & 7) ^ (4 | (lane >> 4))) * 8};
 
-  // This thread's load slots: slot s = i*NT + wave*64 + lane of a tile is
-  // (row s/8, swizzled chunk s%8); the global row is clamped to a valid one.
-  // Buffer resources over this tile's rows: 32-bit offsets from the tile's
-  // first row (rows past M / N clamp to the last valid one); a paired tile
-  // reads its up rows through a second resource N rows further on.  The K
-  // offset rides in the per-lane offset, which the range check covers: a
-  // chunk past K of the tail tile reads the next row's head (in bounds) or,
-  // past the operand's last element, zero; zero_k_tail clears those chunks.
-  const uint16_t* Ab = A + (int64_t)m0 * lda;
-  // num_records covers this tile's rows only (at most BM rows from the
-  // first): the host check that every in-tile offset fits 31 bits then
-  // bounds it too, however large the rest of the operand is
-  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)Ab, (short)0, (int)(((int64_t)min(M - 1 - m0, BM - 1) * lda + K) * 2), 0x00020000);
-  const uint16_t* Bb0 = B + (int64_t)n0 * ldb;
-  const int b_rec = (int)(((int64_t)min(N - 1 - n0, (PAIRED ? BN / 2 : BN) - 1) * ldb + K) * 2);
-  const __amdgpu_buffer_rsrc_t rb0 = __builtin_amdgcn_make_buffer_rsrc((void*)Bb0, (short)0, b_rec, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rb1 = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(Bb0 + (PAIRED ? (int64_t)N * ldb : 0)), (short)0, b_rec, 0x00020000);
-  uint32_t a_vo[SLOTS_PER_THREAD], b_vo[SLOTS_PER_THREAD];
-  // slot i covers tile rows [i * NT / CPR, (i + 1) * NT / CPR): whether it
-  // reads up rows is known at compile time, so the resource stays uniform
-  static_assert(128 % (NT / CPR) == 0, "a load slot straddles the gate / up halves");
+  // ---- load streams.  Stage T of a tile (global stage s) is read in phases
+  // 4s + 1 .. 4s + 4: group 0 in 4s + 1, 4s + 3 (its steps 2s, 2s + 1),
+  // group 1 in 4s + 2, 4s + 4; group 0 computes in 4s + 2, 4s + 4 and group
+  // 1 in 4s + 3, 4s + 5.  Each memory phase issues 4 loads per wave, 16 per
+  // CU, among its fragment reads, so the loads are spread evenly over the
+  // phases and the compute phases are MFMAs only:
+  //   group 0, memory of step 2s     (4s + 1): W rows 0-127 of stage s + 1
+  //   group 1, memory of step 2s     (4s + 2): W rows 128-255 of stage s + 1
+  //   group 0, memory of step 2s + 1 (4s + 3): X rows 128-255 of stage s + 2
+  //   group 1, memory of step 2s + 1 (4s + 4): X rows 0-127 of stage s + 2
+  // W stage s + 1 goes into the W slots stage s - 1 used (last read in phase
+  // 4s); X stage s + 2 into the X slots of stage s - 1 (last read in 4s - 1
+  // or 4s).  At the end of its second memory phase of a stage each wave
+  // waits for all its loads but the 4 it just issued: group 0's W half of
+  // stage s + 1 (needed in 4s + 5) and X rows of stage s + 1 (4s + 6), group
+  // 1's W half of stage s + 1 and X rows of stage s + 1 (both 4s + 5).  Every
+  // wait for loads is followed by a barrier before the data is read: an
+  // LDS-DMA write can become visible a little after vmcnt counts it done,
+  // and a read straight after the wait (no barrier between) has seen stale
+  // rows on MI355X.
+  // st[0]: this wave's W stream (group 0 rows 0-127, group 1 rows 128-255);
+  // st[1]: its X stream (group 0 X rows 128-255, group 1 X rows 0-127).
+  Stream<PAIRED> st[2];
+  st[0].what = 1;
+  st[0].half = grp;
+  st[1].what = 0;
+  st[1].half = 1 - grp;
 #pragma unroll
-  for (int i = 0; i < SLOTS_PER_THREAD; ++i) {
-    const int s = i * NT + wave * 64 + lane;
-    const int r = s / CPR, cp = s % CPR;
-    const int chunk = cp ^ chunk_swizzle(r);
-    const int am = min(r, M - 1 - m0);
-    const int bn = PAIRED ? min(r & 127, N - 1 - n0) : min(r, N - 1 - n0);
-    a_vo[i] = (uint32_t)(((int64_t)am * lda + chunk * 8) * 2);
-    b_vo[i] = (uint32_t)(((int64_t)bn * ldb + chunk * 8) * 2);
+  for (int h = 0; h < 2; ++h) {
+    st[h].round = 0;
+    st[h].T = 0;
+    st[h].setup(ga, wq, lane, lchunk8);
   }
+  auto w_slot = [&](int stage_mod, int half) { return lds0 + (W_SLOT0 + 2 * stage_mod + half) * SLOT_BYTES; };
+  auto x_slot = [&](int stage_mod, int g) { return lds0 + (X_RING * g + stage_mod) * SLOT_BYTES; };
+  const uint32_t blk = 4 * wq * 1024;  // this wave's first 1 KB block in a slot
 
-  const int ktiles = (K + BK - 1) / BK;
-  const bool k_tail = (K % BK) != 0;
-
-  auto issue = [&](int kt, int stage) {
-    const uint32_t koff = (uint32_t)kt * (BK * 2);
-    char* sa = lds + stage * STAGE_BYTES;
+  // ---- fragments: lane l reads row (l % 16), chunk 4 h + (l / 16) of a
+  // 16-row block for step h of a stage
+  const int frag[2] = {swz(lane & 15, lane >> 4), swz(lane & 15, 4 + (lane >> 4))};
+  // W row of the wave's n-block i (paired: blocks 0-1 gate, 2-3 up)
+  auto wrow = [&](int i) { return PAIRED ? (i >> 1) * 128 + wq * 32 + (i & 1) * 16 : wq * 64 + i * 16; };
+  bf16x8 xf[FM], wf[FN];
+  // the step's 12 fragment reads with the phase's 4 loads of stream `ls`
+  // into the slot at `dst` among them (one after every 3 reads)
+  auto mem_phase = [&](int xmod, int wmod, int h, Stream<PAIRED>& ls, uint32_t dst) {
+    const char* xs = lds + (X_RING * grp + xmod) * SLOT_BYTES;
+    const char* ws = lds + (W_SLOT0 + 2 * wmod) * SLOT_BYTES;
 #pragma unroll
-    for (int i = 0; i < SLOTS_PER_THREAD; ++i) {
-      char* dst = sa + (i * NT + wave * 64) * 16;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr)dst, 16, a_vo[i] + koff, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds((PAIRED && i * (NT / CPR) >= 128) ? rb1 : rb0,
-                                               (lds_ptr)(dst + TILE_BYTES), 16,
-                                               b_vo[i] + koff, 0, 0, 0);
+    for (int i = 0; i < FN; ++i) {
+      wf[i] = *reinterpret_cast<const bf16x8*>(ws + wrow(i) * ROW_BYTES + frag[h]);
+      xf[2 * i] = *reinterpret_cast<const bf16x8*>(xs + 32 * i * ROW_BYTES + frag[h]);
+      xf[2 * i + 1] = *reinterpret_cast<const bf16x8*>(xs + (32 * i + 16) * ROW_BYTES + frag[h]);
+      dma(ls.rsrc, ls.off(ga, i, lchunk8), dst + blk + i * 1024);
+    }
+    ls.advance(ga, wq, lane, lchunk8);
+  };
+
+  f32x4 acc[FN][FM];
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  auto compute = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j) acc[i][j] = mfma16(wf[i], xf[j], acc[i][j]);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // ---- epilogue of the tile at (m0, n0): acc[i][j][r] is C[m][n] with
+  // m = m0 + 128 grp + 16 j + l % 16, n = (first column of block i) + 4 (l / 16) + r
+  auto epilogue = [&](int m0, int n0) {
+    const int mrow = m0 + 128 * grp + (lane & 15);
+    const int nq = 4 * (lane >> 4);
+    constexpr int NBLK = PAIRED ? FN / 2 : FN;
+#pragma unroll
+    for (int i = 0; i < NBLK; ++i) {
+      const int n = PAIRED ? n0 + wq * 32 + i * 16 + nq : n0 + wq * 64 + i * 16 + nq;
+      if (n >= N) continue;
+      const bool full = vec_store && n + 3 < N;
+      float badd[4] = {0.f, 0.f, 0.f, 0.f}, badd2[4] = {0.f, 0.f, 0.f, 0.f};
+      if (EPI == CATOPT_EPI_BIAS || EPI == CATOPT_EPI_BIAS_ADD2) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) badd[r] = n + r < N ? bf16_to_f32(bias[n + r]) : 0.f;
+      }
+      if (EPI == CATOPT_EPI_BIAS_ADD2) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) badd2[r] = n + r < N ? bf16_to_f32(bias2[n + r]) : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        const int m = mrow + 16 * j;
+        if (m >= M) continue;
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float a = acc[i][j][r];
+          if (PAIRED) {
+            const float b = acc[i + 2][j][r];
+            o[r] = (EPI == CATOPT_EPI_SILU_MUL) ? silu_f(a) * b : a * sigmoid_f(b);
+          } else if (EPI == CATOPT_EPI_BIAS_ADD2) {
+            o[r] = (a + badd[r]) + badd2[r];  // (x·wᵀ + bias) + bias2, in that order
+          } else {
+            o[r] = a + badd[r];
+          }
+        }
+        uint16_t* dst = C + (int64_t)m * ldc + n;
+        if (full) {
+          const u32x2 pk = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+          *reinterpret_cast<u32x2*>(dst) = pk;
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n + r < N) dst[r] = f32_to_bf16(o[r]);
+        }
+      }
     }
   };
-  // zero the chunks past K of the tail tile (after its loads landed)
-  auto zero_k_tail = [&](int kt, int stage) {
-    const int k0 = kt * BK;
-    char* sa = lds + stage * STAGE_BYTES;
-    for (int s = tid; s < 2 * BM * CPR; s += NT) {
-      const int t = s / (BM * CPR), rem = s % (BM * CPR);  // operand, slot
-      const int r = rem / CPR, cp = rem % CPR;
-      const int chunk = cp ^ chunk_swizzle(r);
-      if (k0 + chunk * 8 >= K) *reinterpret_cast<u32x4*>(sa + t * TILE_BYTES + rem * 16) = u32x4{0, 0, 0, 0};
-    }
-  };
 
-  f32x16 acc[4][TJ];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < TJ; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  // ---- stagger: the workgroups of XCD x start x * `stagger` short sleeps
+  // (about 0.5 us each) late, so the XCDs finish their tiles, and store
+  // them, at different times instead of all at once
+  if ((ga.G & 7) == 0)
+    for (int i = (blockIdx.x & 7) * stagger; i > 0; --i) __builtin_amdgcn_s_sleep(16);
 
-  // B-tile row of the wave's column block j (paired: the first TJ/2 blocks
-  // are gate rows, the rest the matching up rows 128 further down).
-  auto brow = [&](int j) {
-    return PAIRED ? (j / (TJ / 2)) * 128 + wn * (WCOLS / 2) + (j % (TJ / 2)) * 32 : wn * WCOLS + j * 32;
-  };
-
-  // Prologue: tiles 0 .. NSTAGE-2 in flight.  Every thread issues the same
-  // number of loads per tile slot (slots past the last tile reload it into a
-  // stage nobody reads), so "all but the newest NSTAGE-2 tiles landed" is
-  // one fixed vmcnt.
-  constexpr int LOADS_PER_TILE = 2 * SLOTS_PER_THREAD;
-#pragma unroll
-  for (int p = 0; p < NSTAGE - 1; ++p) issue(min(p, ktiles - 1), p);
-  wait_vm_lgkm0<LOADS_PER_TILE * (NSTAGE - 2)>();
+  // ---- prologue: stage 0 (each wave its W and X rows) and X of stage 1
+  for (int i = 0; i < DMA_PER_PHASE; ++i) dma(st[0].rsrc, st[0].off(ga, i, lchunk8), w_slot(0, grp) + blk + i * 1024);
+  st[0].advance(ga, wq, lane, lchunk8);
+  for (int p = 0; p < 2; ++p) {
+    for (int i = 0; i < DMA_PER_PHASE; ++i) dma(st[1].rsrc, st[1].off(ga, i, lchunk8), x_slot(p, 1 - grp) + blk + i * 1024);
+    st[1].advance(ga, wq, lane, lchunk8);
+  }
+  zero_acc();
+  wait_vm_lgkm0<0>();
   __syncthreads();
-  if (k_tail && ktiles == 1) {
-    zero_k_tail(0, 0);
-    __syncthreads();
-  }
+  if (grp == 1) __syncthreads();  // group 1 runs one phase behind
 
-  // Fragment registers: two sets, k-step ks of a tile uses set ks & 1.  The
-  // fragments of k-step ks+1 are read before the MFMAs of k-step ks are
-  // issued, and the last k-step's MFMAs are issued after the barrier that
-  // publishes the next tile, behind that tile's first fragment reads, so the
-  // matrix cores keep working across the barrier.
-  constexpr int KS = BK / 16;
-  static_assert(KS % 2 == 0, "the k-step register sets alternate within a tile");
-  bf16x8 af[2][4], bfr[2][TJ];
-  auto read_frags = [&](int stage, int ks, int set) {
-    const char* As = lds + stage * STAGE_BYTES;
-    const char* Bs = As + TILE_BYTES;
-    const int chunk = 2 * ks + g;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      af[set][i] = *reinterpret_cast<const bf16x8*>(As + swz(wm * 128 + i * 32 + l32, chunk));
-#pragma unroll
-    for (int j = 0; j < TJ; ++j)
-      bfr[set][j] = *reinterpret_cast<const bf16x8*>(Bs + swz(brow(j) + l32, chunk));
-  };
-  auto mfmas = [&](int set) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) acc[i][j] = mfma32x32x16(af[set][i], bfr[set][j], acc[i][j]);
-  };
-
-  read_frags(0, 0, 0);
-  int cur = 0;
-  for (int kt = 0; kt < ktiles; ++kt) {
-    // the stage tile kt-1 used receives tile kt + NSTAGE - 1 (its last reads
-    // happened before the barrier that ended iteration kt-1)
-    issue(min(kt + NSTAGE - 1, ktiles - 1), cur == 0 ? NSTAGE - 1 : cur - 1);
-    const int nxt = cur + 1 == NSTAGE ? 0 : cur + 1;
-#pragma unroll
-    for (int ks = 0; ks + 1 < KS; ++ks) {
-      // k-step ks's fragments (read one step earlier) have landed before the
-      // next step's reads go out: the MFMAs below then wait on nothing, where
-      // the compiler's own wait before them would also cover the new reads.
-      wait_lgkm0();
-      read_frags(cur, ks + 1, (ks + 1) & 1);
-      mfmas(ks & 1);
-      // LLVM's single-wave GEMM strategy spreads the reads among the MFMAs
-      // (measured +1% over issuing the reads as one batch ahead of them)
-      __builtin_amdgcn_iglp_opt(1);
-      __builtin_amdgcn_sched_barrier(0);
+  int round = 0, T = 0;      // the stage being computed (tile round, stage in tile)
+  int xmod = 0, wmod = 0;    // its X and W slot indices
+  int pm0 = -1, pn0 = -1;    // tile whose epilogue is pending
+  int lt = ga.slot;
+  TileMap tile = tile_of(lt, tiles_m, tiles_n);
+  for (;;) {
+    // ---- first step of the stage: fragments, and this wave's W rows of
+    // the next stage into the W slot of the previous one
+    __builtin_amdgcn_sched_barrier(0);
+    if (pm0 >= 0) {  // first stage of a tile: the previous tile's stores, fresh accumulators
+      epilogue(pm0, pn0);
+      zero_acc();
+      pm0 = -1;
     }
-    // the last k-step's fragments have landed on both paths below, so the
-    // MFMAs after the branch do not wait for the next tile's first reads
+    const int xnext2 = xmod == 0 ? 2 : xmod - 1;  // (stage + 2) mod 3 == (stage - 1) mod 3
+    mem_phase(xmod, wmod, 0, st[0], w_slot(wmod ^ 1, grp));
     wait_lgkm0();
-    if (kt + 1 < ktiles) {
-      // loads land in issue order: all but the newest NSTAGE-2 tiles means
-      // tile kt+1 is in place
-      wait_vm_lgkm0<LOADS_PER_TILE * (NSTAGE - 2)>();
-      __syncthreads();
-      if (k_tail && kt + 2 == ktiles) {
-        zero_k_tail(kt + 1, nxt);
-        __syncthreads();
-      }
-      read_frags(nxt, 0, 0);
-    }
+    __syncthreads();
+    compute();
+    __syncthreads();
+    // ---- second step: fragments, and this wave's X rows of stage + 2 into
+    // the X slot of stage - 1; then everything but those landed
     __builtin_amdgcn_sched_barrier(0);
-    mfmas((KS - 1) & 1);
-    __builtin_amdgcn_sched_barrier(0);
-    cur = nxt;
-  }
-  __builtin_amdgcn_s_waitcnt(0);  // drain the reloads past the last tile
-
-  // Epilogue: lane owns output column (l32) of each 32-wide block and 16 rows.
-  if (PAIRED) {
-#pragma unroll
-    for (int j = 0; j < TJ / 2; ++j) {
-      const int n = n0 + wn * (WCOLS / 2) + j * 32 + l32;
-      if (n >= N) continue;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = m0 + wm * 128 + i * 32 + acc_row(r, g);
-          if (m >= M) continue;
-          const float a = acc[i][j][r], b = acc[i][j + TJ / 2][r];
-          const float o = (EPI == CATOPT_EPI_SILU_MUL) ? silu_f(a) * b : a * sigmoid_f(b);
-          C[(int64_t)m * ldc + n] = f32_to_bf16(o);
-        }
-      }
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-      const int n = n0 + wn * WCOLS + j * 32 + l32;
-      if (n >= N) continue;
-      float badd = 0.f;
-      if (EPI == CATOPT_EPI_BIAS || EPI == CATOPT_EPI_BIAS_ADD2) badd = bf16_to_f32(bias[n]);
-      float badd2 = 0.f;
-      if (EPI == CATOPT_EPI_BIAS_ADD2) badd2 = bf16_to_f32(bias2[n]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = m0 + wm * 128 + i * 32 + acc_row(r, g);
-          if (m >= M) continue;
-          float o = acc[i][j][r];
-          if (EPI == CATOPT_EPI_BIAS || EPI == CATOPT_EPI_BIAS_ADD2) o += badd;
-          if (EPI == CATOPT_EPI_BIAS_ADD2) o += badd2;
-          C[(int64_t)m * ldc + n] = f32_to_bf16(o);
-        }
-      }
+    mem_phase(xmod, wmod, 1, st[1], x_slot(xnext2, 1 - grp));
+    wait_vm_lgkm0<DMA_PER_PHASE>();
+    __syncthreads();
+    compute();
+    __syncthreads();
+    // ---- next stage
+    xmod = xmod == X_RING - 1 ? 0 : xmod + 1;
+    wmod ^= 1;
+    if (++T == kst) {
+      T = 0;
+      pm0 = tile.tm * BM;
+      pn0 = tile.tn * WROWS;
+      lt = (++round) * ga.G + ga.slot;
+      if (lt >= ga.nblocks) break;
+      tile = tile_of(lt, tiles_m, tiles_n);
     }
   }
+  if (grp == 0) __syncthreads();  // match group 1's extra barrier
+  epilogue(pm0, pn0);
+  __builtin_amdgcn_s_waitcnt(0);  // the repeat loads past the last tile have landed
 }
 
 template <int EPI>
@@ -348,8 +448,22 @@ int32_t launch(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb,
   const int tiles_n = (N + (PAIRED ? BN / 2 : BN) - 1) / (PAIRED ? BN / 2 : BN);
   const int64_t nblocks = (int64_t)tiles_m * tiles_n;
   if (nblocks > 0x7fffffff || batch > 65535) return CATOPT_E_UNSUPPORTED;
-  gemm_bf16_nt<EPI><<<dim3((uint32_t)nblocks, (uint32_t)batch), dim3(NT), LDS_BYTES, s>>>(
-      A, lda, B, ldb, bias, bias2, C, ldc, M, N, K, tiles_m, tiles_n, sA, sB, sC);
+  // persistent: one workgroup per CU (each walks its tiles in rounds)
+  static int n_cu = 0;  // idempotent; benign race (same value written)
+  if (n_cu == 0) {
+    int dev = 0, v = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return set_hip_error(e);
+    n_cu = v > 0 ? v : 1;
+  }
+  const int64_t grid = nblocks < n_cu ? nblocks : n_cu;
+  // 8-byte stores of four columns need 8-byte aligned rows of C
+  const int vec_store = (ldc % 4 == 0) && (sC % 4 == 0) && ((reinterpret_cast<uintptr_t>(C) & 7) == 0);
+  // XCD start offsets only pay when there are several rounds of tiles
+  const int stagger = nblocks >= 2 * grid ? 4 : 0;
+  gemm_bf16_nt<EPI><<<dim3((uint32_t)grid, (uint32_t)batch), dim3(NT), LDS_BYTES, s>>>(
+      A, lda, B, ldb, bias, bias2, C, ldc, M, N, K, tiles_m, tiles_n, sA, sB, sC, vec_store, stagger);
   CATOPT_LAUNCH_CHECK();
   return CATOPT_OK;
 }
