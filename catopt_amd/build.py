@@ -51,8 +51,8 @@ HIPCC_FLAGS = [
 ]
 
 
-# hipBLASLt runs the plain (epilogue-free) bf16 GEMMs; the fused ones are ours.
-LINK_LIBS = ["-lhipblaslt"]
+# every kernel is this library's own: no vendor library is linked
+LINK_LIBS: list[str] = []
 
 SOURCE_FLAGS = {
     "retention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],

@@ -13,9 +13,6 @@
 namespace catopt {
 bool gemm_bf16_nt_fast_ok(int64_t M, int64_t N, int64_t K, const void* x, int64_t ldx,
                           const void* w, int64_t ldw, const void* y, int64_t ldy);
-// hipBLASLt path for plain bf16 GEMMs (gemm_blaslt.hip); false: not taken.
-bool blaslt_linear_bf16(int64_t M, int64_t N, int64_t K, const void* x, int64_t ldx, const void* w,
-                        int64_t ldw, void* y, int64_t ldy, hipStream_t s);
 int32_t gemm_bf16_nt_launch(int32_t epi, int64_t M, int64_t N, int64_t K, const void* x,
                             int64_t ldx, const void* w, int64_t ldw, const void* bias,
                             const void* bias2, void* y, int64_t ldy, int64_t batch,
@@ -262,12 +259,6 @@ extern "C" int32_t catopt_hip_linear(int32_t dtype, int64_t M, int64_t N, int64_
   if (epilogue == CATOPT_EPI_BIAS_ADD2 && !bias2) return CATOPT_E_INVAL;
   if (M > 0x7fffffffLL || N > 0x3fffffffLL || K > 0x7fffffffLL) return CATOPT_E_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // A plain bf16 GEMM (no epilogue) of library size goes to hipBLASLt; the
-  // fused epilogues stay on this library's kernels.
-  if (dtype == CATOPT_BF16 && epilogue == CATOPT_EPI_NONE && M * N * K >= (int64_t(1) << 30) &&
-      aligned16(x) && aligned16(w) && aligned16(y) && ldx % 8 == 0 && ldw % 8 == 0 && ldy % 8 == 0 &&
-      blaslt_linear_bf16(M, N, K, x, ldx, w, ldw, y, ldy, s))
-    return CATOPT_OK;
   if (dtype == CATOPT_BF16 && gemm_bf16_nt_fast_ok(M, N, K, x, ldx, w, ldw, y, ldy))
     return gemm_bf16_nt_launch(epilogue, M, N, K, x, ldx, w, ldw, bias, bias2, y, ldy, 1, 0, 0, 0, s);
   if (dtype == CATOPT_F32 && !paired && skinny_ok(M, N, K, x, ldx, w, ldw))

@@ -448,14 +448,19 @@ int32_t launch(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb,
   const int tiles_n = (N + (PAIRED ? BN / 2 : BN) - 1) / (PAIRED ? BN / 2 : BN);
   const int64_t nblocks = (int64_t)tiles_m * tiles_n;
   if (nblocks > 0x7fffffff || batch > 65535) return CATOPT_E_UNSUPPORTED;
-  // persistent: one workgroup per CU (each walks its tiles in rounds)
-  static int n_cu = 0;  // idempotent; benign race (same value written)
+  // persistent: one workgroup per CU (each walks its tiles in rounds); the
+  // CU count is read once per device (idempotent; a race writes the same value)
+  static int cu_count[64] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_hip_error(e);
+  int n_cu = dev >= 0 && dev < 64 ? cu_count[dev] : 0;
   if (n_cu == 0) {
-    int dev = 0, v = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e == hipSuccess) e = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev);
+    int v = 0;
+    e = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess) return set_hip_error(e);
     n_cu = v > 0 ? v : 1;
+    if (dev >= 0 && dev < 64) cu_count[dev] = n_cu;
   }
   const int64_t grid = nblocks < n_cu ? nblocks : n_cu;
   // 8-byte stores of four columns need 8-byte aligned rows of C

@@ -92,11 +92,9 @@ int32_t catopt_hip_rmsnorm(int32_t dtype, int64_t rows, int64_t cols,
  * CATOPT_EPI_SILU_MUL / CATOPT_EPI_GLU, w holds 2N rows (the concat of the
  * two projections, first half then second half).  bias / bias2 are [N]
  * vectors of `dtype` (NULL unless the epilogue reads them).  fp32
- * accumulation.  bf16 runs on 32x32x16 bf16 MFMA; fp32 on 32x32x2 fp32 MFMA.
- * A bf16 call with CATOPT_EPI_NONE and M·N·K >= 2^30 (a plain library GEMM)
- * runs hipBLASLt (first heuristic algorithm needing no workspace, cached per
- * shape), falling back to the kernel above if hipBLASLt declines;
- * CATOPT_HIP_NO_BLASLT=1 in the environment disables that route.
+ * accumulation.  bf16 with K-contiguous, 16-byte aligned operands and
+ * K % 8 == 0 runs the persistent 16x16x32 bf16 MFMA kernel (one workgroup
+ * per CU); other bf16 and all fp32 calls run 32x32x2 fp32 MFMA kernels.
  * Replaces the "linear" binding (torch_bridge.py:1251-1253), the bias adds
  * of the ASSOC_LINEAR_BIAS RHS (laws/tensor.py:1374-1394), and the
  * chunk/silu/mul (or glu) bindings of the SWIGLU_FUSE / GLU_FOLD RHS

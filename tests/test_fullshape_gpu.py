@@ -1,10 +1,11 @@
 """Parity on the production code paths: the grids and shapes the configs run.
 
 The edge-shape tests in ``test_kernels_gpu.py`` use small grids, which skip
-branches that only the full workloads take: the GEMM's XCD remap and its
-8-M-tile grouping (active when the tile count is a multiple of 8), the
-large-GEMM route, and the attention kernel's XCD remap in causal mode.  Here
-those branches run, and C2–C5 are delivered through ``HipSink`` at their full
+branches that only the full workloads take: the GEMM's XCD-aware tile order
+and its 8-M-tile grouping (active when the grid is a multiple of 8), and the
+attention kernel's XCD remap in causal mode.  Here
+those branches run, as do the persistent GEMM's multi-round tile streams
+(C2's GEMMs), and C2–C5 are delivered through ``HipSink`` at their full
 shapes, with every output element of sampled tiles compared against the
 numpy oracle in float64:
 
@@ -97,7 +98,8 @@ def test_linear_paired_grouped_grid(dev, epi):
 
 
 def test_linear_large_plain(dev):
-    # M·N·K = 2^30: the size class of the down projection's plain GEMM
+    # M·N·K = 2^30, 16 tiles: the plain (no-epilogue) GEMM of the down
+    # projection's kind on a grid whose workgroups take one tile each
     M = N = Kd = 1024
     x = _rand((M, Kd), torch.bfloat16, 47)
     w = _rand((N, Kd), torch.bfloat16, 48, 0.05)
@@ -112,6 +114,26 @@ def test_linear_k_tail_grouped_grid(dev):
     w = _rand((N, Kd), torch.bfloat16, 50, 0.05)
     y = K.linear(x.to(dev), w.to(dev))
     _gate(oracle.linear(_np(x), _np(w)), y, TOL_BF16)
+
+
+@pytest.mark.parametrize("epi", [L.EPI_NONE, L.EPI_BIAS, L.EPI_SILU_MUL])
+def test_linear_persistent_rounds_ragged(dev, epi):
+    # 17 x 33 = 561 tiles: more than two rounds of the one-workgroup-per-CU
+    # grid (the loads run ahead across tile boundaries and each tile's
+    # stores overlap the next tile), with ragged M and N edges and a K tail
+    # (K = 200: three full stages and one of 8)
+    paired = epi == L.EPI_SILU_MUL
+    M, Kd = 4160, 200
+    N = 33 * 128 - 124 if paired else 33 * 256 - 248
+    x = _rand((M, Kd), torch.bfloat16, 51)
+    w = _rand(((2 if paired else 1) * N, Kd), torch.bfloat16, 52, 0.05)
+    b = _rand((N,), torch.bfloat16, 53) if epi == L.EPI_BIAS else None
+    y = K.linear(x.to(dev), w.to(dev), None if b is None else b.to(dev), epilogue=epi)
+    if paired:
+        ref = oracle.silu(oracle.linear(_np(x), _np(w[:N]))) * oracle.linear(_np(x), _np(w[N:]))
+    else:
+        ref = oracle.linear(_np(x), _np(w), None if b is None else _np(b))
+    _gate(ref, y, TOL_BF16)
 
 
 # ------------------------------------------------------- attention grid
