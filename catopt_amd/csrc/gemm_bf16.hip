@@ -215,7 +215,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_nt(
     const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restrict__ W, int64_t ldb,
     const uint16_t* __restrict__ bias, const uint16_t* __restrict__ bias2,
     uint16_t* __restrict__ C, int64_t ldc, int M, int N, int K, int tiles_m, int tiles_n,
-    int64_t sA, int64_t sB, int64_t sC, int vec_store, int stagger) {
+    int64_t sA, int64_t sB, int64_t sC, int vec_store) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   constexpr bool PAIRED = (EPI == CATOPT_EPI_SILU_MUL || EPI == CATOPT_EPI_GLU);
   constexpr int WROWS = PAIRED ? BN / 2 : BN;  // weight rows per projection in a tile
@@ -319,61 +319,74 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_nt(
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // ---- epilogue of the tile at (m0, n0): acc[i][j][r] is C[m][n] with
-  // m = m0 + 128 grp + 16 j + l % 16, n = (first column of block i) + 4 (l / 16) + r
+  // ---- epilogue of the tile at (m0, n0).  acc[i][j][r] is C[m][n] with
+  // m = m0 + 128 grp + 16 j + l % 16 and n = (first column of block i) +
+  // 4 (l / 16) + r.  Adjacent blocks i, i+1 trade halves between lane rows
+  // (v_permlane16_swap) so each lane holds 8 consecutive columns: one
+  // 16-byte store per lane, 64 contiguous bytes per output row (8-byte stores
+  // of 32-byte row pieces cost 2-7% more kernel time).
   auto epilogue = [&](int m0, int n0) {
     const int mrow = m0 + 128 * grp + (lane & 15);
-    const int nq = 4 * (lane >> 4);
+    const int q = lane >> 4;
     constexpr int NBLK = PAIRED ? FN / 2 : FN;
 #pragma unroll
-    for (int i = 0; i < NBLK; ++i) {
-      const int n = PAIRED ? n0 + wq * 32 + i * 16 + nq : n0 + wq * 64 + i * 16 + nq;
-      if (n >= N) continue;
-      const bool full = vec_store && n + 3 < N;
-      float badd[4] = {0.f, 0.f, 0.f, 0.f}, badd2[4] = {0.f, 0.f, 0.f, 0.f};
-      if (EPI == CATOPT_EPI_BIAS || EPI == CATOPT_EPI_BIAS_ADD2) {
+    for (int i = 0; i < NBLK; i += 2) {
+      // blocks i, i+1: 4 columns per lane each -> 8 consecutive per lane
+      const int nb = PAIRED ? n0 + wq * 32 + i * 16 : n0 + wq * 64 + i * 16;
+      float bv[2][4], bv2[2][4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) badd[r] = n + r < N ? bf16_to_f32(bias[n + r]) : 0.f;
-      }
-      if (EPI == CATOPT_EPI_BIAS_ADD2) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) badd2[r] = n + r < N ? bf16_to_f32(bias2[n + r]) : 0.f;
-      }
-#pragma unroll
-      for (int j = 0; j < FM; ++j) {
-        const int m = mrow + 16 * j;
-        if (m >= M) continue;
-        float o[4];
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float a = acc[i][j][r];
-          if (PAIRED) {
-            const float b = acc[i + 2][j][r];
-            o[r] = (EPI == CATOPT_EPI_SILU_MUL) ? silu_f(a) * b : a * sigmoid_f(b);
-          } else if (EPI == CATOPT_EPI_BIAS_ADD2) {
-            o[r] = (a + badd[r]) + badd2[r];  // (x·wᵀ + bias) + bias2, in that order
-          } else {
-            o[r] = a + badd[r];
-          }
+          const int n = nb + 16 * h + 4 * q + r;
+          bv[h][r] = (EPI == CATOPT_EPI_BIAS || EPI == CATOPT_EPI_BIAS_ADD2) && n < N ? bf16_to_f32(bias[n]) : 0.f;
+          bv2[h][r] = (EPI == CATOPT_EPI_BIAS_ADD2) && n < N ? bf16_to_f32(bias2[n]) : 0.f;
         }
-        uint16_t* dst = C + (int64_t)m * ldc + n;
-        if (full) {
-          const u32x2 pk = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
-          *reinterpret_cast<u32x2*>(dst) = pk;
-        } else {
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (n + r < N) dst[r] = f32_to_bf16(o[r]);
+      for (int j = 0; j < FM; ++j) {
+        uint32_t pk[2][2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          float o[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float a = acc[i + h][j][r];
+            if (PAIRED) {
+              const float b = acc[i + h + 2][j][r];
+              o[r] = (EPI == CATOPT_EPI_SILU_MUL) ? a * __builtin_amdgcn_rcpf(1.0f + __expf(-a)) * b
+                                                  : a * __builtin_amdgcn_rcpf(1.0f + __expf(-b));
+            } else if (EPI == CATOPT_EPI_BIAS_ADD2) {
+              o[r] = (a + bv[h][r]) + bv2[h][r];
+            } else {
+              o[r] = a + bv[h][r];
+            }
+          }
+          pk[h][0] = pack_bf16x2(o[0], o[1]);
+          pk[h][1] = pack_bf16x2(o[2], o[3]);
+        }
+        // rows q = 1, 3 take block i+1 columns 0-3 / 8-11 of rows 0, 2 and
+        // give them their block i columns 4-7 / 12-15
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+          auto sw = __builtin_amdgcn_permlane16_swap(pk[0][w], pk[1][w], false, false);
+          pk[0][w] = sw[0];
+          pk[1][w] = sw[1];
+        }
+        const int m = mrow + 16 * j;
+        const int n = nb + 16 * (q & 1) + 8 * (q >> 1);
+        if (m >= M || n >= N) continue;
+        uint16_t* dst = C + (int64_t)m * ldc + n;
+        if (vec_store && (ldc % 8 == 0) && n + 7 < N) {
+          *reinterpret_cast<u32x4*>(dst) = u32x4{pk[0][0], pk[0][1], pk[1][0], pk[1][1]};
+        } else {
+          const uint32_t wv[4] = {pk[0][0], pk[0][1], pk[1][0], pk[1][1]};
+#pragma unroll
+          for (int r = 0; r < 8; ++r)
+            if (n + r < N) dst[r] = (uint16_t)(wv[r >> 1] >> (16 * (r & 1)));
         }
       }
     }
   };
-
-  // ---- stagger: the workgroups of XCD x start x * `stagger` short sleeps
-  // (about 0.5 us each) late, so the XCDs finish their tiles, and store
-  // them, at different times instead of all at once
-  if ((ga.G & 7) == 0)
-    for (int i = (blockIdx.x & 7) * stagger; i > 0; --i) __builtin_amdgcn_s_sleep(16);
 
   // ---- prologue: stage 0 (each wave its W and X rows) and X of stage 1
   for (int i = 0; i < DMA_PER_PHASE; ++i) dma(st[0].rsrc, st[0].off(ga, i, lchunk8), w_slot(0, grp) + blk + i * 1024);
@@ -465,10 +478,8 @@ int32_t launch(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb,
   const int64_t grid = nblocks < n_cu ? nblocks : n_cu;
   // 8-byte stores of four columns need 8-byte aligned rows of C
   const int vec_store = (ldc % 4 == 0) && (sC % 4 == 0) && ((reinterpret_cast<uintptr_t>(C) & 7) == 0);
-  // XCD start offsets only pay when there are several rounds of tiles
-  const int stagger = nblocks >= 2 * grid ? 4 : 0;
   gemm_bf16_nt<EPI><<<dim3((uint32_t)grid, (uint32_t)batch), dim3(NT), LDS_BYTES, s>>>(
-      A, lda, B, ldb, bias, bias2, C, ldc, M, N, K, tiles_m, tiles_n, sA, sB, sC, vec_store, stagger);
+      A, lda, B, ldb, bias, bias2, C, ldc, M, N, K, tiles_m, tiles_n, sA, sB, sC, vec_store);
   CATOPT_LAUNCH_CHECK();
   return CATOPT_OK;
 }
