@@ -18,7 +18,7 @@ ABI_VERSION = 1
 OK, E_INVAL, E_UNSUPPORTED, E_HIP, E_WORKSPACE = 0, 1, 2, 3, 4
 F32, BF16 = 0, 1
 EPI_NONE, EPI_BIAS, EPI_BIAS_ADD2, EPI_SILU_MUL, EPI_GLU = 0, 1, 2, 3, 4
-MASK_NONE, MASK_CAUSAL, MASK_BOOL = 0, 1, 2
+MASK_NONE, MASK_CAUSAL, MASK_BOOL, MASK_BIAS = 0, 1, 2, 3
 SCAN_AUTO, SCAN_STREAM, SCAN_CHUNKED = 0, 1, 2
 
 _i32, _i64, _f32, _p = C.c_int32, C.c_int64, C.c_float, C.c_void_p
@@ -43,6 +43,7 @@ SIGNATURES: dict[str, tuple] = {
         [_i32, _i64, _i64, _i64, _i64, _i64, _i64, _p, _pi64, _p, _pi64, _p, _pi64,
          _f32, _i32, _i64, _p, _i64, _i32, _p, _pi64, _p, _p, _p],
     ),
+    "catopt_hip_om_rows": (_i32, [_i32, _i64, _i64, _p, _i64, _i32, _p, _p, _p, _i64, _p]),
     "catopt_hip_om_compose": (_i32, [_i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p]),
     "catopt_hip_retention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
     "catopt_hip_retention_fwd": (
@@ -139,11 +140,23 @@ def load(path: Path | str | None = None) -> C.CDLL:
         return lib
 
 
+_calls = 0  # library entry points that returned OK in this process
+
+
 def check(fn: str, status: int) -> None:
-    """Raise :class:`HipKernelError` for a non-zero status."""
+    """Raise :class:`HipKernelError` for a non-zero status; count the call
+    otherwise (:func:`call_count`)."""
+    global _calls
     if status != OK:
         hip = _lib.catopt_hip_last_hip_error() if _lib is not None else 0
         raise HipKernelError(fn, status, hip)
+    _calls += 1
+
+
+def call_count() -> int:
+    """Number of successful launching entry-point calls so far (a host-side
+    counter; graph replays launch without calling in and are not counted)."""
+    return _calls
 
 
 def i64_array(vals) -> C.Array:

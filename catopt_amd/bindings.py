@@ -32,7 +32,7 @@ import torch.nn.functional as F
 
 from . import kernels as K
 
-__all__ = ["HIP_BINDINGS", "HipOpTable", "attr_of", "om_elem_dense"]
+__all__ = ["HIP_BINDINGS", "HipOpTable", "attr_of", "om_elem_dense", "torch_fallback_count"]
 
 
 def attr_of(kw: dict, *names: str, default: Any = None) -> Any:
@@ -74,7 +74,20 @@ def _kernel_dtype(*ts: Any) -> bool:
 
 # --------------------------------------------------------------- HIP-backed
 # Outside the kernels' dtype envelope (fp64, fp16, int) these bindings run
-# the same op as a torch device op; on a host tensor they raise.
+# the same op as a torch device op, counted by torch_fallback_count(); on a
+# host tensor they raise.
+
+_torch_fallbacks = 0
+
+
+def _fell_back() -> None:
+    global _torch_fallbacks
+    _torch_fallbacks += 1
+
+
+def torch_fallback_count() -> int:
+    """Calls of a HIP-backed binding that ran its torch device op instead."""
+    return _torch_fallbacks
 
 
 def _linear(x, w, *a, **kw):
@@ -82,6 +95,7 @@ def _linear(x, w, *a, **kw):
     _on_device(x, w, bias)
     if _kernel_dtype(x, w, bias) and x.dim() >= 1 and w.dim() == 2:
         return K.linear(x, w, bias)
+    _fell_back()
     return F.linear(x, w, bias)
 
 
@@ -89,6 +103,7 @@ def _matmul(a, b, *args, **kw):
     _on_device(a, b)
     if _kernel_dtype(a, b) and a.dim() >= 1 and b.dim() >= 1 and not (a.dim() == 1 and b.dim() == 1):
         return K.matmul(a, b)
+    _fell_back()
     return torch.matmul(a, b)
 
 
@@ -102,6 +117,7 @@ def _rms_norm(x, w=None, *a, **kw):
         nshape = (int(shape),) if shape is not None else (x.shape[-1],)
     if len(nshape) == 1 and nshape[0] == x.shape[-1] and _kernel_dtype(x, w):
         return K.rmsnorm(x, w, eps)
+    _fell_back()
     return F.rms_norm(x, nshape, weight=w, eps=eps)
 
 
@@ -109,6 +125,7 @@ def _silu(x, *a, **kw):
     _on_device(x)
     if _kernel_dtype(x):
         return K.silu(x)
+    _fell_back()
     return F.silu(x)
 
 
@@ -123,6 +140,7 @@ def _om_compose(f, g, *a, **kw):
             and m1.shape == m2.shape and a1.shape == a2.shape and l1.shape == m1.shape:
         m, lv, acc = K.om_compose(f, g)
         return m.reshape(m1.shape), lv.reshape(l1.shape), acc.reshape(a1.shape)
+    _fell_back()
     return _om_compose_torch(f, g)
 
 
@@ -140,8 +158,19 @@ def _om_compose_torch(f, g):
 
 def om_elem_dense(s, v, *a, **kw):
     """``_om_elem`` (torch_bridge.py:1974-1981) over a materialised score:
-    ``(rowmax s, Σ exp(s - m), exp(s - m) @ v)``.  The OM executor never
-    reaches this: it lowers the score pattern to the fused attention kernel."""
+    ``(rowmax s, Σ exp(s - m), exp(s - m) @ v)``, raw (a fully masked row
+    gives NaN ``l`` and ``a``).  Device fp32 / bf16 operands run the
+    ``catopt_hip_om_rows`` row kernel and the HIP GEMM in fp32; the carrier
+    comes back in the operands' promoted dtype, as the tensor formula gives
+    it."""
+    _on_device(s, v)
+    if isinstance(s, torch.Tensor) and isinstance(v, torch.Tensor) and s.dim() and v.dim() \
+            and s.numel() and v.numel() \
+            and {s.dtype, v.dtype} <= {torch.float32, torch.bfloat16} and s.device.type == "cuda":
+        dt = torch.promote_types(s.dtype, v.dtype)
+        m, lv, acc = K.om_elem_scores(s, v)
+        return m.to(dt), lv.to(dt), acc.to(dt)
+    _fell_back()
     m = s.amax(dim=-1, keepdim=True)
     e = torch.exp(s - m)
     return m, e.sum(dim=-1, keepdim=True), _matmul(e, v)
@@ -150,10 +179,17 @@ def om_elem_dense(s, v, *a, **kw):
 def _omd_elem(s, a, b, *x, **kw):
     """``_omd_elem`` (xcarrier.py:380-400): ``(m, l, e@a, e@b)``; a coefficient
     ``a`` of 3 or more axes is the dense fibre ``(…,K,d,i)`` (key axis
-    contracted through a ``(d·i)``-flattened view)."""
-    m = s.amax(dim=-1, keepdim=True)
-    e = torch.exp(s - m)
-    lv = e.sum(dim=-1, keepdim=True)
+    contracted through a ``(d·i)``-flattened view).  The row statistics of a
+    device fp32 / bf16 score come from the ``catopt_hip_om_rows`` kernel."""
+    _on_device(s, a, b)
+    if isinstance(s, torch.Tensor) and s.dim() and s.numel() and s.device.type == "cuda" \
+            and s.dtype in (torch.float32, torch.bfloat16):
+        m, lv, e = (t.to(s.dtype) for t in K.om_rows(s))
+    else:
+        _fell_back()
+        m = s.amax(dim=-1, keepdim=True)
+        e = torch.exp(s - m)
+        lv = e.sum(dim=-1, keepdim=True)
     if a.dim() >= 3:
         d, i = a.shape[-2], a.shape[-1]
         ea = _matmul(e, a.reshape(*a.shape[:-2], d * i))
@@ -194,6 +230,7 @@ def _decay(g, *a, **kw):
     _on_device(g)
     if g.dtype == torch.float32 and g.dim() <= 1 and g.device.type == "cuda":
         return K.decay(g, t)
+    _fell_back()
     pos = torch.arange(t, dtype=g.dtype, device=g.device)
     diff = pos.unsqueeze(-1) - pos.unsqueeze(-2)
     return torch.tril(g[..., None, None] ** diff.clamp_min(0))
@@ -207,6 +244,7 @@ def _decay_vec(g, *a, **kw):
     _on_device(g)
     if g.dtype == torch.float32 and g.dim() <= 1 and g.device.type == "cuda":
         return K.decay_vec(g, t, off, sign)
+    _fell_back()
     pos = torch.arange(t, dtype=g.dtype, device=g.device)
     return g[..., None] ** (pos * sign + off)
 
@@ -231,6 +269,62 @@ def _attnbias(m, *a, **kw):
     if m.dtype == torch.bool:
         return torch.where(m, torch.zeros((), device=m.device), torch.full((), float("-inf"), device=m.device))
     return m
+
+
+def _sdpa(q, k, v, *a, **kw):
+    """``scaled_dot_product_attention`` (torch_bridge.py:1225-1245: a
+    positional mask, attrs ``arg3``..``arg6`` = attn_mask, dropout_p,
+    is_causal, scale).  bf16 ``(…, T, d)`` operands with one leading shape,
+    ``d = dv`` in (64, 128), no dropout, a positive scale and at most one of
+    ``is_causal`` / a mask that is one ``(Tq, Tk)`` plane shared over the
+    leading axes run the fused attention kernel (a bool mask keeps, a float
+    one adds; ``is_causal`` keeps ``j <= i``; a fully masked row is 0, as
+    torch gives it); any other call runs torch's op."""
+    mask = a[0] if a else attr_of(kw, "attn_mask", "arg3", default=None)
+    dropout = float(attr_of(kw, "dropout_p", "arg4", default=0.0) or 0.0)
+    causal = bool(attr_of(kw, "is_causal", "arg5", default=False))
+    scale = attr_of(kw, "scale", "arg6", default=None)
+    _on_device(q, k, v, mask)
+    kw_mask = _sdpa_kernel_mask(q, k, v, mask, causal, dropout)
+    if kw_mask is not None:
+        sc = 1.0 / math.sqrt(q.shape[-1]) if scale is None else float(scale)
+        if math.isfinite(sc) and sc > 0:
+            lead = q.shape[:-2]
+            q4, k4, v4 = (t.reshape(-1, 1, *t.shape[-2:]) for t in (q, k, v))
+            o = K.attention(q4, k4, v4, sc, empty_rows="zero", **kw_mask)
+            return o.reshape(*lead, o.shape[-2], o.shape[-1])
+    _fell_back()
+    return F.scaled_dot_product_attention(q, k, v, attn_mask=mask, dropout_p=dropout, is_causal=causal,
+                                          scale=None if scale is None else float(scale))
+
+
+def _sdpa_kernel_mask(q, k, v, mask, causal, dropout) -> dict | None:
+    """Mask arguments of the attention kernel for an sdpa call, or ``None``
+    when the call is outside the kernel's envelope."""
+    ts = (q, k, v)
+    if dropout != 0.0 or not all(isinstance(t, torch.Tensor) and t.dtype == torch.bfloat16
+                                 and t.device.type == "cuda" for t in ts):
+        return None
+    if not 2 <= q.dim() <= 4 or k.shape[:-2] != q.shape[:-2] or v.shape[:-2] != q.shape[:-2]:
+        return None
+    d = q.shape[-1]
+    if d not in (64, 128) or k.shape[-1] != d or v.shape[-1] != d or v.shape[-2] != k.shape[-2]:
+        return None
+    if mask is None:
+        return {"causal": True, "causal_off": 0} if causal else {}
+    if causal or not isinstance(mask, torch.Tensor) or mask.dim() < 2:
+        return None
+    tq, tk = q.shape[-2], k.shape[-2]
+    if mask.shape[-2:] != (tq, tk):
+        return None
+    m3 = mask.reshape(-1, tq, tk)
+    if m3.shape[0] != 1 and not bool((m3 == m3[:1]).all()):
+        return None
+    if mask.dtype == torch.bool:
+        return {"mask": m3[0]}
+    if mask.dtype.is_floating_point:
+        return {"bias": m3[0]}
+    return None
 
 
 def _split_sizes(t, kw):
@@ -309,10 +403,7 @@ HIP_BINDINGS: dict[str, Callable] = {
     "mean": lambda x, *a, **kw: x.mean(*_dims(kw)),
     "amax": lambda x, *a, **kw: x.amax(*_dims(kw)),
     "softmax": lambda x, *a, **kw: F.softmax(x, dim=int(attr_of(kw, "dim", default=-1))),
-    "sdpa": lambda q, k, v, *a, **kw: F.scaled_dot_product_attention(
-        q, k, v, attn_mask=a[0] if a else kw.get("attn_mask"),
-        is_causal=bool(attr_of(kw, "is_causal", "arg5", default=False)),
-        scale=attr_of(kw, "scale", "arg6", default=None)),
+    "sdpa": _sdpa,
     "masked_fill": lambda x, m, v, *a, **kw: x.masked_fill(m, _scalar_like(v)),
     "where": lambda c, x, y, *a, **kw: torch.where(c, x, y),
     "eq": lambda x, y, *a, **kw: x == y,

@@ -94,7 +94,7 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
     const uint16_t* __restrict__ v, int64_t vsb, int64_t vsh, int64_t vst,
     uint16_t* __restrict__ o, int64_t osb, int64_t osh, int64_t ost, float* __restrict__ m_out,
     float* __restrict__ l_out, int H, int Tq, int Tk, float scale, int64_t causal_off,
-    const uint8_t* __restrict__ mask, int64_t mask_ld, int normalize) {
+    const void* __restrict__ mask, int64_t mask_ld, int normalize) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   using L = AttnLds<D>;
   // 1-D grid of nqt x H x B tiles.  Workgroups are dealt round robin over
@@ -120,6 +120,7 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
   const int q0 = qt * QT;
   const int qw0 = q0 + wave * QW;  // first query of this wave
   const float c = scale * 1.4426950408889634f;
+  const float inv_scale = 1.0f / scale;
 
   // Q fragments (MFMA B operand) for the wave's two 32-query blocks.
   bf16x8 qf[QB][D / 16];
@@ -258,7 +259,7 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
       // ---- mask (diagonal / tail / bool tiles only)
       bool need_mask = kv0 + KVB > Tk;
       if (MASK == CATOPT_MASK_CAUSAL) need_mask = need_mask || (int64_t)kv0 + KVB - 1 > (int64_t)qw0 + causal_off;
-      if (MASK == CATOPT_MASK_BOOL) need_mask = true;
+      if (MASK == CATOPT_MASK_BOOL || MASK == CATOPT_MASK_BIAS) need_mask = true;
       if (need_mask) {
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
@@ -273,13 +274,18 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
               const int key = kv0 + 32 * kb + acc_row(r, g);
               bool keep = key < Tk;
               if (MASK == CATOPT_MASK_CAUSAL) keep = keep & ((int64_t)key <= (int64_t)qrow + causal_off);
-              if (MASK == CATOPT_MASK_BOOL) {
+              float add = 0.f;
+              if (MASK == CATOPT_MASK_BOOL || MASK == CATOPT_MASK_BIAS) {
                 const int qc = qrow < Tq ? qrow : Tq - 1;
                 const int kc = key < Tk ? key : Tk - 1;
-                const bool mk = mask[(int64_t)qc * mask_ld + kc] != 0;
-                keep = keep & (qrow < Tq) & mk;
+                const int64_t mi = (int64_t)qc * mask_ld + kc;
+                if (MASK == CATOPT_MASK_BOOL) keep = keep & (static_cast<const uint8_t*>(mask)[mi] != 0);
+                // the bias is in units of the scaled score; the running
+                // scores here are q·k, scaled at the exponential
+                if (MASK == CATOPT_MASK_BIAS) add = static_cast<const float*>(mask)[mi] * inv_scale;
+                keep = keep & (qrow < Tq);
               }
-              sacc[kb][qb][r] = keep ? sacc[kb][qb][r] : -__builtin_inff();
+              sacc[kb][qb][r] = keep ? sacc[kb][qb][r] + add : -__builtin_inff();
             }
           }
         }
@@ -374,7 +380,9 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
     const float l_tot = l_sum * fix;
     if (qrow >= Tq) continue;
     const float inv = normalize ? 1.0f / l_sum : fix;
-    const bool nan_row = normalize && l_sum == 0.f;  // fully masked row: 0/0 (om_apply)
+    // fully masked row: 0/0 = NaN for om_apply (normalize 1), 0 for sdpa (2)
+    const bool empty_row = normalize && l_sum == 0.f;
+    const float fill = normalize == 2 ? 0.f : __builtin_nanf("");
     uint16_t* orow = o + (int64_t)qrow * ost;
 #pragma unroll
     for (int db = 0; db < D / 32; ++db) {
@@ -383,7 +391,7 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
         const int d = 32 * db + 8 * rg + 4 * g;
         float x0 = oacc[db][qb][4 * rg + 0] * inv, x1 = oacc[db][qb][4 * rg + 1] * inv;
         float x2 = oacc[db][qb][4 * rg + 2] * inv, x3 = oacc[db][qb][4 * rg + 3] * inv;
-        if (nan_row) x0 = x1 = x2 = x3 = __builtin_nanf("");
+        if (empty_row) x0 = x1 = x2 = x3 = fill;
         *reinterpret_cast<u32x2*>(orow + d) = u32x2{pack_bf16x2(x0, x1), pack_bf16x2(x2, x3)};
       }
     }
@@ -399,7 +407,7 @@ template <int D, int MASK>
 int32_t attn_launch(const uint16_t* q, const int64_t* qs, const uint16_t* k, const int64_t* ks,
                     const uint16_t* v, const int64_t* vs, uint16_t* o, const int64_t* os,
                     float* m_out, float* l_out, int64_t B, int64_t H, int64_t Tq, int64_t Tk,
-                    float scale, int64_t causal_off, const uint8_t* mask, int64_t mask_ld,
+                    float scale, int64_t causal_off, const void* mask, int64_t mask_ld,
                     int normalize, hipStream_t s) {
   static bool attr_done = false;
   if (!attr_done) {
@@ -423,7 +431,7 @@ int32_t attn_dispatch_mask(int32_t mode, const uint16_t* q, const int64_t* qs, c
                            const int64_t* ks, const uint16_t* v, const int64_t* vs, uint16_t* o,
                            const int64_t* os, float* m_out, float* l_out, int64_t B, int64_t H,
                            int64_t Tq, int64_t Tk, float scale, int64_t causal_off,
-                           const uint8_t* mask, int64_t mask_ld, int normalize, hipStream_t s) {
+                           const void* mask, int64_t mask_ld, int normalize, hipStream_t s) {
   switch (mode) {
     case CATOPT_MASK_NONE:
       return attn_launch<D, CATOPT_MASK_NONE>(q, qs, k, ks, v, vs, o, os, m_out, l_out, B, H, Tq, Tk, scale, causal_off, mask, mask_ld, normalize, s);
@@ -431,6 +439,8 @@ int32_t attn_dispatch_mask(int32_t mode, const uint16_t* q, const int64_t* qs, c
       return attn_launch<D, CATOPT_MASK_CAUSAL>(q, qs, k, ks, v, vs, o, os, m_out, l_out, B, H, Tq, Tk, scale, causal_off, mask, mask_ld, normalize, s);
     case CATOPT_MASK_BOOL:
       return attn_launch<D, CATOPT_MASK_BOOL>(q, qs, k, ks, v, vs, o, os, m_out, l_out, B, H, Tq, Tk, scale, causal_off, mask, mask_ld, normalize, s);
+    case CATOPT_MASK_BIAS:
+      return attn_launch<D, CATOPT_MASK_BIAS>(q, qs, k, ks, v, vs, o, os, m_out, l_out, B, H, Tq, Tk, scale, causal_off, mask, mask_ld, normalize, s);
     default:
       return CATOPT_E_INVAL;
   }
@@ -450,11 +460,12 @@ extern "C" int32_t catopt_hip_attn_fwd(int32_t dtype, int64_t B, int64_t H, int6
                                        const int64_t* q_strides, const void* k,
                                        const int64_t* k_strides, const void* v,
                                        const int64_t* v_strides, float scale, int32_t mask_mode,
-                                       int64_t causal_off, const uint8_t* mask, int64_t mask_ld,
+                                       int64_t causal_off, const void* mask, int64_t mask_ld,
                                        int32_t normalize, void* o, const int64_t* o_strides,
                                        float* m_out, float* l_out, void* stream) {
   if (B < 0 || H < 0 || Tq < 0 || Tk < 0) return CATOPT_E_INVAL;
-  if (mask_mode < CATOPT_MASK_NONE || mask_mode > CATOPT_MASK_BOOL) return CATOPT_E_INVAL;
+  if (mask_mode < CATOPT_MASK_NONE || mask_mode > CATOPT_MASK_BIAS) return CATOPT_E_INVAL;
+  if (normalize < 0 || normalize > 2) return CATOPT_E_INVAL;
   if (dtype != CATOPT_BF16) return CATOPT_E_UNSUPPORTED;
   if (d != dv || (d != 128 && d != 64)) return CATOPT_E_UNSUPPORTED;
   if (!(scale > 0.f) || !__builtin_isfinite(scale)) return CATOPT_E_UNSUPPORTED;
@@ -465,7 +476,9 @@ extern "C" int32_t catopt_hip_attn_fwd(int32_t dtype, int64_t B, int64_t H, int6
       !strides_ok(o_strides))
     return CATOPT_E_INVAL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return CATOPT_E_INVAL;
-  if (mask_mode == CATOPT_MASK_BOOL && (!mask || mask_ld < Tk)) return CATOPT_E_INVAL;
+  if ((mask_mode == CATOPT_MASK_BOOL || mask_mode == CATOPT_MASK_BIAS) && (!mask || mask_ld < Tk))
+    return CATOPT_E_INVAL;
+  if (mask_mode == CATOPT_MASK_BIAS && (reinterpret_cast<uintptr_t>(mask) & 3)) return CATOPT_E_INVAL;
   if (Tq > 0x7fffffffLL || Tk > 0x7fffffffLL || H > 65535 || B > 65535) return CATOPT_E_UNSUPPORTED;
   // per-thread tile offsets are 32-bit: 64 rows of either stride must fit
   if ((k_strides[2] + 1) * 64 + d >= 0x7fffffffLL || (v_strides[2] + 1) * 64 + d >= 0x7fffffffLL)

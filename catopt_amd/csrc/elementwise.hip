@@ -47,6 +47,11 @@ int32_t unary_launch(int32_t dtype, int64_t n, const void* x, const void* u, voi
 // m/l outputs are written by the dv == 0 thread of each row after all
 // threads of the row have read m1/m2/l1/l2 (outputs may alias input 1, so
 // each thread reads its scalars before any write of the same row).
+// max that propagates NaN, as torch.maximum / torch.amax do (fmaxf drops it)
+__device__ __forceinline__ float nan_max(float a, float b) {
+  return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b);
+}
+
 __global__ __launch_bounds__(kThreads) void om_compose_kernel(
     int64_t rows, int64_t dv, const float* m1, const float* l1, const float* a1,
     const float* m2, const float* l2, const float* a2, float* m, float* l, float* a) {
@@ -55,7 +60,7 @@ __global__ __launch_bounds__(kThreads) void om_compose_kernel(
        i += (int64_t)gridDim.x * kThreads) {
     const int64_t r = i / dv;
     const float ma = m1[r], mb = m2[r];
-    const float mx = fmaxf(ma, mb);
+    const float mx = nan_max(ma, mb);
     const bool fa = __builtin_isfinite(ma), fb = __builtin_isfinite(mb);
     const float ea = fa ? __expf(ma - mx) : 0.f;
     const float eb = fb ? __expf(mb - mx) : 0.f;
@@ -71,13 +76,55 @@ __global__ __launch_bounds__(kThreads) void om_compose_ml_kernel(
   for (int64_t r = (int64_t)blockIdx.x * kThreads + threadIdx.x; r < rows;
        r += (int64_t)gridDim.x * kThreads) {
     const float ma = m1[r], mb = m2[r];
-    const float mx = fmaxf(ma, mb);
+    const float mx = nan_max(ma, mb);
     const bool fa = __builtin_isfinite(ma), fb = __builtin_isfinite(mb);
     const float ea = fa ? __expf(ma - mx) : 0.f;
     const float eb = fb ? __expf(mb - mx) : 0.f;
     const float lv = (fa ? l1[r] * ea : 0.f) + (fb ? l2[r] * eb : 0.f);
     l[r] = lv;
     m[r] = mx;
+  }
+}
+
+// Row statistics of an explicit score block (one wave per row): a pass for
+// the NaN-propagating row max, a pass writing e = exp(s - m) and summing it.
+// The sum reduces in a fixed xor-tree order, so results are deterministic.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void om_rows_kernel(int64_t rows, int64_t cols,
+                                                           const T* __restrict__ s, int64_t lds,
+                                                           int sanitize, float* __restrict__ m,
+                                                           float* __restrict__ l,
+                                                           float* __restrict__ e, int64_t lde) {
+  const int64_t r = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;  // whole wave
+  const T* sr = s + r * lds;
+  float mx = -__builtin_inff();
+  int has_nan = 0;
+  for (int64_t c = lane; c < cols; c += 64) {
+    const float v = load_f32(sr, c);
+    has_nan |= v != v;
+    mx = fmaxf(mx, v);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    has_nan |= __shfl_xor(has_nan, o, 64);
+  }
+  if (has_nan) mx = __builtin_nanf("");
+  const bool zero = sanitize && !__builtin_isfinite(mx);
+  float* er = e + r * lde;
+  float sum = 0.f;
+  for (int64_t c = lane; c < cols; c += 64) {
+    const float x = zero ? 0.f : __expf(load_f32(sr, c) - mx);
+    er[c] = x;
+    sum += x;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  if (lane == 0) {
+    m[r] = mx;
+    l[r] = sum;
   }
 }
 
@@ -135,6 +182,27 @@ extern "C" int32_t catopt_hip_om_compose(int64_t rows, int64_t dv, const float* 
     CATOPT_LAUNCH_CHECK();
   }
   om_compose_ml_kernel<<<grid_for(rows), kThreads, 0, s>>>(rows, m1, l1, m2, l2, m, l);
+  CATOPT_LAUNCH_CHECK();
+  return CATOPT_OK;
+}
+
+extern "C" int32_t catopt_hip_om_rows(int32_t dtype, int64_t rows, int64_t cols, const void* s,
+                                      int64_t lds, int32_t sanitize, float* m, float* l, float* e,
+                                      int64_t lde, void* stream) {
+  if (rows < 0 || cols < 0 || lds < cols || lde < cols) return CATOPT_E_INVAL;
+  if (dtype != CATOPT_F32 && dtype != CATOPT_BF16) return CATOPT_E_UNSUPPORTED;
+  if (rows == 0) return CATOPT_OK;
+  if (!m || !l || (cols > 0 && (!s || !e))) return CATOPT_E_INVAL;
+  constexpr int64_t kRowsPerBlock = kThreads / 64;
+  const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  if (blocks > 0x7fffffffLL) return CATOPT_E_UNSUPPORTED;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == CATOPT_F32)
+    om_rows_kernel<float><<<dim3((uint32_t)blocks), kThreads, 0, st>>>(
+        rows, cols, static_cast<const float*>(s), lds, sanitize, m, l, e, lde);
+  else
+    om_rows_kernel<uint16_t><<<dim3((uint32_t)blocks), kThreads, 0, st>>>(
+        rows, cols, static_cast<const uint16_t*>(s), lds, sanitize, m, l, e, lde);
   CATOPT_LAUNCH_CHECK();
   return CATOPT_OK;
 }

@@ -1,36 +1,52 @@
-"""Online-softmax executor: ``om_apply(<om tree>)`` on the HIP attention kernel.
+"""Online-softmax executor: ``om_apply(<om tree>)`` on the HIP kernels.
 
 The counterpart of ``BatchedOMModule`` (luisfuturist/catopt
 ``packages/catopt-carriers/src/catopt_carriers/om_lower.py:496-835``, plan
-builder ``build_om_plan`` :334-437).  The delivered form of the ``OM_LIFT``
-law (``om.py:153-193``) is
+builder ``build_om_plan`` :334-437, score modes ``_analyze_elem_group``
+:271-331).  The tree's leaves are ``om_elem(s, v)`` blocks and packaged
+carriers ``om(m, l, a)``, combined by ``om_compose``; every om tree plans,
+as in the reference, and each leaf is classified once, at construction:
 
-    om_apply(om_elem(s, v)),   s = masked_fill(scale · q kᵀ, M, -inf)
+* ``attn`` — the score is a scaled ``q kᵀ`` with an optional mask, in the
+  spellings catopt's laws deliver:
 
-possibly split over key blocks into ``om_compose`` trees of ``om_elem``
-leaves (``om.py:1116-1400``).  The reference materialises every leaf's score
-block and reduces the tree level by level (~10 elementwise launches per
-level, ``om_lower.py:817-832``).  Here each leaf's score pattern is parsed
-once, at construction, into ``(q, k, v, scale, mask)``:
+  - the scale as ``mul``/``div`` by a constant around the product, or on
+    ``q`` as ``mul(q, fill(q, value=SC))`` (the sdpa-cat right-hand sides,
+    ``om.py:1195-1230``);
+  - one ``matmul(q, transpose(k))``, or a key-axis ``concat`` of such
+    products sharing ``q`` (``concat(q kᵢᵀ) = q · concat(kᵢ)ᵀ``);
+  - ``masked_fill(·, M, -inf)`` with ``M`` the causal generator
+    ``cmask(x, off)`` (also under ``split`` / ``slice`` along either of the
+    last two axes: the block's offset is folded into the causal bound), a
+    weight-only bool (a shifted lower triangle, compared bit-exactly, is the
+    causal mode; any other plane a keep-mask) or an input-dependent mask;
+  - ``add(·, attnbias(m))`` or ``add(·, B)`` (the attn_mask right-hand side,
+    ``om.py:1315-1340``, and its ``split`` blocks): a bool ``m`` is a
+    keep-mask, a float one an additive bias; a weight-only bias holding only
+    0 and -inf is a keep-mask.
 
-* one leaf: one launch of the fused attention kernel (scores, mask, online
-  softmax and ``a / l`` never leave the chip);
-* several leaves: one unnormalised kernel launch per leaf (emitting the
-  ``(m, l, a)`` carrier), combined pairwise in tree order with the
-  ``om_compose`` kernel, read out as ``a / l``.
+  bf16 operands with head dim 64 or 128 and a mask that is one ``(Tq, Tk)``
+  plane shared over the leading axes run one launch of the fused attention
+  kernel (scores, mask, exponentials and ``e @ v`` stay on chip; a single
+  leaf is normalised in the kernel).  Unmasked fp32 operands run the fp32
+  carrier kernel.  Any other call — another head dim, a per-batch mask —
+  takes the score path below for that leaf.
+* ``scores`` — any other score (the reference's ``slice`` / ``stack``
+  modes): the score block is evaluated, its row statistics and
+  ``exp(s - m)`` come from ``catopt_hip_om_rows`` and ``e @ v`` from the HIP
+  GEMM.
+* ``om`` — a packaged carrier, used as evaluated.
 
-The masked set ``M`` is classified at construction when it is weight-only:
-the causal generator ``cmask(x, off)`` (``om.py:1023-1029``, keep
-``j <= i - off``) and any bool Param equal to a shifted lower triangle
-(compared bit-exactly) become the kernel's implicit causal mode; any other
-bool mask is handed to the kernel as a uint8 keep-mask.  A mask that depends
-on the inputs is evaluated per call.  ``-inf`` is the only accepted fill: a
-finite fill changes what a fully masked row means.
-
-A root that does not parse leaves ``_plan = None`` and every call runs the
-embedded generic module (``om_lower.py:730-731``).  A call outside the
-kernel's envelope (dtype other than bf16, head dim other than 64/128) also
-runs the generic module and increments ``fallbacks``.
+Leaf carriers are sanitised as ``om_lower.py:792-798`` does (a row whose max
+is not finite contributes ``l = a = 0``), combined by the canonical
+adjacent-pair reduction with the ``om_compose`` kernel (the ``isfinite``
+guards of ``torch_bridge.py:1984-2006``, NaN-propagating max), and read out
+as ``a / l`` unclamped: a fully masked row is NaN, as dense softmax.  A
+DAG-shared leaf contributes once per occurrence.  A root that is not an om
+tree leaves ``_plan = None`` and every call runs the embedded generic module
+(``om_lower.py:730-731``).  A call with host inputs runs the generic
+module, and a leaf whose operands are not fp32 / bf16 runs the module's own
+``om_elem`` / ``om_compose`` bindings; both count in ``fallbacks``.
 """
 
 from __future__ import annotations
@@ -43,8 +59,8 @@ from torch import nn
 
 from .. import kernels as K
 from ..bindings import attr_of, scalar_value
-from ..evaluator import HipIRModule
-from ..ir import IR, is_op
+from ..evaluator import HipIRModule, _is_param, _is_var, eval_term
+from ..ir import IR, Op, is_op, postorder
 from .base import HipExecutorBase
 
 __all__ = ["HipOMModule", "build_om_plan", "is_om_term", "mask_kwargs", "om_leaves", "parse_score"]
@@ -52,16 +68,13 @@ __all__ = ["HipOMModule", "build_om_plan", "is_om_term", "mask_kwargs", "om_leav
 
 def is_om_term(term: Any) -> bool:
     """Term-level probe: an ``om_apply`` over an om tree."""
-    return is_op(term, "om_apply") and len(term.args) >= 1 and _om_tree_ok(term.args[0])
-
-
-def _om_tree_ok(t: Any) -> bool:
-    return om_leaves(t) is not None
+    return is_op(term, "om_apply") and len(term.args) >= 1 and om_leaves(term.args[0]) is not None
 
 
 def om_leaves(t: Any) -> list | None:
-    """Leaves of an ``om_compose`` tree, left to right; ``None`` if a leaf is
-    not an ``om_elem``."""
+    """Leaves (``om_elem`` blocks and packaged ``om`` carriers) of an
+    ``om_compose`` tree, left to right and once per occurrence; ``None`` if
+    another node appears."""
     out: list = []
     stack = [t]
     while stack:
@@ -69,7 +82,7 @@ def om_leaves(t: Any) -> list | None:
         if is_op(n, "om_compose", 2):
             stack.append(n.args[1])
             stack.append(n.args[0])
-        elif is_op(n, "om_elem", 2):
+        elif is_op(n, "om_elem", 2) or is_op(n, "om", 3):
             out.append(n)
         else:
             return None
@@ -81,17 +94,33 @@ def _is_neg_inf(t: Any) -> bool:
     return v is not None and v == float("-inf")
 
 
+def _scale_factor(t: Any) -> float | None:
+    """The multiplier a factor term stands for: a finite constant, or the
+    constant map ``fill(x, value=c)`` (``full_like(x, c)``)."""
+    c = scalar_value(t)
+    if c is not None:
+        return c if math.isfinite(c) else None
+    if is_op(t, "fill", 1):
+        try:
+            v = float(attr_of(t.attrs, "value", default=None))
+        except (TypeError, ValueError):
+            return None
+        return v if math.isfinite(v) else None
+    return None
+
+
 def _peel_scale(s: Any) -> tuple[Any, float]:
+    """``(x, c)`` with ``s = c · x`` through ``mul`` / ``div`` by constants."""
     scale = 1.0
     while True:
         if is_op(s, "mul", 2):
             a, b = s.args
-            cb, ca = scalar_value(b), scalar_value(a)
-            if cb is not None and math.isfinite(cb):
+            cb, ca = _scale_factor(b), _scale_factor(a)
+            if cb is not None:
                 scale *= cb
                 s = a
                 continue
-            if ca is not None and math.isfinite(ca):
+            if ca is not None:
                 scale *= ca
                 s = b
                 continue
@@ -102,6 +131,32 @@ def _peel_scale(s: Any) -> tuple[Any, float]:
                 s = s.args[0]
                 continue
         return s, scale
+
+
+_SAME_RANK = frozenset({"concat", "split", "slice", "chunk", "transpose", "contiguous", "fill", "cmask",
+                        "attnbias", "masked_fill", "neg", "exp", "to", "clone"})
+
+
+def _rank(t: Any) -> int | None:
+    """Rank of a term: a typed leaf's, carried through rank-preserving ops
+    and ``matmul`` of two operands of rank >= 2."""
+    for _ in range(64):
+        shape = getattr(getattr(t, "typ", None), "shape", None)
+        if shape is not None:
+            return len(shape)
+        if not is_op(t) or not t.args:
+            return None
+        if t.op == "matmul" and len(t.args) == 2:
+            ra, rb = _rank(t.args[0]), _rank(t.args[1])
+            return max(ra, rb) if ra is not None and rb is not None and min(ra, rb) >= 2 else None
+        if t.op in ("mul", "div", "add", "sub") and len(t.args) == 2:
+            ra, rb = _rank(t.args[0]), _rank(t.args[1])
+            known = [r for r in (ra, rb) if r is not None]
+            return max(known) if known else None
+        if t.op not in _SAME_RANK:
+            return None
+        t = t.args[0]
+    return None
 
 
 def _transposed_operand(kt: Any) -> Any | None:
@@ -115,28 +170,84 @@ def _transposed_operand(kt: Any) -> Any | None:
     dims = {int(d0), int(d1)}
     if dims == {-2, -1}:
         return kt.args[0]
-    typ = getattr(kt.args[0], "typ", None)  # a leaf of known rank n: dims n-2, n-1
-    rank = len(typ.shape) if typ is not None else None
+    rank = _rank(kt.args[0])  # a leaf of known rank n: dims n-2, n-1
     if rank is not None and rank >= 2 and dims == {rank - 2, rank - 1}:
         return kt.args[0]
     return None
 
 
-def parse_score(s: Any) -> dict | None:
-    """``(q, k, scale, mask)`` of ``masked_fill(scale·q kᵀ, M, -inf)``."""
-    mask = None
-    if is_op(s, "masked_fill", 3):
-        if not _is_neg_inf(s.args[2]):
-            return None
-        mask = s.args[1]
-        s = s.args[0]
+def _qk_product(s: Any) -> tuple[Any, Any, float] | None:
+    """``(q, k, c)`` of ``c · matmul(c' · q, transpose(k))``, ``c`` the
+    product of both scales."""
     s, scale = _peel_scale(s)
     if not is_op(s, "matmul", 2):
         return None
     k = _transposed_operand(s.args[1])
     if k is None:
         return None
-    return {"q": s.args[0], "k": k, "scale": scale, "mask": mask}
+    q, qs = _peel_scale(s.args[0])
+    return q, k, scale * qs
+
+
+def _last_axis(t: Any, dim: Any) -> bool:
+    if dim is None:
+        return False
+    d = int(dim)
+    rank = _rank(t)
+    return d == -1 or (rank is not None and d == rank - 1)
+
+
+def _qk_parts(s: Any) -> dict | None:
+    """``q``, ``k`` and scale of a score product: one ``q kᵀ``; a key-axis
+    ``concat`` of products sharing ``q`` and scale, whose ``k`` is the
+    key-axis concat of the blocks' keys; or a ``split`` / ``slice`` block of
+    either along the key or query axis, taken of ``k`` or ``q`` instead
+    (the reference's ``slice`` score mode)."""
+    one = _qk_product(s)
+    if one is not None:
+        return {"q": one[0], "k": one[1], "scale": one[2]}
+    body, outer = _peel_scale(s)
+    if (is_op(body, "split", 1) or is_op(body, "slice", 1)) and _block_start(body) is not None:
+        inner = _qk_parts(body.args[0])
+        if inner is None:
+            return None
+        side = "k" if _block_axis(body) == -1 else "q"
+        pushed = _push_block(body, inner[side])
+        if pushed is None:
+            return None
+        return dict(inner, **{side: pushed, "scale": inner["scale"] * outer})
+    if not is_op(body, "concat") or len(body.args) < 2:
+        return None
+    if not _last_axis(body, attr_of(body.attrs, "dim", "axis", default=None)):
+        return None
+    parts = [_qk_product(p) for p in body.args]
+    if any(p is None for p in parts):
+        return None
+    q0, _, c0 = parts[0]
+    if any(p[0] is not q0 or p[2] != c0 for p in parts):
+        return None
+    k = Op.make("concat", *[p[1] for p in parts], dim=-2)
+    return {"q": q0, "k": k, "scale": c0 * outer}
+
+
+def parse_score(s: Any) -> dict | None:
+    """``q``, ``k``, ``scale`` and the mask of a scaled-``q kᵀ`` score:
+    ``mask`` the masked set ``M`` of ``masked_fill(·, M, -inf)``, ``bias``
+    the addend ``B`` of ``add(·, B)``; ``None`` for any other score."""
+    if is_op(s, "masked_fill", 3):
+        if not _is_neg_inf(s.args[2]):
+            return None  # a finite fill changes what a fully masked row means
+        p = _qk_parts(s.args[0])
+        return None if p is None else dict(p, mask=s.args[1], bias=None)
+    if is_op(s, "add", 2):
+        a, b = s.args
+        for prod, addend in ((a, b), (b, a)):
+            p = _qk_parts(prod)
+            if p is not None:
+                return dict(p, mask=None, bias=addend)
+        return None
+    p = _qk_parts(s)
+    return None if p is None else dict(p, mask=None, bias=None)
 
 
 def _triangle_offset(masked: torch.Tensor) -> int | None:
@@ -163,64 +274,183 @@ def _triangle_offset(masked: torch.Tensor) -> int | None:
     return off if torch.equal(ref, keep) else None
 
 
-class HipOMModule(HipExecutorBase, nn.Module):
-    """Planned executor for ``om_apply(<om tree>)`` (module docstring)."""
+def _block_axis(t: Any) -> int | None:
+    """The axis, counted from the end (-1 keys, -2 queries), along which a
+    ``split`` / ``slice`` takes its block; ``None`` for another axis or an
+    unknown rank.  A negative ``slice`` dim counts as axis 0, as the slice
+    binding indexes (``torch_bridge.py:1347-1350``)."""
+    dim = attr_of(t.attrs, "dim", "axis", default=None)
+    if dim is None:
+        return None
+    d = int(dim)
+    rank = _rank(t.args[0])
+    if is_op(t, "slice", 1) and d < 0:
+        d = 0
+    if d >= 0:
+        if rank is None:
+            return None
+        d -= rank
+    return d if d in (-1, -2) else None
 
-    def __init__(self, ir: IR, param_values: dict | None = None, *, eval_mod: HipIRModule | None = None,
-                 device: Any = None, ops=None) -> None:
-        super().__init__()
-        self.eval_mod = eval_mod if eval_mod is not None else HipIRModule(ir, param_values, device=device, ops=ops)
-        self._inputs = list(ir.inputs)
-        self._const_cache: dict = {}
-        self.fallbacks = 0
-        self._plan = build_om_plan(self.eval_mod._root, self.eval_mod)
-        self._init_graph_state()
 
-    @property
-    def n_leaves(self) -> int:
-        return 0 if self._plan is None else len(self._plan["leaves"])
+def _block_start(t: Any) -> tuple[Any, int, int] | None:
+    """``(base, axis, start)`` of a ``split`` / ``slice`` taking a block of
+    ``base`` along one of its last two axes."""
+    d = _block_axis(t)
+    if d is None:
+        return None
+    base = t.args[0]
+    if is_op(t, "split", 1):
+        idx = attr_of(t.attrs, "index", default=None)
+        sizes = attr_of(t.attrs, "sizes", "split_size", default=None)
+        if idx is None or sizes is None:
+            return None
+        idx = int(idx)
+        if isinstance(sizes, (list, tuple)):
+            return base, d, sum(int(x) for x in sizes[:idx])
+        return base, d, idx * int(sizes)
+    if not is_op(t, "slice", 1):
+        return None
+    start = attr_of(t.attrs, "start", default=0) or 0
+    step = attr_of(t.attrs, "step", default=1) or 1
+    if int(step) != 1 or int(start) < 0:
+        return None
+    return base, d, int(start)
 
-    def _forward_impl(self, *xs: Any) -> Any:
-        if self._plan is None:
-            return self.eval_mod(*xs)
-        x, env = self._input_env(xs)
-        ev = self.ev_factory(env, x)
-        carriers = []
-        leaves = self._plan["leaves"]
-        single = len(leaves) == 1
-        for lf in leaves:
-            q, k, v = ev(lf["q"]), ev(lf["k"]), ev(lf["v"])
-            mask_kw = self._mask_kwargs(lf, ev)
-            if mask_kw is None or not _in_envelope(q, k, v):
-                self.fallbacks += 1
-                return self.eval_mod(*xs)
-            q4, k4, v4, lead = _as_bhtd(q, k, v)
-            if q4 is None:
-                self.fallbacks += 1
-                return self.eval_mod(*xs)
-            if single:
-                o = K.attention(q4, k4, v4, lf["scale"], normalize=True, **mask_kw)
-                return o.reshape(*lead, o.shape[-2], o.shape[-1])
-            a, m, lsum = K.attention(q4, k4, v4, lf["scale"], normalize=False, return_ml=True, **mask_kw)
-            carriers.append((m, lsum, a.float()))
-        # pairwise combine in tree order (adjacent pairs, odd tail carried up)
-        while len(carriers) > 1:
-            nxt = [K.om_compose(carriers[i], carriers[i + 1]) for i in range(0, len(carriers) - 1, 2)]
-            if len(carriers) % 2:
-                nxt.append(carriers[-1])
-            carriers = [(m.reshape(carriers[0][0].shape), lv.reshape(carriers[0][1].shape),
-                         acc.reshape(carriers[0][2].shape)) for m, lv, acc in nxt]
-        m, lsum, acc = carriers[0]
-        out = (acc / lsum).to(ev(leaves[0]["q"]).dtype)
-        return out.reshape(*lead, out.shape[-2], out.shape[-1])
 
-    def _mask_kwargs(self, lf: dict, ev) -> dict | None:
-        return mask_kwargs(lf, ev)
+def _push_block(t: Any, operand: Any) -> Any | None:
+    """The block ``t`` takes of a score, taken instead of ``operand``'s
+    sequence axis (-2 of ``q`` for query blocks, of ``k`` for key blocks)."""
+    attrs = dict(t.attrs)
+    attrs.pop("axis", None)
+    if is_op(t, "split", 1):
+        attrs["dim"] = -2
+        return Op.make("split", operand, **attrs)
+    rank = _rank(operand)
+    if rank is None or rank < 2:
+        return None
+    attrs["dim"] = rank - 2
+    return Op.make("slice", operand, **attrs)
+
+
+def _cmask_causal_off(M: Any) -> int | None:
+    """Causal bound of a ``cmask(x, off)`` masked set or a block of it: keep
+    key ``j`` for query ``i`` iff ``j <= i + result`` in the block's own
+    coordinates (``cmask`` masks ``j + off > i``, ``om.py:1023-1029``)."""
+    qstart = kstart = 0
+    t = M
+    while is_op(t, "split", 1) or is_op(t, "slice", 1):
+        st = _block_start(t)
+        if st is None:
+            return None
+        t, axis, start = st
+        if axis == -1:
+            kstart += start
+        else:
+            qstart += start
+    if not is_op(t, "cmask", 1):
+        return None
+    return qstart - kstart - int(t.attrs.get("off", 0) or 0)
+
+
+def _shared_plane(t: torch.Tensor) -> torch.Tensor | None:
+    """The one ``(Tq, Tk)`` plane ``t`` holds over its leading axes, or
+    ``None`` when they carry different planes."""
+    if not isinstance(t, torch.Tensor) or t.dim() < 2:
+        return None
+    t3 = t.reshape(-1, *t.shape[-2:])
+    if t3.shape[0] != 1 and not bool(((t3 == t3[:1]) | (t3.isnan() & t3[:1].isnan())).all()):
+        return None
+    return t3[0]
+
+
+def _const_value(t: Any, eval_mod: HipIRModule) -> torch.Tensor | None:
+    """The value of a weight-only mask term at construction: a (folded)
+    Param, or any other parameter-only subtree (``split`` / ``slice`` /
+    ``attnbias`` of a Param, which the weight fold leaves in place)
+    evaluated once on the device; ``None`` for a term that reads an
+    input."""
+    pv = eval_mod._pv(t)
+    if pv is not None or not isinstance(t, Op):
+        return pv
+    for node in postorder(t):
+        for a in node.args:
+            if _is_var(a) or (_is_param(a) and eval_mod._pv(a) is None):
+                return None
+    try:
+        out = eval_term(t, {}, eval_mod._param_map, eval_mod.ops)
+    except Exception:
+        return None  # not foldable: the mask is evaluated per call
+    return out if isinstance(out, torch.Tensor) else None
+
+
+def _keep_const(lf: dict, keep: torch.Tensor) -> None:
+    off = _triangle_offset(~keep)
+    if off is not None:
+        lf["mask_kind"], lf["causal_off"] = "causal", -off
+        return
+    plane = _shared_plane(keep)
+    if plane is None:
+        lf["mask_kind"] = "scores"  # a per-batch mask
+    else:
+        lf["mask_kind"], lf["keep"] = "bool_const", plane.contiguous()
+
+
+def _bias_const(lf: dict, bias: torch.Tensor) -> None:
+    vals = bias.float()
+    if bool(((vals == 0) | (vals == float("-inf"))).all()):
+        _keep_const(lf, vals == 0)  # a 0 / -inf bias is a keep-mask
+        return
+    plane = _shared_plane(vals)
+    if plane is None:
+        lf["mask_kind"] = "scores"
+    else:
+        lf["mask_kind"], lf["bias_plane"] = "bias_const", plane.contiguous()
+
+
+def _classify_mask(lf: dict, eval_mod: HipIRModule) -> bool:
+    """Fix the kernel mask mode of a parsed leaf (keys ``mask`` / ``bias``)
+    where the mask is known at construction; ``False`` when it cannot be a
+    kernel mode at all.  ``mask_kind`` "scores" marks a weight-only mask
+    that differs over the leading axes."""
+    M, B = lf.get("mask"), lf.get("bias")
+    if M is None and B is None:
+        lf["mask_kind"] = "none"
+        return True
+    if M is not None:
+        off = _cmask_causal_off(M)
+        if off is not None:
+            lf["mask_kind"], lf["causal_off"] = "causal", off
+            return True
+        pv = _const_value(M, eval_mod)
+        if pv is None:
+            lf["mask_kind"] = "runtime"
+            return True
+        if not isinstance(pv, torch.Tensor) or pv.dtype != torch.bool:
+            return False
+        _keep_const(lf, ~pv)
+        return True
+    coerce = is_op(B, "attnbias", 1)  # attnbias(m): torch's attn_mask coercion
+    src = B.args[0] if coerce else B
+    pv = _const_value(src, eval_mod)
+    if pv is None:
+        lf["mask_kind"], lf["bias_term"], lf["attnbias"] = "bias_runtime", src, coerce
+        return True
+    if not isinstance(pv, torch.Tensor) or pv.dim() < 2:
+        return False
+    if pv.dtype == torch.bool:
+        if not coerce:
+            return False  # adding a bool is not a mask
+        _keep_const(lf, pv)
+    else:
+        _bias_const(lf, pv)
+    return True
 
 
 def mask_kwargs(lf: dict, ev) -> dict | None:
-    """Attention-kernel mask arguments of a parsed leaf; ``None`` when a
-    runtime mask is not a single ``(Tq, Tk)`` plane shared over (B, H)."""
+    """Attention-kernel mask arguments of an ``attn`` leaf; ``None`` when the
+    call's mask is not one ``(Tq, Tk)`` plane shared over the leading axes
+    (the leaf then takes the score path)."""
     kind = lf["mask_kind"]
     if kind == "none":
         return {}
@@ -228,13 +458,27 @@ def mask_kwargs(lf: dict, ev) -> dict | None:
         return {"causal": True, "causal_off": lf["causal_off"]}
     if kind == "bool_const":
         return {"mask": lf["keep"]}
-    masked = ev(lf["mask"])
-    if not isinstance(masked, torch.Tensor) or masked.dim() < 2:
-        return None
-    m2 = masked.reshape(-1, *masked.shape[-2:])
-    if m2.shape[0] != 1:
-        return None
-    return {"mask": torch.logical_not(m2[0].to(torch.bool))}
+    if kind == "bias_const":
+        return {"bias": lf["bias_plane"]}
+    if kind == "runtime":
+        masked = ev(lf["mask"])
+        if not isinstance(masked, torch.Tensor) or masked.dtype != torch.bool:
+            return None
+        plane = _shared_plane(masked)
+        return None if plane is None else {"mask": torch.logical_not(plane)}
+    if kind == "bias_runtime":
+        b = ev(lf["bias_term"])
+        if not isinstance(b, torch.Tensor):
+            return None
+        plane = _shared_plane(b)
+        if plane is None:
+            return None
+        if b.dtype == torch.bool:
+            return {"mask": plane} if lf["attnbias"] else None
+        if not b.dtype.is_floating_point:
+            return None
+        return {"bias": plane}
+    return None
 
 
 def _in_envelope(q, k, v) -> bool:
@@ -247,6 +491,22 @@ def _in_envelope(q, k, v) -> bool:
     return d in (64, 128) and k.shape[-1] == d and v.shape[-1] == d and 2 <= q.dim() <= 4
 
 
+def _f32_envelope(q, k, v) -> bool:
+    """Operands of the fp32 carrier kernel: ``dk <= 128``, ``dv <= 256``, one
+    leading shape (or a 2-D ``q`` / ``v`` shared over it)."""
+    ts = (q, k, v)
+    if not all(isinstance(t, torch.Tensor) and t.device.type == "cuda" and t.dtype == torch.float32
+               for t in ts):
+        return False
+    if q.dim() < 2 or k.dim() < 2 or v.dim() < 2:
+        return False
+    lead = tuple(k.shape[:-2])
+    return (0 < q.shape[-1] <= 128 and k.shape[-1] == q.shape[-1] and 0 < v.shape[-1] <= 256
+            and v.shape[-2] == k.shape[-2] > 0
+            and (q.dim() == 2 or tuple(q.shape[:-2]) == lead)
+            and (v.dim() == 2 or tuple(v.shape[:-2]) == lead))
+
+
 def _as_bhtd(q, k, v):
     lead = tuple(q.shape[:-2])
     if k.shape[:-2] != q.shape[:-2] or v.shape[:-2] != q.shape[:-2] or k.shape[-2] != v.shape[-2]:
@@ -257,7 +517,8 @@ def _as_bhtd(q, k, v):
 
 
 def build_om_plan(root: Any, eval_mod: HipIRModule) -> dict | None:
-    """Parse ``om_apply(<om tree>)`` into per-leaf kernel arguments."""
+    """Classify the leaves of ``om_apply(<om tree>)``; ``None`` for any other
+    root."""
     if not is_op(root, "om_apply") or not root.args:
         return None
     leaves = om_leaves(root.args[0])
@@ -265,44 +526,146 @@ def build_om_plan(root: Any, eval_mod: HipIRModule) -> dict | None:
         return None
     plan_leaves = []
     for leaf in leaves:
+        if is_op(leaf, "om", 3):
+            plan_leaves.append({"kind": "om", "m": leaf.args[0], "l": leaf.args[1], "a": leaf.args[2]})
+            continue
         s, v = leaf.args
+        lf: dict = {"kind": "scores", "s": s, "v": v}
         sc = parse_score(s)
-        if sc is None:
-            return None
-        if not (math.isfinite(sc["scale"]) and sc["scale"] > 0):
-            # the kernel tracks the row max of q·k and scales it, which is the
-            # max of the scaled scores only for a positive scale
-            return None
-        lf = {"q": sc["q"], "k": sc["k"], "v": v, "scale": sc["scale"], "mask": sc["mask"]}
-        if not _classify_mask(lf, eval_mod):
-            return None
+        # the kernels track the row max of q·k and scale it, which is the max
+        # of the scaled scores only for a positive scale
+        if sc is not None and math.isfinite(sc["scale"]) and sc["scale"] > 0:
+            la = dict(lf, q=sc["q"], k=sc["k"], scale=sc["scale"], mask=sc["mask"], bias=sc["bias"])
+            if _classify_mask(la, eval_mod) and la["mask_kind"] != "scores":
+                la["kind"] = "attn"
+                lf = la
         plan_leaves.append(lf)
     return {"leaves": plan_leaves}
 
 
-def _classify_mask(lf: dict, eval_mod: HipIRModule) -> bool:
-    m = lf["mask"]
-    if m is None:
-        lf["mask_kind"] = "none"
-        return True
-    if is_op(m, "cmask", 1):
-        lf["mask_kind"] = "causal"
-        lf["causal_off"] = -int(m.attrs.get("off", 0) or 0)
-        return True
-    pv = eval_mod._pv(m)
-    if pv is not None:  # weight-only mask (folded into a Param)
-        if pv.dtype != torch.bool:
-            return False
-        off = _triangle_offset(pv)
-        if off is not None:
-            lf["mask_kind"] = "causal"
-            lf["causal_off"] = -off
-            return True
-        m2 = pv.reshape(-1, *pv.shape[-2:])
-        if m2.shape[0] != 1:
-            return False
-        lf["mask_kind"] = "bool_const"
-        lf["keep"] = torch.logical_not(m2[0]).contiguous()
-        return True
-    lf["mask_kind"] = "runtime"
-    return True
+def _device_float(*ts) -> bool:
+    return all(isinstance(t, torch.Tensor) and t.device.type == "cuda"
+               and t.dtype in (torch.float32, torch.bfloat16) for t in ts)
+
+
+def _identity_like(f: tuple) -> tuple:
+    m, lv, a = f
+    return torch.full_like(m, float("-inf")), torch.zeros_like(lv), torch.zeros_like(a)
+
+
+def _broadcast_carriers(carriers: list) -> list:
+    """Expand every carrier component to the common broadcast shape of that
+    component, as the reference's stacked reduction does
+    (``om_lower.py:806-826``)."""
+    shapes = [torch.broadcast_shapes(*[c[i].shape for c in carriers]) for i in range(3)]
+    return [tuple(t if t.shape == sh else t.expand(sh).contiguous() for t, sh in zip(c, shapes))
+            for c in carriers]
+
+
+class HipOMModule(HipExecutorBase, nn.Module):
+    """Planned executor for ``om_apply(<om tree>)`` (module docstring)."""
+
+    def __init__(self, ir: IR, param_values: dict | None = None, *, eval_mod: HipIRModule | None = None,
+                 device: Any = None, ops=None) -> None:
+        super().__init__()
+        self.eval_mod = eval_mod if eval_mod is not None else HipIRModule(ir, param_values, device=device, ops=ops)
+        self._inputs = list(ir.inputs)
+        self._const_cache: dict = {}
+        self.fallbacks = 0       # leaves (or whole calls) run on the generic tensor ops
+        self.kernel_leaves = 0   # leaves of the last call on an attention kernel
+        self._plan = build_om_plan(self.eval_mod._root, self.eval_mod)
+        self._init_graph_state()
+
+    @property
+    def n_leaves(self) -> int:
+        return 0 if self._plan is None else len(self._plan["leaves"])
+
+    @property
+    def leaf_kinds(self) -> list[str]:
+        """Plan class of each leaf ("attn", "scores" or "om")."""
+        return [] if self._plan is None else [lf["kind"] for lf in self._plan["leaves"]]
+
+    def _attn(self, lf: dict, ev, normalize: bool):
+        """An ``attn`` leaf on the attention kernels: the normalised output
+        when ``normalize`` (bf16 kernel only), else ``((m, l, a), dtype)``;
+        ``None`` outside the kernels' envelopes."""
+        q, k, v = ev(lf["q"]), ev(lf["k"]), ev(lf["v"])
+        if not _in_envelope(q, k, v):
+            if normalize or lf["mask_kind"] != "none" or not _f32_envelope(q, k, v):
+                return None
+            self.kernel_leaves += 1
+            return K.attn_carrier_f32(q, k, v, float(lf["scale"])), v.dtype
+        mask_kw = mask_kwargs(lf, ev)
+        if mask_kw is None:
+            return None
+        q4, k4, v4, lead = _as_bhtd(q, k, v)
+        if q4 is None:
+            return None
+        self.kernel_leaves += 1
+        if normalize:
+            o = K.attention(q4, k4, v4, lf["scale"], normalize=True, **mask_kw)
+            return o.reshape(*lead, o.shape[-2], o.shape[-1])
+        a, m, lsum = K.attention(q4, k4, v4, lf["scale"], normalize=False, return_ml=True, **mask_kw)
+        tq, dv = a.shape[-2], a.shape[-1]
+        return (m.reshape(*lead, tq, 1), lsum.reshape(*lead, tq, 1), a.float().reshape(*lead, tq, dv)), v.dtype
+
+    def _carrier(self, lf: dict, ev):
+        """``((m, l, a), value dtype)`` of one leaf, sanitised.  Operands
+        outside the kernels' dtypes run the module's own ``om_elem`` /
+        ``om_compose`` bindings (counted in ``fallbacks``)."""
+        if lf["kind"] == "attn":
+            r = self._attn(lf, ev, normalize=False)
+            if r is not None:
+                return r
+        if lf["kind"] == "om":
+            f = (ev(lf["m"]), ev(lf["l"]), ev(lf["a"]))
+            if _device_float(*f):
+                f = tuple(t.float() for t in f)
+                # composing with the ⊕ identity applies the isfinite guard
+                return self._compose(_identity_like(f), f), f[2].dtype
+            self.fallbacks += 1
+            return self.eval_mod.ops["om_compose"](_identity_like(f), f), f[2].dtype
+        s, v = ev(lf["s"]), ev(lf["v"])
+        if _device_float(s, v) and s.dim() and v.dim() and s.numel() and v.numel():
+            return K.om_elem_scores(s, v, sanitize=True), torch.promote_types(s.dtype, v.dtype)
+        self.fallbacks += 1
+        m, lv, a = self.eval_mod.ops["om_elem"](s, v)
+        fin = torch.isfinite(m)
+        return (m, torch.where(fin, lv, 0.0), torch.where(fin, a, 0.0)), a.dtype
+
+    def _compose(self, f: tuple, g: tuple) -> tuple:
+        if all(isinstance(t, torch.Tensor) and t.device.type == "cuda" and t.dtype == torch.float32
+               for t in (*f, *g)):
+            m, lv, acc = K.om_compose(f, g)
+            return m.reshape(f[0].shape), lv.reshape(f[1].shape), acc.reshape(f[2].shape)
+        self.fallbacks += 1
+        return self.eval_mod.ops["om_compose"](f, g)
+
+    def _forward_impl(self, *xs: Any) -> Any:
+        if self._plan is None:
+            return self.eval_mod(*xs)
+        if any(isinstance(t, torch.Tensor) and t.device.type != "cuda" for t in xs):
+            self.fallbacks += 1  # host inputs: the generic module (which raises on the product table)
+            return self.eval_mod(*xs)
+        x, env = self._input_env(xs)
+        ev = self.ev_factory(env, x)
+        self.kernel_leaves = 0
+        leaves = self._plan["leaves"]
+        if len(leaves) == 1 and leaves[0]["kind"] == "attn":
+            o = self._attn(leaves[0], ev, normalize=True)
+            if o is not None:
+                return o
+        carriers, out_dtype = [], None
+        for lf in leaves:
+            f, dt = self._carrier(lf, ev)
+            carriers.append(f)
+            out_dtype = dt if out_dtype is None else torch.promote_types(out_dtype, dt)
+        carriers = _broadcast_carriers(carriers)
+        # canonical adjacent-pair reduction, odd tail carried up (om_lower.py:800-832)
+        while len(carriers) > 1:
+            nxt = [self._compose(carriers[i], carriers[i + 1]) for i in range(0, len(carriers) - 1, 2)]
+            if len(carriers) % 2:
+                nxt.append(carriers[-1])
+            carriers = nxt
+        _, lsum, acc = carriers[0]
+        return (acc / lsum).to(out_dtype)

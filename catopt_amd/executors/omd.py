@@ -170,7 +170,7 @@ def _plain_score(leaf: Any) -> dict | None:
         return None
     sc = parse_score(leaf.args[0])
     if sc is not None:
-        return dict(sc, axes=None) if sc["mask"] is None else None
+        return dict(sc, axes=None) if sc["mask"] is None and sc["bias"] is None else None
     s, scale = _peel_scale(leaf.args[0])
     if not is_op(s, "matmul", 2) or not is_op(s.args[1], "transpose", 1):
         return None

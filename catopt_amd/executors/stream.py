@@ -12,12 +12,15 @@ block plus the carrier, never the full q × T_kv score matrix.
 
 Leaves:
 
-* ``om_elem(s, v)`` whose score parses as ``scale · q kᵀ`` (optionally
-  ``masked_fill(…, M, -inf)``) with bf16 operands and head dim 64 / 128: one
-  launch of the HIP attention kernel in carrier mode (scores, mask and
+* ``om_elem(s, v)`` whose score parses as a positively scaled ``q kᵀ`` with
+  a mask the attention kernel takes (the spellings of the batched om
+  executor: ``masked_fill(…, M, -inf)``, ``add(…, attnbias(m))``, key-axis
+  ``concat`` scores) with bf16 operands and head dim 64 / 128: one launch
+  of the HIP attention kernel in carrier mode (scores, mask and
   exponentials stay on chip; the carrier is fp32);
 * any other ``om_elem(s, v)``: the score and value operands are evaluated and
-  folded with ``om_elem`` (``torch_bridge.py:1974-1981``);
+  folded with ``om_elem`` (``torch_bridge.py:1974-1981``; on device fp32 /
+  bf16 operands the ``catopt_hip_om_rows`` row kernel and the HIP GEMM);
 * a packaged carrier ``om(m, l, a)``: used as is.
 
 States compose with the HIP ``om_compose`` kernel when both carriers are
@@ -35,6 +38,7 @@ recorded into a hipGraph by the caller.
 
 from __future__ import annotations
 
+import math
 from typing import Any
 
 import torch
@@ -137,9 +141,12 @@ def build_stream_plan(root: Any, eval_mod: HipIRModule) -> dict | None:
         s, v = leaf.args
         lf: dict = {"kind": "elem", "s": s, "v": v}
         sc = parse_score(s)
-        if sc is not None:
-            lq = {"q": sc["q"], "k": sc["k"], "v": v, "scale": sc["scale"], "mask": sc["mask"]}
-            if _classify_mask(lq, eval_mod):
+        # the kernel scales the row max of q·k: the scaled scores' max only
+        # for a positive scale
+        if sc is not None and math.isfinite(sc["scale"]) and sc["scale"] > 0:
+            lq = {"q": sc["q"], "k": sc["k"], "v": v, "scale": sc["scale"], "mask": sc["mask"],
+                  "bias": sc["bias"]}
+            if _classify_mask(lq, eval_mod) and lq["mask_kind"] != "scores":
                 lf.update(lq)
                 lf["kind"] = "qk"
         plan.append(lf)

@@ -215,16 +215,24 @@ def attention(
     causal: bool = False,
     causal_off: int = 0,
     mask: torch.Tensor | None = None,
+    bias: torch.Tensor | None = None,
     normalize: bool = True,
     return_ml: bool = False,
+    empty_rows: str = "nan",
 ):
     """Online-softmax attention ``(B,H,T,d)`` bf16.
 
     ``causal`` keeps key ``j`` for query ``i`` iff ``j <= i + causal_off``;
-    ``mask`` is a bool keep-mask ``(Tq, Tk)`` shared over (B, H).  With
+    ``mask`` is a bool keep-mask ``(Tq, Tk)`` shared over (B, H); ``bias``
+    an additive float ``(Tq, Tk)`` plane added to ``scale·q kᵀ`` (``-inf``
+    entries mask).  With
     ``normalize=False`` the raw numerator ``a`` is returned; ``return_ml``
-    adds the fp32 ``(m, l)`` om carriers, shaped ``(B, H, Tq, 1)``.
+    adds the fp32 ``(m, l)`` om carriers, shaped ``(B, H, Tq, 1)``.  A fully
+    masked row normalises to NaN (``empty_rows="nan"``, om_apply's 0/0) or
+    to 0 (``"zero"``, torch's scaled_dot_product_attention).
     """
+    if empty_rows not in ("nan", "zero"):
+        raise ValueError(f"empty_rows is 'nan' or 'zero', got {empty_rows!r}")
     _need_device(q, k, v, mask)
     lib = L.load()
     if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
@@ -247,25 +255,58 @@ def attention(
     mode = L.MASK_NONE
     mask_u8 = None
     mask_ld = 0
+    if (mask is not None) + (bias is not None) + bool(causal) > 1:
+        raise ValueError("pass at most one of causal=True, mask, bias")
     if mask is not None:
-        if causal:
-            raise ValueError("pass either causal=True or a mask, not both")
         if mask.shape[-2:] != (Tq, Tk) or mask.numel() != Tq * Tk:
             raise NotImplementedError("mask must be a (Tq, Tk) keep-mask shared over (B, H)")
         mask_u8 = mask.reshape(Tq, Tk).to(torch.uint8).contiguous()
         mask_ld = Tk
         mode = L.MASK_BOOL
+    elif bias is not None:
+        _need_device(bias)
+        if bias.shape[-2:] != (Tq, Tk) or bias.numel() != Tq * Tk:
+            raise NotImplementedError("bias must be a (Tq, Tk) plane shared over (B, H)")
+        mask_u8 = bias.reshape(Tq, Tk).to(torch.float32).contiguous()
+        mask_ld = Tk
+        mode = L.MASK_BIAS
     elif causal:
         mode = L.MASK_CAUSAL
     st = lib.catopt_hip_attn_fwd(
         L.BF16, B, H, Tq, Tk, d, dv, _ptr(q), L.i64_array(qs), _ptr(k), L.i64_array(ks),
         _ptr(v), L.i64_array(vs), float(scale), mode, int(causal_off), _ptr(mask_u8), mask_ld,
-        int(bool(normalize)), _ptr(o), L.i64_array([o.stride(0), o.stride(1), o.stride(2)]),
+        (2 if empty_rows == "zero" else 1) if normalize else 0, _ptr(o), L.i64_array([o.stride(0), o.stride(1), o.stride(2)]),
         _ptr(m), _ptr(l), _stream(q))
     L.check("catopt_hip_attn_fwd", st)
     if return_ml:
         return o, m.unsqueeze(-1), l.unsqueeze(-1)
     return o
+
+
+def om_rows(s: torch.Tensor, sanitize: bool = False) -> tuple:
+    """Row statistics of a score block ``s (…, cols)``: ``m = rowmax``,
+    ``e = exp(s - m)``, ``l = Σ e`` in fp32 (``m``, ``l`` shaped ``(…, 1)``).
+    ``sanitize`` zeroes ``l`` and ``e`` on rows whose max is not finite."""
+    _need_device(s)
+    lib = L.load()
+    dt = _dtype_code(s)
+    cols = s.shape[-1]
+    s2, lds = _rows_view(s) if s.dim() else (s.reshape(1, 1), 1)
+    rows = s2.shape[0]
+    m = torch.empty(s.shape[:-1] + (1,), dtype=torch.float32, device=s.device)
+    lv = torch.empty_like(m)
+    e = torch.empty(s.shape, dtype=torch.float32, device=s.device)
+    st = lib.catopt_hip_om_rows(dt, rows, cols, _ptr(s2), lds, int(bool(sanitize)), _ptr(m), _ptr(lv),
+                                _ptr(e), cols, _stream(s))
+    L.check("catopt_hip_om_rows", st)
+    return m, lv, e
+
+
+def om_elem_scores(s: torch.Tensor, v: torch.Tensor, sanitize: bool = False) -> tuple:
+    """The om element of an explicit score block: ``(rowmax s, Σ exp(s - m),
+    exp(s - m) @ v)`` in fp32, ``v`` broadcasting like ``matmul``."""
+    m, lv, e = om_rows(s, sanitize)
+    return m, lv, matmul(e, v.to(torch.float32))
 
 
 def om_compose(f, g):

@@ -33,8 +33,9 @@ from typing import Any, Mapping
 import torch
 
 from . import _lib as L
-from .bindings import HipOpTable
+from .bindings import HipOpTable, torch_fallback_count
 from .evaluator import HipIRModule
+from .folds import specialize_causal
 from .executors import (
     HipChunkedDecayModule,
     HipOMModule,
@@ -117,6 +118,13 @@ class HipSink:
     def lower(self, ir: IR, params: dict | None = None) -> HipIRModule:
         return HipIRModule(ir, params, ops=self._ops, device=self.device)
 
+    def specialize_causal(self, term: Any, params: dict, memo: dict) -> Any:
+        """The causal-mask const fold (``adapters.py:102-113``):
+        ``sdpa(q, k, v, mask) → sdpa(q, k, v, arg5=True)`` where the
+        parameter-only mask is the causal keep-mask, evaluated on this
+        sink's device; ``memo["_hit"]`` records a rewrite."""
+        return specialize_causal(term, params, memo, ops=self._ops, device=self.device)
+
     def verify(self, ref: Any, opt: Any, inputs: Any, *, rtol: float = 1e-4,
                atol: float | None = None) -> VerifyReport:
         return verify_module(ref, opt, inputs, rtol=rtol, atol=atol)
@@ -189,8 +197,12 @@ def deliver(ir: IR, params: dict | None, sink: Any, example_inputs: Any = None, 
 
     ``stats`` carries the reference's keys — ``lowering`` ("batched" or
     "generic"), ``executor``, ``runner``, ``cuda_graph``,
-    ``cuda_graph_failure`` — plus ``hip_kernel`` (the planned executor ran
-    its HIP path) and ``fallbacks``.
+    ``cuda_graph_failure`` — plus ``fallbacks`` (the planned executor's
+    generic-path calls or leaves) and, with ``example_inputs``, the record of
+    one counted eager call: ``hip_calls`` (HIP entry points it ran),
+    ``torch_fallback_ops`` (HIP-backed bindings that took their torch device
+    op) and ``hip_kernel`` (``hip_calls > 0``; without inputs, whether a
+    planned executor engaged).
     """
     stats: dict = {}
     spec = route_spec(ir.root, sink)
@@ -203,6 +215,16 @@ def deliver(ir: IR, params: dict | None, sink: Any, example_inputs: Any = None, 
     stats["executor"] = spec.name if spec is not None else "generic"
     stats["lowering"] = "batched" if engaged else "generic"
     stats["hip_kernel"] = engaged
+    if example_inputs is not None:
+        # one eager call, counted: HIP entry points that ran, and HIP-backed
+        # bindings that took their torch device op instead
+        xs = example_inputs if isinstance(example_inputs, (tuple, list)) else (example_inputs,)
+        n_hip, n_torch = L.call_count(), torch_fallback_count()
+        with torch.no_grad():
+            module(*xs)
+        stats["hip_calls"] = L.call_count() - n_hip
+        stats["torch_fallback_ops"] = torch_fallback_count() - n_torch
+        stats["hip_kernel"] = stats["hip_calls"] > 0
     if runner is not None and example_inputs is not None:
         stats["runner"] = getattr(runner, "name", type(runner).__name__)
         module = runner.apply(module, example_inputs, stats)

@@ -60,7 +60,8 @@ enum catopt_epilogue {
 enum catopt_mask_mode {
   CATOPT_MASK_NONE = 0,
   CATOPT_MASK_CAUSAL = 1,    /* keep key j for query i iff j <= i + causal_off */
-  CATOPT_MASK_BOOL = 2       /* keep where mask[i, j] != 0 (uint8 keep-mask) */
+  CATOPT_MASK_BOOL = 2,      /* keep where mask[i, j] != 0 (uint8 keep-mask) */
+  CATOPT_MASK_BIAS = 3       /* add the fp32 bias mask[i, j] to scale·q·kᵀ (-inf masks) */
 };
 
 /* ABI version of the loaded library; equals CATOPT_HIP_ABI_VERSION. */
@@ -127,13 +128,18 @@ int32_t catopt_hip_matmul(int32_t dtype, int64_t batch, int64_t M, int64_t N,
  * Online-softmax attention forward over (batch, heads):
  *   s = scale · q kᵀ, masked entries set to -inf,
  *   (m, l, a) = (rowmax s, Σ exp(s - m), exp(s - m) · v)
- *   o = a / l           when normalize != 0   (om_apply: unclamped, a
+ *   o = a / l           when normalize == 1   (om_apply: unclamped, a
  *                                              fully masked row gives NaN)
+ *   o = a / l           when normalize == 2   (sdpa: a fully masked row
+ *                                              gives 0)
  *   o = a               when normalize == 0   (the raw om numerator)
  * q: [B, H, Tq, d], k: [B, H, Tk, d], v: [B, H, Tk, dv], o: [B, H, Tq, dv];
  * the last axis is contiguous, the other three axes take explicit strides
- * (element counts, order b, h, t).  mask (mode CATOPT_MASK_BOOL) is a uint8
- * keep-mask [Tq, Tk] with row stride mask_ld, shared over (b, h).  m_out
+ * (element counts, order b, h, t).  mask is a [Tq, Tk] plane with row
+ * stride mask_ld, shared over (b, h): a uint8 keep-mask in mode
+ * CATOPT_MASK_BOOL, an fp32 additive bias (4-byte aligned) in mode
+ * CATOPT_MASK_BIAS — sdpa's float attn_mask, the attnbias(m) score term of
+ * the explicit-mask form (om.py:1036-1050, 1315-1335).  m_out
  * and l_out (fp32, [B, H, Tq] contiguous) are optional: the om carriers
  * for om_compose with other key blocks.  bf16 only; d = dv = 128 or 64.
  * Replaces, for the OM_LIFT delivered form (om.py:153-193):
@@ -149,15 +155,32 @@ int32_t catopt_hip_attn_fwd(int32_t dtype, int64_t B, int64_t H, int64_t Tq,
                             const void* k, const int64_t* k_strides,
                             const void* v, const int64_t* v_strides,
                             float scale, int32_t mask_mode,
-                            int64_t causal_off, const uint8_t* mask,
+                            int64_t causal_off, const void* mask,
                             int64_t mask_ld, int32_t normalize, void* o,
                             const int64_t* o_strides, float* m_out,
                             float* l_out, void* stream);
 
 /*
+ * Row statistics of an explicit score block for the om element
+ * (_om_elem, torch_bridge.py:1974-1981; _batched_elem, om_lower.py:
+ * 462-472): for each row r of s [rows, cols] (fp32 or bf16, row stride lds)
+ *   m[r] = max_c s[r, c]            (NaN when the row holds a NaN, as amax)
+ *   e[r, c] = exp(s[r, c] - m[r]),  l[r] = Σ_c e[r, c]
+ * in fp32 (e with row stride lde); a = e @ v then follows on the GEMM.
+ * sanitize != 0 zeroes l and e on rows whose m is not finite (the leaf
+ * sanitising of BatchedOMModule, om_lower.py:792-798); sanitize == 0 keeps
+ * the raw binding's NaN for a fully masked row.
+ */
+int32_t catopt_hip_om_rows(int32_t dtype, int64_t rows, int64_t cols,
+                           const void* s, int64_t lds, int32_t sanitize,
+                           float* m, float* l, float* e, int64_t lde,
+                           void* stream);
+
+/*
  * Combine two om carriers (m, l, a) elementwise — the FlashAttention merge
  * with the isfinite guards of _om_compose (torch_bridge.py:1984-2006):
- *   mx = max(m1, m2); e_i = isfinite(m_i) ? exp(m_i - mx) : 0;
+ *   mx = max(m1, m2) (NaN-propagating, as torch.maximum);
+ *   e_i = isfinite(m_i) ? exp(m_i - mx) : 0;
  *   l = l1 e1 + l2 e2;  a = a1 e1 + a2 e2.
  * m, l: [rows] fp32; a: [rows, dv] fp32.  Outputs may alias input 1.
  */

@@ -54,9 +54,12 @@ def _om_compose(f, g, *a, **kw):
     m1, l1, a1 = f
     m2, l2, a2 = g
     mx = torch.maximum(m1, m2)
-    e1 = torch.where(torch.isfinite(m1), torch.exp(m1 - mx), torch.zeros_like(mx))
-    e2 = torch.where(torch.isfinite(m2), torch.exp(m2 - mx), torch.zeros_like(mx))
-    return mx, l1 * e1 + l2 * e2, a1 * e1 + a2 * e2
+    f1, f2 = torch.isfinite(m1), torch.isfinite(m2)
+    e1 = torch.where(f1, torch.exp(m1 - mx), torch.zeros_like(mx))
+    e2 = torch.where(f2, torch.exp(m2 - mx), torch.zeros_like(mx))
+    # a block whose max is not finite contributes nothing, NaN l / a included
+    lv = torch.where(f1, l1 * e1, 0.0) + torch.where(f2, l2 * e2, 0.0)
+    return mx, lv, torch.where(f1, a1 * e1, 0.0) + torch.where(f2, a2 * e2, 0.0)
 
 
 def _om_elem(s, v, *a, **kw):

@@ -204,12 +204,12 @@ def test_om_parse_declines_a_finite_fill_and_an_untransposed_key():
 @pytest.mark.parametrize("c", [0.0, -2.0])
 def test_om_plan_declines_a_non_positive_scale(c):
     # the kernel scales the row max of q·k, which is the max of the scaled
-    # scores only for a positive scale: such a leaf runs the generic module
+    # scores only for a positive scale: such a leaf takes the score path
     q, k, v = (Var(n, TensorType((1, 2, 16, 64))) for n in "qkv")
     s = mk("mul", mk("matmul", q, mk("transpose", k, dim0=-2, dim1=-1)), Const(c))
     root = mk("om_apply", mk("om_elem", s, v))
     mod = HipOMModule(IR(root, [q, k, v]), {}, ops=cpu_table())
-    assert mod._plan is None
+    assert mod.leaf_kinds == ["scores"]
     qs, ks, vs = (torch.randn(1, 2, 16, 64, dtype=torch.float64) for _ in range(3))
     out = mod(qs, ks, vs)
     ref = torch.softmax(c * (qs @ ks.transpose(-2, -1)), -1) @ vs
