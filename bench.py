@@ -1,6 +1,6 @@
 """Delivered-form throughput of the HIP executor on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--forms c1,c2,c3,c4,c5,aff,omd,copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--forms c1,c2,c3,c4,c5,aff,omd,copy,read]
                     [--cpu-budget SECONDS] [--no-cpu]
 
 One "step" is one forward of a delivered form over one batch of synthetic
@@ -102,9 +102,18 @@ def time_graph_replays(fn, n: int = 30, warmup: int = 5) -> dict:
         t1.synchronize()
         ts.append(t0.elapsed_time(t1))
     q = statistics.quantiles(ts, n=4)
+    # the same n replays issued back to back between two events, as the eager
+    # step is timed: no host round trip between steps
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(n):
+        g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    b2b = t0.elapsed_time(t1) / n
     del g
     return {"median_ms": round(statistics.median(ts), 5), "iqr_ms": round(q[2] - q[0], 5), "n": n,
-            "warmup": warmup}
+            "warmup": warmup, "back_to_back_ms": round(b2b, 5)}
 
 
 def time_graph(fn, reps: int = 50) -> float:
@@ -134,7 +143,7 @@ def time_graph(fn, reps: int = 50) -> float:
     return t0.elapsed_time(t1) / (3 * reps)
 
 
-def cpu_threads() -> int:
+def _blas_threads() -> int:
     try:
         from threadpoolctl import threadpool_info
 
@@ -142,6 +151,32 @@ def cpu_threads() -> int:
         return max(n) if n else 1
     except Exception:  # pragma: no cover - threadpoolctl missing
         return 1
+
+
+def cpu_threads() -> int:
+    """Threads a BLAS-backed numpy baseline can use: the BLAS pool, capped by
+    the CPUs this process may run on."""
+    return max(1, min(_blas_threads(), len(os.sched_getaffinity(0))))
+
+
+def host_provenance() -> dict:
+    """What the CPU baseline ran on: CPU model, the CPUs this process may
+    use, the BLAS pool, and the library versions."""
+    import numpy
+    import torch
+
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:  # pragma: no cover
+        pass
+    return {"cpu_model": model, "affinity_cpus": len(os.sched_getaffinity(0)), "os_cpu_count": os.cpu_count(),
+            "blas_threads": _blas_threads(), "torch": torch.__version__, "numpy": numpy.__version__,
+            "python": sys.version.split()[0]}
 
 
 def time_cpu(fn, budget_s: float, min_reps: int = 2) -> tuple[float, int, object]:
@@ -689,8 +724,36 @@ class CopyStream(Form):
     dominant = step
 
 
+class ReadStream(Form):
+    """Read-only HBM stream over 2 GiB (``catopt_hip_hbm_read``): the
+    achievable read rate, the ceiling for the read-dominated scans (C5 reads
+    94% of its bytes), beside the copy's read + write figure."""
+
+    name, dtype, unit, bound = "read", "u32", "GB/s", "hbm"
+    NBYTES = 2 << 30
+    workload = "read-only stream over 2 GiB (catopt_hip_hbm_read), every byte read once"
+    peak = PEAK["hbm_gbs"]
+    work = dom_work = float(NBYTES)
+    dom_name = "hbm_read_kernel"
+    dom_key = "hbm_read_kernel (2 GiB)"
+
+    def setup(self, dev):
+        import torch
+
+        from catopt_amd import kernels as K
+
+        self.K = K
+        self.src = torch.ones(self.NBYTES // 4, dtype=torch.float32, device=dev)
+        self.sink = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def step(self):
+        self.K.hbm_read(self.src, self.sink)
+
+    dominant = step
+
+
 FORMS = {f.name: f for f in (C1WeightChain, C2SwiGLU, C3Attention, C4Retention, C5SSM, DenseScan,
-                                OmdScanAttention, CopyStream)}
+                                OmdScanAttention, CopyStream, ReadStream)}
 HEADLINE = "c2"
 
 
@@ -748,6 +811,8 @@ def measure(form: Form, dev, steps: int, warmup: int, cpu_budget: float | None) 
             rec["cpu_baseline"] = form.cpu(cpu_budget)
         except MemoryError as exc:  # pragma: no cover
             rec["cpu_baseline"] = {"error": str(exc)}
+        if rec["cpu_baseline"] is not None:
+            rec["cpu_baseline"]["host"] = host_provenance()
     form.free()
     torch.cuda.empty_cache()
     return rec
@@ -758,7 +823,7 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--forms", default="c1,c2,c3,c4,c5,aff,omd,copy")
+    ap.add_argument("--forms", default="c1,c2,c3,c4,c5,aff,omd,copy,read")
     ap.add_argument("--cpu-budget", type=float, default=10.0,
                     help="seconds of CPU oracle work for the headline form (others get a third)")
     ap.add_argument("--no-cpu", action="store_true")

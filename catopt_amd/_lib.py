@@ -52,6 +52,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "catopt_hip_decay": (_i32, [_i64, _i64, _p, _p, _p]),
     "catopt_hip_decay_vec": (_i32, [_i64, _i64, _i64, _i64, _p, _p, _p]),
+    "catopt_hip_hbm_read": (_i32, [_p, _i64, _p, _p]),
     "catopt_hip_scan_workspace_bytes": (_i64, [_i64, _i64]),
     "catopt_hip_affd_scan_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32]),
     "catopt_hip_ssm_scan_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i32]),

@@ -128,6 +128,27 @@ __global__ __launch_bounds__(kThreads) void om_rows_kernel(int64_t rows, int64_t
   }
 }
 
+// Read-only HBM stream: every 16-byte word of src is read once (four
+// nontemporal loads in flight per lane) and folded into an XOR that is
+// stored only if it equals a sentinel, so the loads stay live while the
+// kernel writes (almost) nothing.
+__global__ __launch_bounds__(kThreads) void hbm_read_kernel(const u32x4* __restrict__ src, int64_t n16,
+                                                            uint32_t* __restrict__ sink) {
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const u32x4 a = __builtin_nontemporal_load(src + i);
+    const u32x4 b = __builtin_nontemporal_load(src + i + stride);
+    const u32x4 c = __builtin_nontemporal_load(src + i + 2 * stride);
+    const u32x4 d = __builtin_nontemporal_load(src + i + 3 * stride);
+    acc ^= a ^ b ^ c ^ d;
+  }
+  for (; i < n16; i += stride) acc ^= __builtin_nontemporal_load(src + i);
+  const uint32_t x = acc.x ^ acc.y ^ acc.z ^ acc.w;
+  if (x == 0x9e3779b9u) sink[0] = x;
+}
+
 // decay(γ, t)[h, i, j] = γ_h^(i-j) (i >= j) else 0
 __global__ __launch_bounds__(kThreads) void decay_kernel(int64_t H, int64_t t,
                                                          const float* __restrict__ gamma,
@@ -224,6 +245,19 @@ extern "C" int32_t catopt_hip_decay_vec(int64_t H, int64_t t, int64_t offset, in
   if (!gamma || !out) return CATOPT_E_INVAL;
   decay_vec_kernel<<<grid_for(H * t), kThreads, 0, static_cast<hipStream_t>(stream)>>>(
       H, t, offset, sign, gamma, out);
+  CATOPT_LAUNCH_CHECK();
+  return CATOPT_OK;
+}
+
+extern "C" int32_t catopt_hip_hbm_read(const void* src, int64_t nbytes, uint32_t* sink, void* stream) {
+  if (nbytes < 0 || (nbytes & 15)) return CATOPT_E_INVAL;
+  if (nbytes == 0) return CATOPT_OK;
+  if (!src || !sink || !aligned16(src)) return CATOPT_E_INVAL;
+  const int64_t n16 = nbytes / 16;
+  int64_t blocks = (n16 + kThreads - 1) / kThreads;
+  if (blocks > 4096) blocks = 4096;  // 16 workgroups per CU, each lane several words
+  hbm_read_kernel<<<dim3((uint32_t)blocks), kThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const u32x4*>(src), n16, sink);
   CATOPT_LAUNCH_CHECK();
   return CATOPT_OK;
 }

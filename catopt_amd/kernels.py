@@ -624,3 +624,15 @@ def silu_mul(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
     L.check("catopt_hip_silu_mul",
             lib.catopt_hip_silu_mul(_dtype_code(gc), gc.numel(), _ptr(gc), _ptr(uc), _ptr(y), _stream(g)))
     return y
+
+
+def hbm_read(buf: torch.Tensor, sink: torch.Tensor) -> None:
+    """Read every byte of a contiguous device buffer once (the read-only HBM
+    stream; ``sink`` is a 4-byte device scratch)."""
+    _need_device(buf, sink)
+    lib = L.load()
+    if not buf.is_contiguous() or sink.numel() * sink.element_size() < 4:
+        raise ValueError("hbm_read takes a contiguous buffer and a 4-byte sink")
+    nbytes = buf.numel() * buf.element_size()
+    st = lib.catopt_hip_hbm_read(_ptr(buf), nbytes - nbytes % 16, _ptr(sink), _stream(buf))
+    L.check("catopt_hip_hbm_read", st)

@@ -224,6 +224,16 @@ int32_t catopt_hip_decay_vec(int64_t H, int64_t t, int64_t offset,
                              int64_t sign, const float* gamma, float* out,
                              void* stream);
 
+/*
+ * Read-only HBM stream over nbytes (a multiple of 16) of a 16-byte aligned
+ * buffer: every byte is read once and nothing is written (sink, 4 bytes,
+ * is stored only for one sentinel value of the data's XOR).  A measurement
+ * kernel with no counterpart in the reference: the achievable read rate
+ * against which the read-dominated scans are placed.
+ */
+int32_t catopt_hip_hbm_read(const void* src, int64_t nbytes, uint32_t* sink,
+                            void* stream);
+
 /* scan schedules (catopt_hip_affd_scan, catopt_hip_ssm_scan) */
 enum catopt_scan_schedule {
   CATOPT_SCAN_AUTO = 0,       /* streaming when the lanes fill the GPU, else chunk-parallel */
