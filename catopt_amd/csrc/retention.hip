@@ -26,9 +26,14 @@
 //                                         B = P straight from the sᵀ accumulator
 //   wave w owns state rows dk = 32w..32w+31:
 //     S = γ^C S + Kᵀ (γ^(C-c) V)          A = k via the transposing LDS read,
-//                                         B = decayed v, likewise; the workgroup
-//                                         decays the v slice once per chunk
+//                                         B = v likewise, each lane decaying
+//                                         its own elements in registers
 //   o[q] = X(0, qb) + X(1, qb), the pair meeting in LDS.
+// One barrier per chunk: the state update reads no shared decayed copy of v,
+// the S fragments and the pair exchange alternate between two LDS buffers by
+// chunk parity, and waves (0, qb) store chunk i's output at the start of
+// chunk i + 1, once the partner's half is in place.  Within a wave the
+// chains X, sᵀ and S are independent, and their MFMAs are interleaved.
 // An MFMA's k index is only a summation order: products over keys take their
 // keys in the sᵀ accumulator's row order 8(r/4) + 4g + r%4 (so P feeds an
 // MFMA without a shuffle), products over dk take dims in natural order, and
@@ -62,10 +67,11 @@ constexpr int STAGE = 2 * KQ_BYTES + V_BYTES;
 #define CATOPT_RET_STAGES 3
 #endif
 constexpr int NSTAGE = CATOPT_RET_STAGES;
-constexpr int OFF_SF = NSTAGE * STAGE;            // S fragments [4 waves][2][64 lanes] x 16 B
-constexpr int OFF_X = OFF_SF + 4 * 2 * 64 * 16;   // pair exchange [2 qb][4][64 lanes] x 16 B
-constexpr int OFF_VD = OFF_X + 2 * 4 * 64 * 16;   // decayed v slice γ^(C-c) v_c, [64][32] bf16
-constexpr int LDS_BYTES = OFF_VD + V_BYTES;
+constexpr int SF_BYTES = 4 * 2 * 64 * 16;          // S fragments [4 waves][2][64 lanes] x 16 B
+constexpr int X_BYTES = 2 * 4 * 64 * 16;           // pair exchange [2 qb][4][64 lanes] x 16 B
+constexpr int OFF_SF = NSTAGE * STAGE;             // two S fragment buffers (chunk parity)
+constexpr int OFF_X = OFF_SF + 2 * SF_BYTES;       // two exchange buffers (chunk parity)
+constexpr int LDS_BYTES = OFF_X + 2 * X_BYTES;
 static_assert(NSTAGE >= 2 && LDS_BYTES <= 160 * 1024, "LDS ring does not fit");
 constexpr int LOADS_PER_CHUNK = 9;  // global->LDS instructions per thread per chunk
 
@@ -134,8 +140,6 @@ __global__ __launch_bounds__(NT, 1) void retention_scan(
     const int key = 32 * kb + acc_row(r, g);
     dec[r] = key <= qrow ? scale * __builtin_amdgcn_exp2f((float)(qrow - key) * lg) : 0.f;
   }
-  // γ^(C - key) of the v row this thread decays (row tid / 4)
-  const float vdec = __builtin_amdgcn_exp2f((float)(CH - (tid >> 2)) * lg);
 
   // load slots: k and q 4 x 16 B each, v one 16-byte slot
   int kq_goff[4];
@@ -159,16 +163,36 @@ __global__ __launch_bounds__(NT, 1) void retention_scan(
     dma16(v + t0 + v_goff, sb + 2 * KQ_BYTES);
   };
 
+  // transposed k rows dk = 32w + 16(G&1) + 4(jj&3) .. for the state update,
+  // and transposed v rows dv = 16(G&1) + 4(jj&3) .. (byte offset dvb), both
+  // at keys 16u + 4(G>>1) + (0..3, +8)
+  const int dk_t = 32 * wave + 16 * (G & 1) + 4 * (jj & 3);
+  const int dvb = (16 * (G & 1) + 4 * (jj & 3)) * 2;
+  // γ^(C - key) of this lane's transposed-v elements for u = 3 (keys
+  // 48 + 4(G>>1) + e, e = 0..3, 8..11); the factors of block u are those of
+  // block u + 1 times γ^16, so every exponent stays >= 0
+  float vf3[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int key = 48 + 4 * (G >> 1) + (e < 4 ? e : e + 4);
+    vf3[e] = __builtin_amdgcn_exp2f((float)(CH - key) * lg);
+  }
+  const float g16 = __builtin_amdgcn_exp2f(16.f * lg);
+
   f32x16 S;  // state rows dk = 32 * wave + acc_row(r, g), column dv = l32 of the slice
 #pragma unroll
   for (int r = 0; r < 16; ++r) S[r] = 0.f;
-  // S fragments in LDS, natural dk order: entry (w, r4, dv) holds bf16
-  // S[32w + 8 r4 + (0..7)][dv]; the owner lane (dv, g) writes its half
-  // S[32w + 8 r4 + 4g + (0..3)] = its accumulator registers 4 r4 .. 4 r4 + 3.
-  char* sf_own = lds + OFF_SF + (wave * 128 + l32) * 16 + g * 8;  // + r4 * 512
-  char* xch = lds + OFF_X + qb * 4096 + lane * 16;
+  // S fragments in LDS (two buffers, chunk parity), natural dk order: entry
+  // (w, r4, dv) holds bf16 S[32w + 8 r4 + (0..7)][dv]; the owner lane (dv, g)
+  // writes its half S[32w + 8 r4 + 4g + (0..3)] = its accumulator registers
+  // 4 r4 .. 4 r4 + 3.
+  const int sf_own = OFF_SF + (wave * 128 + l32) * 16 + g * 8;  // + par * SF_BYTES + r4 * 512
+  const int xch = OFF_X + qb * 4096 + lane * 16;                // + par * X_BYTES + r4 * 1024
 #pragma unroll
-  for (int r4 = 0; r4 < 4; ++r4) *reinterpret_cast<u32x2*>(sf_own + r4 * 512) = u32x2{0, 0};
+  for (int r4 = 0; r4 < 4; ++r4) *reinterpret_cast<u32x2*>(lds + sf_own + r4 * 512) = u32x2{0, 0};
+  f32x16 Xo;  // waves kb = 0: their X of the previous chunk, stored once the partner's arrives
+#pragma unroll
+  for (int r = 0; r < 16; ++r) Xo[r] = 0.f;
 
   // Prologue: chunks 0 .. NSTAGE-2 in flight.  Every thread issues exactly
   // LOADS_PER_CHUNK loads per chunk slot (a slot past the end re-reads the
@@ -179,149 +203,146 @@ __global__ __launch_bounds__(NT, 1) void retention_scan(
   wait_vm_lgkm0<LOADS_PER_CHUNK * (NSTAGE - 2)>();
   __syncthreads();
 
-  // one chunk; its stage is a compile-time constant (the loop below runs
-  // the chunks NSTAGE at a time), so LDS addresses fold to immediates
-  auto chunk = [&](int ci, auto stage_tag) {
+  // o rows of chunk cj for waves kb = 0: own X plus the partner's, read from
+  // the exchange buffer of cj's parity
+  auto store_out = [&](int cj, const f32x4* y) {
+    uint16_t* orow = o + ((int64_t)cj * CH + qrow) * HD + sl * SL + 4 * g;
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4)
+      *reinterpret_cast<u32x2*>(orow + 8 * r4) =
+          u32x2{pack_bf16x2(Xo[4 * r4] + y[r4][0], Xo[4 * r4 + 1] + y[r4][1]),
+                pack_bf16x2(Xo[4 * r4 + 2] + y[r4][2], Xo[4 * r4 + 3] + y[r4][3])};
+  };
+
+  // One chunk, one barrier: the state update needs no decayed copy of v in
+  // LDS (each lane decays its own transposed v elements), the S fragments and
+  // the pair exchange alternate between two buffers by chunk parity, and the
+  // waves kb = 0 finish chunk ci's output at the start of chunk ci + 1.  The
+  // three MFMA chains of a chunk (X, sᵀ, S) are independent and
+  // interleaved.  Stage and wave role are compile-time constants.
+  auto chunk = [&](int ci, auto stage_tag, auto kb_tag, auto diag_tag) {
     constexpr int cur = decltype(stage_tag)::value;
+    constexpr int KB = decltype(kb_tag)::value;
+    constexpr bool DIAG = decltype(diag_tag)::value;
     {
-      const int ahead = ci + NSTAGE - 1;
       constexpr int st = cur == 0 ? NSTAGE - 1 : cur - 1;  // the stage chunk ci - 1 used
-      issue(min(ahead, nchunks - 1), st);
+      issue(min(ci + NSTAGE - 1, nchunks - 1), st);
     }
     const char* Ks = lds + cur * STAGE;
     const char* Qs = Ks + KQ_BYTES;
     const char* Vs = Qs + KQ_BYTES;
+    const int par = ci & 1;
 
-    // Reads are issued in batches ahead of the MFMAs that consume them; the
-    // scheduling fences keep the compiler from pairing each MFMA with the reads
-    // right before it, which would expose the LDS latency once per MFMA.
-
-    // ---- batch 1: this thread's piece of v to decay (row tid/4), the S
-    // fragments of dk blocks 2kb, 2kb+1 and the q dims they meet,
-    // 16 (4kb + i) + 8g + e (natural order)
-    const u32x4 vw = *reinterpret_cast<const u32x4*>(Vs + tid * 16);
-    bf16x8 sf[4], qc[4];
+    // ---- batch: S fragments of dk blocks 2KB, 2KB+1 (this parity), q rows,
+    // k rows (diagonal block), transposed k and v, the partner's X of ci-1
+    bf16x8 sf[4], qf[8], kf[8], kt[4], vr[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 4; ++i)
       sf[i] = *reinterpret_cast<const bf16x8*>(
-          lds + OFF_SF + (((2 * kb + (i >> 1)) * 4 + 2 * (i & 1) + g) * 32 + l32) * 16);
-      qc[i] = *reinterpret_cast<const bf16x8*>(Qs + kq_off(qrow, 2 * (4 * kb + i) + g));
+          lds + OFF_SF + par * SF_BYTES + (((2 * KB + (i >> 1)) * 4 + 2 * (i & 1) + g) * 32 + l32) * 16);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (DIAG || (j >= 4 * KB && j < 4 * KB + 4))
+        qf[j] = *reinterpret_cast<const bf16x8*>(Qs + kq_off(qrow, 2 * j + g));
+      if (DIAG) kf[j] = *reinterpret_cast<const bf16x8*>(Ks + kq_off(32 * KB + l32, 2 * j + g));
     }
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---- X = q S over dk half kb (scaled by scale γ^q below)
-    f32x16 X;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) X[r] = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) X = mfma32x32x16(sf[i], qc[i], X);
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---- decayed v for the state update (VALU work beside the MFMAs)
-    {
-      u32x4 d;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        d[e] = pack_bf16x2(__uint_as_float(vw[e] << 16) * vdec,
-                           __uint_as_float(vw[e] & 0xffff0000u) * vdec);
-      *reinterpret_cast<u32x4*>(lds + OFF_VD + tid * 16) = d;
-    }
-    // transposed k rows dk = 32w + l32 for the state update, keys 16u + 4g + (0..3, +8)
-    bf16x8 kt[4];
-    const int dk = 32 * wave + 16 * (G & 1) + 4 * (jj & 3);
-    const int dvb = (16 * (G & 1) + 4 * (jj & 3)) * 2;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int key0 = 16 * u + 4 * (G >> 1) + (jj >> 2);
-      kt[u] = cat8(ds_read_tr(Ks + kq_off(key0, dk >> 3) + (dk & 7) * 2),
-                   ds_read_tr(Ks + kq_off(key0 + 8, dk >> 3) + (dk & 7) * 2));
+      kt[u] = cat8(ds_read_tr(Ks + kq_off(key0, dk_t >> 3) + (dk_t & 7) * 2),
+                   ds_read_tr(Ks + kq_off(key0 + 8, dk_t >> 3) + (dk_t & 7) * 2));
+      vr[u] = cat8(ds_read_tr(Vs + key0 * (SL * 2) + dvb), ds_read_tr(Vs + (key0 + 8) * (SL * 2) + dvb));
     }
+    f32x4 y[4];
+    if (KB == 0) {
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        y[r4] = *reinterpret_cast<const f32x4*>(lds + xch + (1 - par) * X_BYTES + r4 * 1024);
+    }
+    __builtin_amdgcn_sched_barrier(0);
 
-    // ---- diagonal block: sᵀ (keys 32kb.., queries 32qb..), decayed, times v
-    if (kb <= qb) {
-      bf16x8 kf[8], qf[8], vi[2];
+    // ---- interleaved MFMA chains: X = q S (dk half KB), sᵀ = K Qᵀ,
+    // S = γ^C S + Kᵀ (γ^(C-c) V)
+    f32x16 X, sa;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        kf[j] = *reinterpret_cast<const bf16x8*>(Ks + kq_off(32 * kb + l32, 2 * j + g));
-        qf[j] = *reinterpret_cast<const bf16x8*>(Qs + kq_off(qrow, 2 * j + g));
-      }
+    for (int r = 0; r < 16; ++r) {
+      X[r] = 0.f;
+      sa[r] = 0.f;
+      S[r] *= gC;
+    }
+    float vf[8];
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {  // vᵀ rows dv = l32, keys 32kb + 16u + 4g + (0..3, +8)
-        const int key0 = 32 * kb + 16 * u + 4 * (G >> 1) + (jj >> 2);
-        vi[u] = cat8(ds_read_tr(Vs + key0 * (SL * 2) + dvb), ds_read_tr(Vs + (key0 + 8) * (SL * 2) + dvb));
-      }
-      __builtin_amdgcn_sched_barrier(0);
+    for (int e = 0; e < 8; ++e) vf[e] = vf3[e];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) X[r] *= gq;
-      f32x16 acc;
+    for (int t = 0; t < 4; ++t) {
+      const int u = 3 - t;  // decay factors run from block 3 down
+      X = mfma32x32x16(sf[t], qf[4 * KB + t], X);
+      if (DIAG) sa = mfma32x32x16(kf[2 * t], qf[2 * t], sa);
+      // element e of vr[u] is bf16 half (e & 1) of word e / 2
+      const u32x4 w = __builtin_bit_cast(u32x4, vr[u]);
+      u32x4 vd;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+      for (int e2 = 0; e2 < 4; ++e2)
+        vd[e2] = pack_bf16x2(__uint_as_float(w[e2] << 16) * vf[2 * e2],
+                             __uint_as_float(w[e2] & 0xffff0000u) * vf[2 * e2 + 1]);
 #pragma unroll
-      for (int j = 0; j < HD / 16; ++j) acc = mfma32x32x16(kf[j], qf[j], acc);
+      for (int e = 0; e < 8; ++e) vf[e] *= g16;
+      S = mfma32x32x16(kt[u], __builtin_bit_cast(bf16x8, vd), S);
+      if (DIAG) sa = mfma32x32x16(kf[2 * t + 1], qf[2 * t + 1], sa);
+    }
+    if (KB == 0 && ci > 0) store_out(ci - 1, y);
+
+    // ---- X *= scale γ^q; the diagonal block's decayed scores times v
+#pragma unroll
+    for (int r = 0; r < 16; ++r) X[r] *= gq;
+    if (DIAG) {
       bf16x8 pf[2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) pf[r >> 3][r & 7] = static_cast<__bf16>(acc[r] * dec[r]);
-      X = mfma32x32x16(vi[0], pf[0], X);
-      X = mfma32x32x16(vi[1], pf[1], X);
-    } else {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) X[r] *= gq;
+      for (int r = 0; r < 16; ++r) pf[r >> 3][r & 7] = static_cast<__bf16>(sa[r] * dec[r]);
+      X = mfma32x32x16(vr[2 * KB], pf[0], X);
+      X = mfma32x32x16(vr[2 * KB + 1], pf[1], X);
     }
 
-    // ---- pair reduction: waves (1, qb) hand X to waves (0, qb)
-    if (kb == 1) {
+    // ---- publish: the partner's half of X, and S_{ci+1} for the next chunk
+    if (KB == 1) {
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4)
-        *reinterpret_cast<f32x4*>(xch + r4 * 1024) =
+        *reinterpret_cast<f32x4*>(lds + xch + par * X_BYTES + r4 * 1024) =
             f32x4{X[4 * r4], X[4 * r4 + 1], X[4 * r4 + 2], X[4 * r4 + 3]};
-    }
-    __syncthreads();  // exchange and decayed v written; all S fragments read
-
-    // ---- state update for rows dk = 32 * wave ..: S = γ^C S + kᵀ (decayed v)
-    bf16x8 vd[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int key0 = 16 * u + 4 * (G >> 1) + (jj >> 2);
-      const char* pv = lds + OFF_VD + key0 * (SL * 2) + dvb;
-      vd[u] = cat8(ds_read_tr(pv), ds_read_tr(pv + 8 * SL * 2));
-    }
-    f32x4 y[4];  // partner's X (waves kb = 0)
-    if (kb == 0) {
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) y[r4] = *reinterpret_cast<const f32x4*>(xch + r4 * 1024);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) S[r] *= gC;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) S = mfma32x32x16(kt[u], vd[u], S);
-    u32x2 ow[4];
-    if (kb == 0) {
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4)
-        ow[r4] = u32x2{pack_bf16x2(X[4 * r4] + y[r4][0], X[4 * r4 + 1] + y[r4][1]),
-                       pack_bf16x2(X[4 * r4 + 2] + y[r4][2], X[4 * r4 + 3] + y[r4][3])};
+    } else {
+      Xo = X;
     }
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4)
-      *reinterpret_cast<u32x2*>(sf_own + r4 * 512) =
+      *reinterpret_cast<u32x2*>(lds + sf_own + (1 - par) * SF_BYTES + r4 * 512) =
           u32x2{pack_bf16x2(S[4 * r4], S[4 * r4 + 1]), pack_bf16x2(S[4 * r4 + 2], S[4 * r4 + 3])};
     // loads complete in issue order: all but the newest NSTAGE-2 groups means
     // chunk ci+1's tiles have landed (earlier stores were issued before them)
     wait_vm_lgkm0<LOADS_PER_CHUNK * (NSTAGE - 2)>();
-    __syncthreads();  // next chunk's tiles and S fragments in place; exchange, decayed v free
-    if (kb == 0) {
-      // o[ci*C + qrow][sl*32 + 8 r4 + 4g .. +3]
-      uint16_t* orow = o + ((int64_t)ci * CH + qrow) * HD + sl * SL + 4 * g;
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) *reinterpret_cast<u32x2*>(orow + 8 * r4) = ow[r4];
+    __syncthreads();  // next chunk's tiles, S fragments and this chunk's exchange in place
+  };
+  auto run = [&](auto kb_tag, auto diag_tag) {
+    static_assert(NSTAGE == 3, "the chunk loop below runs three stages");
+    for (int ci = 0; ci < nchunks; ci += 3) {
+      chunk(ci, std::integral_constant<int, 0>{}, kb_tag, diag_tag);
+      if (ci + 1 < nchunks) chunk(ci + 1, std::integral_constant<int, 1>{}, kb_tag, diag_tag);
+      if (ci + 2 < nchunks) chunk(ci + 2, std::integral_constant<int, 2>{}, kb_tag, diag_tag);
     }
   };
-  static_assert(NSTAGE == 3, "the chunk loop below runs three stages");
-  for (int ci = 0; ci < nchunks; ci += 3) {
-    chunk(ci, std::integral_constant<int, 0>{});
-    if (ci + 1 < nchunks) chunk(ci + 1, std::integral_constant<int, 1>{});
-    if (ci + 2 < nchunks) chunk(ci + 2, std::integral_constant<int, 2>{});
+  // wave roles (kb, qb): (0, *) and (1, 1) take a diagonal block, (1, 0) none
+  if (kb == 0)
+    run(std::integral_constant<int, 0>{}, std::true_type{});
+  else if (qb == 1)
+    run(std::integral_constant<int, 1>{}, std::true_type{});
+  else
+    run(std::integral_constant<int, 1>{}, std::false_type{});
+  // the last chunk's output: its exchange is in place after the final barrier
+  if (kb == 0) {
+    f32x4 y[4];
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4)
+      y[r4] = *reinterpret_cast<const f32x4*>(lds + xch + ((nchunks - 1) & 1) * X_BYTES + r4 * 1024);
+    store_out(nchunks - 1, y);
   }
 }
 

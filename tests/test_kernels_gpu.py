@@ -217,7 +217,9 @@ def _gammas(H):
     return np.array([1 - 2.0 ** (-5 - h / 2) for h in range(H)], dtype=np.float32)
 
 
-@pytest.mark.parametrize("B,H,T", [(1, 2, 512), (2, 3, 1024), (1, 1, 64)])
+# (1, 2, 128): two one-chunk segments; (5, 16, 256): more (head, slice) work
+# items than CUs, so one segment per head
+@pytest.mark.parametrize("B,H,T", [(1, 2, 512), (2, 3, 1024), (1, 1, 64), (1, 2, 128), (5, 16, 256)])
 def test_retention_vs_kway_form(dev, B, H, T):
     scale = 1.0
     q = _rand((B, H, T, 128), torch.bfloat16, 100, 1 / math.sqrt(128))
