@@ -36,6 +36,9 @@ __all__ = [
     "postorder",
     "term_to_data",
     "term_from_data",
+    "metavariables",
+    "ir_from_record",
+    "record_from_ir",
 ]
 
 
@@ -226,9 +229,14 @@ def iter_leaves(root: Any) -> Iterator:
 
 
 # ------------------------------------------------------------- wire format
-# JSON-safe encoding of terms, the scheme of ir.py:366-445 (term_to_data /
-# term_from_data): {"var"|"param": name, "shape": [...]}, {"const": v},
-# {"op": name, "args": [...], "attrs": {...}}, tuples as {"__tuple__": [...]}.
+# JSON-safe encoding of terms, the scheme of catopt_core/ir.py:366-445
+# (term_to_data / term_from_data), kept alike so terms written by catopt's
+# own tools (rule caches, lemma certificates, the intake census) load here:
+#   {"mvar": name}                       a pattern metavariable (a bare str leaf)
+#   {"const": v}                          Const, v raw (json writes ±inf as ±Infinity)
+#   {"var" | "param": name, "shape": [..]} typed leaves
+#   {"op": name, "args": [...], "attrs": {k: attr}}
+# with tuple / list attrs as {"__tuple__": [...]} / {"__list__": [...]}.
 
 
 def _attr_to_data(v: Any) -> Any:
@@ -236,10 +244,6 @@ def _attr_to_data(v: Any) -> Any:
         return {"__tuple__": [_attr_to_data(x) for x in v]}
     if isinstance(v, list):
         return {"__list__": [_attr_to_data(x) for x in v]}
-    if isinstance(v, float) and v != v:
-        return {"__float__": "nan"}
-    if isinstance(v, float) and v in (float("inf"), float("-inf")):
-        return {"__float__": "inf" if v > 0 else "-inf"}
     if isinstance(v, (str, int, float, bool)) or v is None:
         return v
     raise TypeError(f"unserializable attribute value: {v!r}")
@@ -251,16 +255,16 @@ def _attr_from_data(v: Any) -> Any:
             return tuple(_attr_from_data(x) for x in v["__tuple__"])
         if "__list__" in v:
             return [_attr_from_data(x) for x in v["__list__"]]
-        if "__float__" in v:
-            return float(v["__float__"])
         raise ValueError(f"bad attr encoding: {v!r}")
     return v
 
 
 def term_to_data(t: Any) -> Any:
     """Encode a term as JSON-safe data (DAG sharing is not preserved)."""
+    if isinstance(t, str):
+        return {"mvar": t}
     if isinstance(t, Const):
-        return {"const": _attr_to_data(t.value)}
+        return {"const": t.value}
     if isinstance(t, Var):
         return {"var": t.name, "shape": list(t.typ.shape)}
     if isinstance(t, Param):
@@ -275,11 +279,14 @@ def term_to_data(t: Any) -> Any:
 
 
 def term_from_data(d: Any) -> Any:
-    """Decode :func:`term_to_data` output (interning shared subterms again)."""
+    """Decode :func:`term_to_data` output (interning shared subterms again).
+    A metavariable decodes to its bare name, as a pattern leaf."""
     if not isinstance(d, dict) or not d:
         raise ValueError(f"bad term encoding: {d!r}")
+    if "mvar" in d:
+        return d["mvar"]
     if "const" in d:
-        return Const(_attr_from_data(d["const"]))
+        return Const(d["const"])
     if "var" in d:
         return Var(d["var"], TensorType(tuple(d["shape"])))
     if "param" in d:
@@ -288,3 +295,41 @@ def term_from_data(d: Any) -> Any:
         return Op.make(d["op"], *[term_from_data(a) for a in d["args"]],
                        **{k: _attr_from_data(v) for k, v in d.get("attrs", {}).items()})
     raise ValueError(f"bad term encoding: {d!r}")
+
+
+def metavariables(t: Any) -> list:
+    """Names of the pattern metavariables (bare str leaves) under ``t``."""
+    if isinstance(t, str):
+        return [t]
+    found: list = []
+    seen: set = set()
+    for n in postorder(t):
+        for a in n.args:
+            if isinstance(a, str) and a not in seen:
+                seen.add(a)
+                found.append(a)
+    return found
+
+
+def ir_from_record(rec: dict) -> IR:
+    """The program of one term record ``{"term": ..., "inputs": [{"name",
+    "shape"}, ...]}`` (the intake census layout, ``intake/ledger.py:127-138``).
+    A term holding pattern metavariables is a law's side, not a program:
+    it is rejected with the names it holds."""
+    term = term_from_data(rec["term"])
+    mv = metavariables(term)
+    if mv:
+        raise ValueError(f"term {rec.get('name', '?')!r} holds pattern metavariables {mv}: "
+                         "a rewrite pattern cannot be lowered")
+    inputs = [Var(i["name"], TensorType(tuple(i["shape"]))) for i in rec.get("inputs", [])]
+    return IR(term, inputs)
+
+
+def record_from_ir(name: str, ir: IR) -> dict:
+    """The term record of a program (the layout :func:`ir_from_record` reads)."""
+    return {
+        "name": name,
+        "ops": sorted({n.op for n in postorder(ir.root)}),
+        "term": term_to_data(ir.root),
+        "inputs": [{"name": v.name, "shape": list(v.typ.shape)} for v in ir.inputs],
+    }
