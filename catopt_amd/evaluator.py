@@ -47,7 +47,7 @@ from torch import nn
 from . import _lib as L
 from . import kernels as K
 from .bindings import HipOpTable, attr_of, scalar_value
-from .graphs import record_graph, signature
+from .graphs import global_module_hooks, record_graph, signature
 from .ir import IR, Const, Op, Param, TensorType, Var, is_op, postorder
 
 __all__ = ["HipIRModule", "FOLD_OPS", "eval_term"]
@@ -61,6 +61,38 @@ FOLD_OPS = frozenset({
     "transpose", "permute", "reshape", "view", "unsqueeze", "squeeze", "flatten", "tril",
     "contiguous", "to", "alias", "clone", "dropout", "logical_not", "eq", "ne", "where",
 })
+
+class _BufferParams:
+    """Param name -> the module buffer holding its value, read at lookup
+    (no per-call copy of the map)."""
+
+    __slots__ = ("_bufs", "_names")
+
+    def __init__(self, bufs: dict, names: dict) -> None:
+        self._bufs, self._names = bufs, names
+
+    def __getitem__(self, name: str) -> torch.Tensor:
+        return self._bufs[self._names[name]]
+
+    def __contains__(self, name: object) -> bool:
+        return name in self._names
+
+    def get(self, name: str, default: Any = None) -> Any:
+        attr = self._names.get(name)
+        return default if attr is None else self._bufs[attr]
+
+    def keys(self):
+        return self._names.keys()
+
+    def items(self):
+        return ((n, self._bufs[a]) for n, a in self._names.items())
+
+    def __iter__(self):
+        return iter(self._names)
+
+    def __len__(self) -> int:
+        return len(self._names)
+
 
 def _is_param(t: Any) -> bool:
     return isinstance(t, Param) or (not is_op(t) and hasattr(t, "name") and type(t).__name__ == "Param")
@@ -170,6 +202,15 @@ class HipIRModule(nn.Module):
         self._root = root
         self._prune()
         self._tape = _Tape(root)
+        self._graph = None  # set by capture_cuda_graph (a plain attribute: forward reads it per call)
+
+    def __call__(self, *xs: Any) -> Any:
+        # nn.Module's call path (hook dispatch) costs microseconds per call,
+        # the same order as the small kernels a step launches; without hooks
+        # it only calls forward
+        if self._forward_hooks or self._forward_pre_hooks or global_module_hooks():
+            return super().__call__(*xs)
+        return self.forward(*xs)
 
     # -- parameters -------------------------------------------------------
 
@@ -182,12 +223,11 @@ class HipIRModule(nn.Module):
         self.register_buffer(attr, t, persistent=False)
 
     @property
-    def _param_map(self) -> dict:
+    def _param_map(self) -> "_BufferParams":
         # re-read per call (the reference's contract: a replaced buffer is
         # picked up), straight from the buffer dict rather than through
         # nn.Module.__getattr__, which costs microseconds per name
-        bufs = self._buffers
-        return {name: bufs[attr] for name, attr in self._buf_names.items()}
+        return _BufferParams(self._buffers, self._buf_names)
 
     def _pv(self, t: Any) -> torch.Tensor | None:
         if _is_param(t) and t.name in self._buf_names:

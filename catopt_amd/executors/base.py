@@ -22,7 +22,7 @@ from typing import Any, Callable
 
 import torch
 
-from ..graphs import record_graph, signature
+from ..graphs import global_module_hooks, record_graph, signature
 from ..ir import is_op
 
 __all__ = ["HipExecutorBase"]
@@ -74,6 +74,13 @@ class HipExecutorBase:
 
     def drop_cuda_graph(self) -> None:
         self._init_graph_state()
+
+    def __call__(self, *xs: Any) -> Any:
+        # skip nn.Module's hook dispatch when no hook is registered: it costs
+        # microseconds per call, the order of a small step's kernels
+        if self._forward_hooks or self._forward_pre_hooks or global_module_hooks():
+            return super().__call__(*xs)
+        return self.forward(*xs)
 
     def forward(self, *xs: Any) -> Any:
         if self._graph is not None and signature(xs) == self._graph_sig:

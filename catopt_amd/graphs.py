@@ -7,7 +7,7 @@ from typing import Callable
 
 import torch
 
-__all__ = ["record_graph", "signature"]
+__all__ = ["global_module_hooks", "record_graph", "signature"]
 
 
 def signature(xs: tuple) -> tuple:
@@ -33,3 +33,11 @@ def record_graph(fn: Callable, example_inputs: tuple, warmup: int = 3) -> tuple:
     with torch.cuda.graph(g):
         out = fn(*static_ins)
     return g, static_ins, out, signature(tuple(static_ins))
+
+
+def global_module_hooks() -> bool:
+    """Whether any process-wide nn.Module hook is registered (the executors
+    then take nn.Module's full call path, so the hooks run)."""
+    m = torch.nn.modules.module
+    return bool(m._global_forward_hooks or m._global_forward_pre_hooks or m._global_backward_hooks
+                or m._global_backward_pre_hooks or getattr(m, "_global_forward_hooks_always_called", None))
