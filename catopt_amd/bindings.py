@@ -275,7 +275,7 @@ def _sdpa(q, k, v, *a, **kw):
     """``scaled_dot_product_attention`` (torch_bridge.py:1225-1245: a
     positional mask, attrs ``arg3``..``arg6`` = attn_mask, dropout_p,
     is_causal, scale).  bf16 ``(…, T, d)`` operands with one leading shape,
-    ``d = dv`` in (64, 128), no dropout, a positive scale and at most one of
+    head dims up to 128, no dropout, a positive scale and at most one of
     ``is_causal`` / a mask that is one ``(Tq, Tk)`` plane shared over the
     leading axes run the fused attention kernel (a bool mask keeps, a float
     one adds; ``is_causal`` keeps ``j <= i``; a fully masked row is 0, as
@@ -307,8 +307,8 @@ def _sdpa_kernel_mask(q, k, v, mask, causal, dropout) -> dict | None:
         return None
     if not 2 <= q.dim() <= 4 or k.shape[:-2] != q.shape[:-2] or v.shape[:-2] != q.shape[:-2]:
         return None
-    d = q.shape[-1]
-    if d not in (64, 128) or k.shape[-1] != d or v.shape[-1] != d or v.shape[-2] != k.shape[-2]:
+    d, dv = q.shape[-1], v.shape[-1]
+    if max(d, dv) > K.ATTENTION_MAX_HEAD_DIM or k.shape[-1] != d or v.shape[-2] != k.shape[-2]:
         return None
     if mask is None:
         return {"causal": True, "causal_off": 0} if causal else {}

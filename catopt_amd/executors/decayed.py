@@ -243,7 +243,9 @@ def _kernel_args(q, k, v, g, p):
     ts = (q, k, v)
     if not all(isinstance(t, torch.Tensor) and t.device.type == "cuda" and t.dtype == torch.bfloat16 for t in ts):
         return None
-    if q.shape != k.shape or q.shape != v.shape or q.shape[-1] != K.RETENTION_HEAD_DIM or not 2 <= q.dim() <= 4:
+    if q.shape != k.shape or v.shape[:-1] != q.shape[:-1] or not 2 <= q.dim() <= 4:
+        return None
+    if max(q.shape[-1], v.shape[-1]) > K.RETENTION_HEAD_DIM:  # narrower heads run zero-padded
         return None
     T = q.shape[-2]
     if T % K.RETENTION_CHUNK or T != p["K"] * p["C"]:

@@ -25,9 +25,9 @@ as in the reference, and each leaf is classified once, at construction:
     keep-mask, a float one an additive bias; a weight-only bias holding only
     0 and -inf is a keep-mask.
 
-  bf16 operands with head dim 64 or 128 and a mask that is one ``(Tq, Tk)``
-  plane shared over the leading axes run one launch of the fused attention
-  kernel (scores, mask, exponentials and ``e @ v`` stay on chip; a single
+  bf16 operands with head dims up to 128 (other widths than 64 / 128
+  zero-padded) and a mask that is one ``(Tq, Tk)`` plane shared over the
+  leading axes run one launch of the fused attention kernel (scores, mask, exponentials and ``e @ v`` stay on chip; a single
   leaf is normalised in the kernel).  Unmasked fp32 operands run the fp32
   carrier kernel.  Any other call — another head dim, a per-batch mask —
   takes the score path below for that leaf.
@@ -487,8 +487,9 @@ def _in_envelope(q, k, v) -> bool:
         return False
     if any(t.dtype != torch.bfloat16 for t in ts):
         return False
-    d = q.shape[-1]
-    return d in (64, 128) and k.shape[-1] == d and v.shape[-1] == d and 2 <= q.dim() <= 4
+    d, dv = q.shape[-1], v.shape[-1]
+    return (0 < d <= K.ATTENTION_MAX_HEAD_DIM and 0 < dv <= K.ATTENTION_MAX_HEAD_DIM and k.shape[-1] == d
+            and 2 <= q.dim() <= 4)
 
 
 def _f32_envelope(q, k, v) -> bool:

@@ -15,7 +15,7 @@ Leaves:
 * ``om_elem(s, v)`` whose score parses as a positively scaled ``q kᵀ`` with
   a mask the attention kernel takes (the spellings of the batched om
   executor: ``masked_fill(…, M, -inf)``, ``add(…, attnbias(m))``, key-axis
-  ``concat`` scores) with bf16 operands and head dim 64 / 128: one launch
+  ``concat`` scores) with bf16 operands and head dims up to 128: one launch
   of the HIP attention kernel in carrier mode (scores, mask and
   exponentials stay on chip; the carrier is fp32);
 * any other ``om_elem(s, v)``: the score and value operands are evaluated and
@@ -95,7 +95,7 @@ def _carrier_qk(q, k, v, scale: float = 1.0, **mask_kw) -> tuple | None:
 
 def om_step_qk(state: tuple | None, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
     """:func:`om_step` for the canonical score ``s = q @ kᵀ`` (no scale),
-    ``om_lower.py:910-917``.  bf16 operands with head dim 64 / 128 never
+    ``om_lower.py:910-917``.  bf16 operands with head dims up to 128 never
     materialise ``s``: the attention kernel emits the block's carrier."""
     e = _carrier_qk(q, k, v, 1.0)
     if e is None:

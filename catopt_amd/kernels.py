@@ -219,6 +219,9 @@ def _bhtd(t: torch.Tensor) -> tuple[torch.Tensor, list[int]]:
     return t, [t.stride(0), t.stride(1), t.stride(2)]
 
 
+ATTENTION_MAX_HEAD_DIM = 128
+
+
 def attention(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -233,7 +236,8 @@ def attention(
     return_ml: bool = False,
     empty_rows: str = "nan",
 ):
-    """Online-softmax attention ``(B,H,T,d)`` bf16.
+    """Online-softmax attention ``(B,H,T,d)`` bf16, head dims up to 128
+    (other widths than 64 / 128 run zero-padded to the next of them).
 
     ``causal`` keeps key ``j`` for query ``i`` iff ``j <= i + causal_off``;
     ``mask`` is a bool keep-mask ``(Tq, Tk)`` shared over (B, H); ``bias``
@@ -255,8 +259,19 @@ def attention(
     if (Bk, Hk, dk) != (B, H, d) or v.shape[:3] != k.shape[:3]:
         raise ValueError(f"attention shape mismatch q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)}")
     dv = v.shape[3]
-    if d != dv or d not in (64, 128):
-        raise NotImplementedError(f"HIP attention supports d = dv in (64, 128), got {d}, {dv}")
+    if max(d, dv) > ATTENTION_MAX_HEAD_DIM or min(d, dv) < 1:
+        raise NotImplementedError(f"HIP attention supports head dims up to {ATTENTION_MAX_HEAD_DIM}, got {d}, {dv}")
+    width = 64 if max(d, dv) <= 64 else 128
+    if d != width or dv != width:
+        # the kernel's widths are 64 and 128 with d = dv: zero columns leave
+        # every score unchanged and add zero output columns, dropped below
+        q, k = (torch.nn.functional.pad(t, (0, width - d)) if d < width else t for t in (q, k))
+        v = torch.nn.functional.pad(v, (0, width - dv)) if dv < width else v
+        r = attention(q, k, v, scale, causal=causal, causal_off=causal_off, mask=mask, bias=bias,
+                      normalize=normalize, return_ml=return_ml, empty_rows=empty_rows)
+        if return_ml:
+            return r[0][..., :dv], r[1], r[2]
+        return r[..., :dv]
     q, qs = _bhtd(q)
     k, ks = _bhtd(k)
     v, vs = _bhtd(v)
@@ -351,16 +366,27 @@ RETENTION_HEAD_DIM = 128
 
 def retention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma: torch.Tensor,
               scale: float = 1.0) -> torch.Tensor:
-    """``scale * Σ_{s<=t} γ_h^(t-s) (q_t·k_s) v_s`` for ``(B,H,T,128)`` bf16."""
+    """``scale * Σ_{s<=t} γ_h^(t-s) (q_t·k_s) v_s`` for ``q, k (B,H,T,dk)``,
+    ``v (B,H,T,dv)`` bf16, ``dk, dv <= 128`` (below 128 they run zero-padded
+    to the kernel's 128: zero columns leave q·k unchanged and add zero output
+    columns, dropped)."""
     _need_device(q, k, v, gamma)
     lib = L.load()
     if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
         raise NotImplementedError("HIP retention runs on bf16 operands")
-    if q.dim() != 4 or q.shape != k.shape or q.shape != v.shape:
-        raise ValueError("retention operands must share a (B, H, T, d) shape")
+    if q.dim() != 4 or q.shape != k.shape or v.dim() != 4 or v.shape[:3] != q.shape[:3]:
+        raise ValueError("retention operands must be q, k (B, H, T, dk) and v (B, H, T, dv)")
     B, H, T, d = q.shape
-    if d != 128 or T % RETENTION_CHUNK:
-        raise NotImplementedError(f"HIP retention needs d = 128 and T % {RETENTION_CHUNK} == 0")
+    dv = v.shape[-1]
+    if max(d, dv) > RETENTION_HEAD_DIM or T % RETENTION_CHUNK:
+        raise NotImplementedError(f"HIP retention needs dk, dv <= {RETENTION_HEAD_DIM} and "
+                                  f"T % {RETENTION_CHUNK} == 0")
+    if d < RETENTION_HEAD_DIM or dv < RETENTION_HEAD_DIM:
+        pad = torch.nn.functional.pad
+        q, k = (pad(t, (0, RETENTION_HEAD_DIM - d)) if d < RETENTION_HEAD_DIM else t for t in (q, k))
+        v = pad(v, (0, RETENTION_HEAD_DIM - dv)) if dv < RETENTION_HEAD_DIM else v
+        return retention(q, k, v, gamma, scale)[..., :dv]
+    d = RETENTION_HEAD_DIM
     g = gamma.to(torch.float32).reshape(-1).contiguous()
     if g.numel() != H:
         raise ValueError("gamma must hold one rate per head")
@@ -369,7 +395,7 @@ def retention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma: torch.Te
     wsb = lib.catopt_hip_retention_workspace_bytes(B, H, T, d, RETENTION_CHUNK)
     if wsb < 0:
         raise ValueError("retention workspace query rejected the shape")
-    ws = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device=q.device)
+    ws = _workspace(wsb, q.device)
     st = lib.catopt_hip_retention_fwd(L.BF16, B, H, T, d, RETENTION_CHUNK, _ptr(q), _ptr(k),
                                       _ptr(v), _ptr(g), float(scale), _ptr(o), _ptr(ws), wsb,
                                       _stream(q))

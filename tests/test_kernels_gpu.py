@@ -183,6 +183,19 @@ def test_attention_bool_mask_nan_rows(dev):
     _gate(np.where(fin, ref, 0), np.where(fin, on, 0), TOL_BF16)
 
 
+@pytest.mark.parametrize("d,dv,causal", [(32, 32, True), (96, 96, False), (80, 48, True), (128, 72, False)])
+def test_attention_other_head_dims(dev, d, dv, causal):
+    # widths other than 64 / 128 run zero-padded to the next of them
+    B, H, T = 1, 2, 192
+    q, k = _rand((B, H, T, d), torch.bfloat16, 130), _rand((B, H, T, d), torch.bfloat16, 131)
+    v = _rand((B, H, T, dv), torch.bfloat16, 132)
+    sc = 1 / math.sqrt(d)
+    o, m, lsum = K.attention(q.to(dev), k.to(dev), v.to(dev), sc, causal=causal, return_ml=True)
+    assert o.shape == (B, H, T, dv) and m.shape == (B, H, T, 1)
+    ref = oracle.attention_om(_np(q), _np(k), _np(v), sc, causal=causal)
+    _gate(ref, o, TOL_BF16)
+
+
 def test_attention_causal_offset_and_cross_lengths(dev):
     q, k, v = _qkv(1, 2, 100, 128, 95, Tk=300)
     o = K.attention(q.to(dev), k.to(dev), v.to(dev), 0.08, causal=True, causal_off=200)
@@ -232,6 +245,20 @@ def test_retention_vs_kway_form(dev, B, H, T):
         ref = oracle.retention_kway(_np(q), _np(k), _np(v), g64, T // 64, scale)
     else:  # a single chunk is the quadratic form itself
         ref = oracle.retention_quadratic(_np(q), _np(k), _np(v), g64, scale)
+    _gate(ref, o, TOL_BF16)
+
+
+@pytest.mark.parametrize("dk,dv", [(64, 64), (96, 64), (128, 80)])
+def test_retention_narrow_heads(dev, dk, dv):
+    # head dims below 128 run zero-padded to the kernel's width
+    B, H, T = 1, 2, 256
+    q = _rand((B, H, T, dk), torch.bfloat16, 120, 1 / math.sqrt(dk))
+    k = _rand((B, H, T, dk), torch.bfloat16, 121, 1 / math.sqrt(dk))
+    v = _rand((B, H, T, dv), torch.bfloat16, 122, 1 / math.sqrt(dv))
+    gam = _gammas(H)
+    o = K.retention(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(gam).to(dev), 0.7)
+    assert o.shape == (B, H, T, dv)
+    ref = oracle.retention_quadratic(_np(q), _np(k), _np(v), gam.astype(np.float64), 0.7)
     _gate(ref, o, TOL_BF16)
 
 

@@ -254,6 +254,21 @@ def test_negative_scale_runs_the_score_path(sink, dev):
     _gate_nan(_oracle_blocks(s, _np(xs[2]), (T,)), out, TOL_F32)
 
 
+@pytest.mark.parametrize("d", [40, 96])
+def test_bf16_leaves_of_other_head_dims_run_the_attention_kernel(sink, dev, d):
+    B, H, Tq, cuts = 1, 2, 128, (64, 64)
+    ir = _sdpa_cat_ir(B, H, Tq, cuts, d, d ** -0.5, True, True)
+    q = _rand((B, H, Tq, d), 5)
+    ks = [_rand((B, H, c, d), 50 + i) for i, c in enumerate(cuts)]
+    vs = [_rand((B, H, c, d), 60 + i) for i, c in enumerate(cuts)]
+    out = _deliver(sink, ir, {}, [t.to(dev) for t in (q, *ks, *vs)], 2)
+    K_ = np.concatenate([_np(k) for k in ks], -2)
+    V = np.concatenate([_np(v) for v in vs], -2)
+    scq = float(torch.tensor(d ** -0.5, dtype=torch.bfloat16))
+    s = np.where(oracle.cmask_keep(Tq, sum(cuts)), scq * (_np(q) @ np.swapaxes(K_, -1, -2)), -np.inf)
+    _gate_nan(_oracle_blocks(s, V, cuts), out, TOL_BF16)
+
+
 @pytest.mark.parametrize("d", [32, 96])
 def test_fp32_attention_runs_the_carrier_kernel(sink, dev, d):
     # fp32 operands, a head dim the bf16 kernel does not take: the fp32

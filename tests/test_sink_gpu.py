@@ -173,6 +173,19 @@ def test_retention_kway_executor(sink, dev, C):
     _gate(oracle.retention_quadratic(_np(q), _np(k), _np(v2), gam.double().numpy(), 0.5), out2, 2e-2)
 
 
+def test_retention_kway_executor_head_dim_64(sink, dev):
+    # d = 64 runs the d = 128 kernel on zero-padded operands, still no fallback
+    B, H, T, d = 2, 2, 256, 64
+    ir, _ = forms.retention_kway_form(B, H, T, d, 64)
+    gam = torch.tensor([1 - 2.0 ** (-5 - h / 2) for h in range(H)], dtype=torch.float32)
+    q, k, v = (_rand((B, H, T, d), torch.bfloat16, 50 + i, 1 / math.sqrt(d)) for i in range(3))
+    res = deliver(ir, {"gamma": gam}, sink, tuple(t.to(dev) for t in (q, k, v)))
+    assert res.stats["executor"] == "om_decayed_chunked" and res.stats["hip_kernel"]
+    out = res.module(*(t.to(dev) for t in (q, k, v)))
+    assert res.module.fallbacks == 0 and out.shape == (B, H, T, d)
+    _gate(oracle.retention_quadratic(_np(q), _np(k), _np(v), gam.double().numpy()), out, 2e-2)
+
+
 def test_retention_verified_against_the_spelled_block_form(sink, dev):
     B, H, T = 1, 2, 256
     ir, _ = forms.retention_kway_form(B, H, T, 128, 64)
