@@ -8,8 +8,9 @@
 // are K-contiguous, the layout the 16x16x32 bf16 MFMA consumes directly (each
 // lane supplies 8 consecutive k of one row).  W rows feed the MFMA's A
 // operand and X rows its B operand, so a lane's accumulators hold four
-// consecutive output columns n of one row m: the epilogue packs them into
-// one 8-byte store.
+// consecutive output columns n of one row m; the epilogue trades halves of
+// adjacent blocks between lane rows (v_permlane16_swap) so that each lane
+// stores 8 consecutive columns with one 16-byte store.
 //
 // Tiling: a 256 (m) x 256 (n) output tile per workgroup of 8 waves, two per
 // SIMD.  Wave w owns m rows [128 (w / 4), +128) and n columns [64 (w % 4),
@@ -20,15 +21,16 @@
 // computes and the other does memory work, and group 1 runs one phase behind
 // group 0, so on every SIMD one wave issues MFMAs back to back while its
 // partner reads its next fragments.  A K stage of 64 is two steps of 32:
-//   memory phase, first step:  read the wave's fragments of the step from LDS
-//     (12 x ds_read_b128) and issue the group's half of the global->LDS loads
-//     of the next stage (group 0 the X tile, group 1 the W tile);
-//   memory phase, second step:  read the fragments, wait for the wave's own
-//     loads of the next stage;
+//   memory phase, first step:  read the wave's 12 fragments of the step
+//     from LDS (ds_read_b128) and issue 4 global->LDS loads of the wave's W
+//     rows of the next stage;
+//   memory phase, second step:  read the fragments, issue 4 loads of the
+//     wave's X rows two stages ahead, wait for every load but those 4;
 //   compute phase:  32 MFMAs over the fragment registers, nothing else.
-// Two LDS stages of 64 KB (X then W) alternate: the next stage goes into the
-// one the previous stage used, which both groups finished reading in the
-// phases before, and it lands two phases before its first reader.
+// LDS holds ten 16 KB slots (160 KB): a ring of 3 stages for each group's
+// 128 X rows and a ring of 2 stages for the 256 W rows.  Each load goes
+// into the slot of a stage that every wave finished reading in an earlier
+// phase; the detailed slot schedule is written at the main loop.
 //
 // Persistent tiles: the grid is one workgroup per CU, and each workgroup
 // walks its tiles in rounds.  The loads run one stage ahead across tile
