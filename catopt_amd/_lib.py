@@ -79,6 +79,8 @@ SIGNATURES: dict[str, tuple] = {
         _i32,
         [_i64, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _i32, _p, _p, _p, _i64, _p],
     ),
+    "catopt_hip_affd_compose_slots": (_i32, [_i64, _i64, _p, _p, _p, _p, _i64, _i64, _p]),
+    "catopt_hip_aff_compose_slots": (_i32, [_i64, _i64, _i64, _p, _p, _p, _p, _i64, _i64, _p]),
     "catopt_hip_silu": (_i32, [_i32, _i64, _p, _p, _p]),
     "catopt_hip_silu_mul": (_i32, [_i32, _i64, _p, _p, _p, _p]),
 }

@@ -21,7 +21,11 @@ when every projected map is a prefix of ONE leaf sequence of one carrier,
 the plan is ``chain`` and all prefix maps come from the HIP scan kernels in
 one pass, then answer every projection and stack by gather (seeded into the
 evaluator's memo, so the score terms around them evaluate unchanged).  Maps
-of any other bracketing (``forest``) are evaluated by the generic module.
+of any other bracketing, or of both carriers, make a ``forest`` plan: per
+carrier, the compose nodes are grouped by depth (leaves at level 0, shared
+subterms once) and each level runs as one HIP launch over slot arrays
+(``catopt_hip_affd_compose_slots`` / ``catopt_hip_aff_compose_slots``);
+the projections are then answered from the slots the same way.
 
 Execution on the device:
 
@@ -29,6 +33,9 @@ Execution on the device:
   lanes from ``[1 | 0]`` with offsets ``[0 | b]`` gives
   ``[∏a | prefix b]``; dense: two ``catopt_hip_aff_scan`` launches
   (``I`` under the maps alone, ``0`` under the maps and offsets);
+* forest maps — the leaf parts stacked into fp32 slot arrays, then one
+  compose launch per level (the diagonal products and sums rounded as the
+  serial evaluation rounds them);
 * leaves — a score ``scale · q kᵀ`` (unmasked) runs the fused fp32 carrier
   kernel ``catopt_hip_attn_carrier_f32`` over the values ``[a | b]``: the
   scores, exponentials and numerators stay on chip; any other score is
@@ -57,7 +64,7 @@ from .. import _lib as L
 from .. import kernels as K
 from ..bindings import _om_compose, attr_of
 from ..evaluator import HipIRModule
-from ..ir import IR, Op, is_op
+from ..ir import IR, Op, Param, Var, is_op
 from .base import HipExecutorBase
 from .om import _peel_scale, parse_score
 from .scan import prefix_chunk_table
@@ -119,6 +126,8 @@ def _step_index(t: Any) -> tuple | None:
 
 def _part_gather(leaves: list, slot: int) -> tuple | None:
     """``(base, dim, indices)`` when every leaf's part ``slot`` indexes one base."""
+    if not all(isinstance(lf, Op) and lf.op in _LEAF and len(lf.args) == 2 for lf in leaves):
+        return None
     idx = [_step_index(lf.args[slot]) for lf in leaves]
     if any(i is None for i in idx):
         return None
@@ -242,21 +251,150 @@ def build_omd_plan(root: Any) -> dict | None:
         dom = next(iter(doms))
         leaf_op, comp_op = ("aff_diag", "affd_compose") if dom == "diag" else ("aff", "aff_compose")
         fast = _spine_positions(maps, leaf_op, comp_op)
-        if fast is not None:
+        if fast is not None and _sig_uniform(fast[1], dom):
             return _chain_plan(plan, dom, fast[1], fast[0], projs, stacks, [m for m in loose if m in maps])
     seqs = {mp: _app_order(mp) for mp in maps}  # terms are content-keyed (cached hashes)
     base = max(seqs.values(), key=len)
-    doms = set(maps.values())
     dom = next(iter(doms))
-    leaf_op = {"diag": "aff_diag", "dense": "aff"}[dom]
+    # opaque leaves (any term evaluating to a pair) may sit in a chain; a leaf
+    # of the other carrier may not
     chain = (len(doms) == 1
              and all(len(s) <= len(base) and all(x is y or x == y for x, y in zip(s, base)) for s in seqs.values())
-             and all(is_op(lf, leaf_op, 2) for lf in base))
-    if not chain:
-        plan["map_mode"] = "forest"
-        return plan
-    pos = {mp: len(s) - 1 for mp, s in seqs.items()}
-    return _chain_plan(plan, dom, base, pos, projs, stacks, [m for m in loose if m in maps])
+             and all(_LEAF.get(lf.op, dom) == dom if isinstance(lf, Op) else True for lf in base)
+             and _sig_uniform(base, dom))
+    if chain:
+        pos = {mp: len(s) - 1 for mp, s in seqs.items()}
+        return _chain_plan(plan, dom, base, pos, projs, stacks, [m for m in loose if m in maps])
+    return _forest_plan(plan, maps, projs, stacks, loose)
+
+
+def _static_shape(t: Any) -> tuple | None:
+    """The shape of a leaf part where the term states it: a variable or
+    weight, or an integer ``select`` / ``getitem`` of one; else ``None``."""
+    if isinstance(t, (Var, Param)):
+        return tuple(t.typ.shape)
+    si = _step_index(t)
+    if si is not None:
+        base = _static_shape(si[0])
+        if base is None or not base:
+            return None
+        dim = si[1] % len(base)
+        return base[:dim] + base[dim + 1:]
+    return None
+
+
+def _leaf_sig(leaf: Any, dom: str) -> Any:
+    """``(dom, shape)`` of an ``aff_diag`` / ``aff`` leaf whose part shapes are
+    known, ``None`` when unknown or opaque, ``False`` when they break the
+    carrier's contract (diagonal: ``a`` and ``b`` of one shape; dense: square
+    ``A`` with ``b`` its leading shape), as ``omd_lower.py:189-217`` checks."""
+    if not isinstance(leaf, Op) or leaf.op not in _LEAF or len(leaf.args) != 2:
+        return None
+    a, b = _static_shape(leaf.args[0]), _static_shape(leaf.args[1])
+    if a is None or b is None:
+        return None
+    if leaf.op == "aff_diag":
+        return (dom, a) if a == b else False
+    if len(a) >= 2 and a[-1] == a[-2] and b == a[:-1]:
+        return (dom, a)
+    return False
+
+
+def _sig_uniform(leaves: list, dom: str) -> bool:
+    sig = None
+    for lf in leaves:
+        s = _leaf_sig(lf, dom)
+        if s is False:
+            return False
+        if s is not None:
+            if sig is None:
+                sig = s
+            elif s != sig:
+                return False
+    return True
+
+
+def _has_projection(t: Any) -> bool:
+    stack, seen = [t], set()
+    while stack:
+        u = stack.pop()
+        if not isinstance(u, Op) or id(u) in seen:
+            continue
+        seen.add(id(u))
+        if u.op in _PROJ:
+            return True
+        stack.extend(u.args)
+    return False
+
+
+def _walk_maps(maps: dict) -> dict | None:
+    """Per carrier: the leaves (level 0, first-met order) and the compose
+    nodes by level (one more than the deeper operand) of every map, shared
+    subterms once; ``None`` when a compose or leaf op belongs to the other
+    carrier, or a map leaf's operands project another map
+    (``omd_lower.py:361-455``).  Iterative: prefix chains nest O(T) deep."""
+    domains: dict = {}
+    for root_mp, expected in maps.items():
+        stack = [(root_mp, expected, False)]
+        while stack:
+            mp, exp, done = stack.pop()
+            if isinstance(mp, Op) and mp.op in _COMPOSE and len(mp.args) == 2:
+                if _COMPOSE[mp.op] != exp:
+                    return None
+                d = domains.setdefault(exp, {"leaves": [], "levels": [], "level_of": {}})
+                if mp in d["level_of"]:
+                    continue
+                if not done:
+                    stack.append((mp, exp, True))
+                    stack.append((mp.args[0], exp, False))
+                    stack.append((mp.args[1], exp, False))
+                    continue
+                lv = max(d["level_of"][c] for c in mp.args) + 1
+                d["level_of"][mp] = lv
+                while len(d["levels"]) < lv:
+                    d["levels"].append([])
+                d["levels"][lv - 1].append(mp)
+                continue
+            if isinstance(mp, Op) and mp.op in _LEAF and len(mp.args) == 2 and _LEAF[mp.op] != exp:
+                return None
+            d = domains.setdefault(exp, {"leaves": [], "levels": [], "level_of": {}})
+            if mp in d["level_of"]:
+                continue
+            d["level_of"][mp] = 0
+            d["leaves"].append(mp)
+            if isinstance(mp, Op) and any(_has_projection(c) for c in mp.args):
+                return None
+    return domains
+
+
+def _forest_plan(plan: dict, maps: dict, projs: list, stacks: list, loose: list) -> dict | None:
+    """Level-batched plan for maps of any bracketing (``omd_lower.py:520-558``):
+    per carrier, leaf slots ``0..n-1`` and then each level's nodes in order,
+    with the operand slots each level's launch reads."""
+    domains = _walk_maps(maps)
+    if domains is None:
+        return None
+    for dom, d in domains.items():
+        if not _sig_uniform(d["leaves"], dom):
+            return None
+        slot = {lf: i for i, lf in enumerate(d["leaves"])}
+        nxt, gathers = len(d["leaves"]), []
+        for nodes in d["levels"]:
+            gathers.append(([slot[t.args[0]] for t in nodes], [slot[t.args[1]] for t in nodes]))
+            for t in nodes:
+                slot[t] = nxt
+                nxt += 1
+        d.update(slot=slot, gathers=gathers, n_slots=nxt,
+                 a_gather=_part_gather(d["leaves"], 0), b_gather=_part_gather(d["leaves"], 1))
+        del d["level_of"]
+    src = {dom: ("forest", dom) for dom in domains}
+    at = lambda mp: domains[maps[mp]]["slot"][mp]  # noqa: E731
+    plan.update(map_mode="forest", forest=domains)
+    plan["proj_seeds"] = [(node, ci, src[maps[mp]], at(mp)) for node, ci, mp in projs]
+    plan["stack_seeds"] = [(node, ci, src[maps[mps[0]]], [at(mp) for mp in mps], dim)
+                           for node, ci, mps, dim in stacks]
+    plan["map_seeds"] = [(mp, src[maps[mp]], at(mp)) for mp in dict.fromkeys(m for m in loose if m in maps)]
+    return plan
 
 
 def _chain_plan(plan: dict, dom: str, base: list, pos: dict, projs: list, stacks: list, loose: list) -> dict:
@@ -266,9 +404,10 @@ def _chain_plan(plan: dict, dom: str, base: list, pos: dict, projs: list, stacks
     stacks of one contiguous run of prefix positions, those runs."""
     plan.update(map_mode="chain", chain_domain=dom, chain_leaves=base,
                 chain_a_gather=_part_gather(base, 0), chain_b_gather=_part_gather(base, 1))
-    plan["proj_seeds"] = [(node, ci, pos[mp]) for node, ci, mp in projs]
-    plan["stack_seeds"] = [(node, ci, [pos[mp] for mp in mps], dim) for node, ci, mps, dim in stacks]
-    plan["map_seeds"] = [(mp, pos[mp]) for mp in dict.fromkeys(loose)]
+    src = ("chain",)
+    plan["proj_seeds"] = [(node, ci, src, pos[mp]) for node, ci, mp in projs]
+    plan["stack_seeds"] = [(node, ci, src, [pos[mp] for mp in mps], dim) for node, ci, mps, dim in stacks]
+    plan["map_seeds"] = [(mp, src, pos[mp]) for mp in dict.fromkeys(loose)]
     plan["blocks"] = _leaf_blocks(plan)
     return plan
 
@@ -276,7 +415,7 @@ def _chain_plan(plan: dict, dom: str, base: list, pos: dict, projs: list, stacks
 def _leaf_blocks(plan: dict) -> list | None:
     """``[(start, length)]`` per leaf when its ``a`` and ``b`` arguments stack
     the same contiguous prefix positions along axis 0; else ``None``."""
-    by_node = {id(node): (ci, idx, dim) for node, ci, idx, dim in plan["stack_seeds"]}
+    by_node = {id(node): (ci, idx, dim) for node, ci, _src, idx, dim in plan["stack_seeds"]}
     out = []
     for lf in plan["leaves"]:
         if lf.op != "omd_elem":
@@ -338,27 +477,56 @@ class HipOmdModule(HipExecutorBase, nn.Module):
 
     # ------------------------------------------------------------ prefix maps
 
-    def _chain_parts(self, ev) -> tuple:
-        """Leaf ``(a, b)`` parts of the chain, step-major."""
-        p = self._plan
+    def _index(self, idx: list, like: torch.Tensor) -> torch.Tensor:
+        return self._cached(("idx", tuple(idx)), like,
+                            lambda x: torch.tensor(idx, dtype=torch.long, device=x.device), dtype=torch.long)
+
+    @staticmethod
+    def _leaf_part(leaf: Any, i: int, ev) -> Any:
+        """Part ``i`` of a map leaf: the ``aff_diag`` / ``aff`` operand, or
+        ``value[i]`` of an opaque leaf (a pair or a stacked tensor), as the
+        generic projection reads it (``omd_lower.py:698-713``)."""
+        if isinstance(leaf, Op) and leaf.op in _LEAF and len(leaf.args) == 2:
+            return ev(leaf.args[i])
+        return ev(leaf)[i]
+
+    def _leaf_parts(self, leaves: list, gathers: tuple, ev) -> tuple:
+        """Leaf ``(a, b)`` parts stacked leaf-major: one ``index_select`` of a
+        shared base when every leaf indexes one, else a stack."""
         out = []
-        for slot in (0, 1):
-            g = p["chain_a_gather"] if slot == 0 else p["chain_b_gather"]
-            t = None
+        for slot, g in enumerate(gathers):
             if g is not None:
                 base, dim, idx = g
                 bt = ev(base)
                 if idx == list(range(bt.shape[dim])):
                     t = bt.movedim(dim, 0)
                 else:
-                    ix = self._cached(("idx", tuple(idx)), bt,
-                                      lambda x: torch.tensor(idx, dtype=torch.long, device=x.device),
-                                      dtype=torch.long)
-                    t = bt.index_select(dim, ix).movedim(dim, 0)
+                    t = bt.index_select(dim, self._index(idx, bt)).movedim(dim, 0)
             else:
-                t = torch.stack([torch.as_tensor(ev(lf.args[slot])) for lf in p["chain_leaves"]])
+                t = torch.stack([torch.as_tensor(self._leaf_part(lf, slot, ev)) for lf in leaves])
             out.append(t)
         return out[0], out[1]
+
+    def _forest_maps(self, ev, dtypes: list) -> dict:
+        """Every map of a forest plan, per carrier: the leaf parts in slots
+        ``0..n-1`` of fp32 slot arrays, then one compose launch per level."""
+        stores = {}
+        for dom, d in self._plan["forest"].items():
+            A, B = self._leaf_parts(d["leaves"], (d["a_gather"], d["b_gather"]), ev)
+            if not (_kernel_dtype(A) and _kernel_dtype(B)):
+                raise _Decline()
+            dtypes += [A.dtype, B.dtype]
+            n0, n = A.shape[0], d["n_slots"]
+            SA = torch.empty((n, *A.shape[1:]), dtype=torch.float32, device=A.device)
+            SB = torch.empty((n, *B.shape[1:]), dtype=torch.float32, device=B.device)
+            SA[:n0].copy_(A)
+            SB[:n0].copy_(B)
+            out0 = n0
+            for fi, gi in d["gathers"]:
+                K.compose_slots(SA, SB, self._index(fi, SA), self._index(gi, SA), out0, dom)
+                out0 += len(fi)
+            stores[("forest", dom)] = (SA, SB)
+        return stores
 
     def _prefix_maps(self, A: torch.Tensor, B: torch.Tensor) -> tuple:
         """Every prefix map ``f_t = leaf_t ∘ … ∘ leaf_0`` of the chain (fp32)."""
@@ -392,17 +560,16 @@ class HipOmdModule(HipExecutorBase, nn.Module):
                           table, states=True)                                       # x_t = A_t x + b_t
         return M.reshape(A.shape), v.reshape(B.shape)
 
-    def _seed(self, memo: dict, Pa: torch.Tensor, Pb: torch.Tensor) -> None:
-        parts = (Pa, Pb)
-        for node, ci, i in self._plan["proj_seeds"]:
-            memo[node] = parts[ci][i]
-        for mp, i in self._plan["map_seeds"]:
-            memo[mp] = (Pa[i], Pb[i])
-        for node, ci, idx, dim in self._plan["stack_seeds"]:
-            src = parts[ci]
-            ix = self._cached(("stk", tuple(idx)), src,
-                              lambda x: torch.tensor(idx, dtype=torch.long, device=x.device), dtype=torch.long)
-            t = src.index_select(0, ix)
+    def _seed(self, memo: dict, stores: dict) -> None:
+        """Answer every projection, stack of projections and map seen in a
+        tensor position from the computed maps (``omd_lower.py:871-887``)."""
+        for node, ci, src, i in self._plan["proj_seeds"]:
+            memo[node] = stores[src][ci][i]
+        for mp, src, i in self._plan["map_seeds"]:
+            memo[mp] = (stores[src][0][i], stores[src][1][i])
+        for node, ci, src, idx, dim in self._plan["stack_seeds"]:
+            t = stores[src][ci]
+            t = t.index_select(0, self._index(idx, t))
             dn = dim % t.dim()
             memo[node] = t.movedim(0, dn) if dn else t
 
@@ -556,21 +723,26 @@ class HipOmdModule(HipExecutorBase, nn.Module):
         dtypes = []
         seeded: set = set()
         Pa = Pb = None
+        stores: dict = {}
         if p["map_mode"] == "chain":
-            A, B = self._chain_parts(ev)
+            A, B = self._leaf_parts(p["chain_leaves"], (p["chain_a_gather"], p["chain_b_gather"]), ev)
             if not (_kernel_dtype(A) and _kernel_dtype(B)):
                 raise _Decline()
             Pa, Pb = self._prefix_maps(A, B)
+            stores[("chain",)] = (Pa, Pb)
             # the result's dtype follows the chain's operands, not the fp32 prefix maps
             dtypes += [A.dtype, B.dtype]
+            seeded = self._seeded_ids
+        elif p["map_mode"] == "forest":
+            stores = self._forest_maps(ev, dtypes)
             seeded = self._seeded_ids
         state = None
         width = tail = None
         self.fused_leaves = 0
         batched = self._batched_blocks(ev, Pa, Pb) if Pa is not None else None
         if batched is None:
-            if Pa is not None:
-                self._seed(memo, Pa, Pb)  # the leaves read their coefficient stacks through the memo
+            if stores:
+                self._seed(memo, stores)  # the leaves read their coefficient stacks through the memo
             batched = self._batched_leaves(ev)
         if batched is not None:
             state, width, tail, sdts = batched

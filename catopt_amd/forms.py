@@ -25,7 +25,9 @@ can feed this package's sink exactly what the orchestrator would route:
   balanced ``aff_compose`` tree (the depth-extracted ``LinearRecurrence``
   term) and the stacked all-prefix form (``xcarrier.py:2276-2293``);
 * :func:`omd_scan_attention_form` — softmax attention over a scan's states
-  as the deferred-affine ``omd_apply`` term (``omd_lower.py:1-12``).
+  as the deferred-affine ``omd_apply`` term (``omd_lower.py:1-12``);
+  :func:`omd_block_restart_form` — the same over states that restart at
+  every key block (maps of several leaf sequences: a forest plan).
 
 Each returns ``(IR, param_shapes)``; parameter values come from the caller.
 """
@@ -49,6 +51,7 @@ __all__ = [
     "dense_scan_prefix_form",
     "diag_ssm_form",
     "omd_scan_attention_form",
+    "omd_block_restart_form",
 ]
 
 mk = Op.make
@@ -302,6 +305,46 @@ def omd_scan_attention_form(T: int, d: int, Tq: int, blocks: int, dk: int = 16, 
     elems = []
     for i in range(blocks):
         blk = fs[i * C:(i + 1) * C]
+        s = mk("matmul", q, mk("transpose", mk("chunk", k, chunks=blocks, dim=0, index=i), dim0=0, dim1=1))
+        elems.append(mk("omd_elem", s, mk("stack", *[mk(pa, f) for f in blk], dim=0),
+                        mk("stack", *[mk(pb, f) for f in blk], dim=0)))
+    root = mk("omd_applym" if dense else "omd_apply", _balanced(elems, "omd_compose"), h)
+    return IR(root, [q, k, a, x, h]), {}
+
+
+def omd_block_restart_form(T: int, d: int, Tq: int, blocks: int, dk: int = 16, *,
+                           dense: bool = False, bracket: str = "chain") -> tuple[IR, dict]:
+    """Attention over scan states that restart from ``h`` at every key block:
+    the coefficient maps of block ``i`` are the local prefixes
+    ``g_j = leaf_j ∘ … ∘ leaf_{iC}`` of that block's own leaves, so no map is
+    a prefix of another block's leaf sequence and the plan is a forest
+    (level-batched, ``omd_lower.py:520-558``; the disjoint-trees case of
+    tests/test_omd_lower.py:184-211 at scale).  ``bracket="chain"`` spells
+    ``g_j = compose(leaf_j, g_{j-1})``; ``"tree"`` spells every ``g_j`` as its
+    own balanced compose tree (equal subtrees are one term).  Operands as
+    :func:`omd_scan_attention_form`."""
+    if T % blocks:
+        raise ValueError("blocks must divide T")
+    q = Var("q", TensorType((Tq, dk)))
+    k = Var("k", TensorType((T, dk)))
+    a = Var("a", TensorType((T, d, d) if dense else (T, d)))
+    x = Var("x", TensorType((T, d)))
+    h = Var("h", TensorType((d,)))
+    leaf_op, comp, pa, pb = ("aff", "aff_compose", "aff_A", "aff_b") if dense else \
+        ("aff_diag", "affd_compose", "affd_a", "affd_b")
+    C = T // blocks
+    elems = []
+    if bracket not in ("chain", "tree"):
+        raise ValueError(bracket)
+    for i in range(blocks):
+        blk, lvs = [], []
+        for j in range(i * C, (i + 1) * C):
+            leaf = mk(leaf_op, mk("select", a, dim=0, index=j), mk("select", x, dim=0, index=j))
+            lvs.append(leaf)
+            if bracket == "tree":
+                blk.append(_balanced(lvs[::-1], comp))  # product order: latest leaf first
+            else:
+                blk.append(leaf if j == i * C else mk(comp, leaf, blk[-1]))
         s = mk("matmul", q, mk("transpose", mk("chunk", k, chunks=blocks, dim=0, index=i), dim0=0, dim1=1))
         elems.append(mk("omd_elem", s, mk("stack", *[mk(pa, f) for f in blk], dim=0),
                         mk("stack", *[mk(pb, f) for f in blk], dim=0)))

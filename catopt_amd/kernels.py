@@ -601,6 +601,38 @@ def aff_scan(A: torch.Tensor, b: torch.Tensor, h0: torch.Tensor, chunk_starts, *
     return out, hf
 
 
+def compose_slots(A: torch.Tensor, B: torch.Tensor, f: torch.Tensor, g: torch.Tensor, out0: int,
+                  domain: str) -> None:
+    """One level of a compose forest, in place: slot ``out0 + j`` of the
+    contiguous fp32 slot arrays becomes ``compose(slot f[j], slot g[j])``
+    (``g`` applied first).  ``domain`` "diag": ``A`` and ``B`` are
+    ``(n_slots, *shape)`` of one shape; "dense": ``A`` is
+    ``(n_slots, *P, d, d)`` and ``B`` is ``(n_slots, *P, d)``.  ``f`` and
+    ``g`` are device int64 slot indices, each below ``out0``."""
+    _need_device(A, B, f, g)
+    lib = L.load()
+    if A.dtype != torch.float32 or B.dtype != torch.float32 or not (A.is_contiguous() and B.is_contiguous()):
+        raise ValueError("compose_slots wants contiguous fp32 slot arrays")
+    if f.dtype != torch.long or g.dtype != torch.long or f.shape != g.shape or f.dim() != 1:
+        raise ValueError("compose_slots wants two int64 index vectors of one length")
+    n, Lv = A.shape[0], f.shape[0]
+    if B.shape[0] != n or not 1 <= out0 <= n or out0 + Lv > n:
+        raise ValueError(f"compose_slots: {Lv} outputs from slot {out0} do not fit {n} slots")
+    if domain == "diag":
+        if A.shape != B.shape:
+            raise ValueError("diagonal slot arrays differ in shape")
+        st = lib.catopt_hip_affd_compose_slots(n, A[0].numel(), _ptr(A), _ptr(B), _ptr(f), _ptr(g), Lv, out0,
+                                               _stream(A))
+        L.check("catopt_hip_affd_compose_slots", st)
+        return
+    d = A.shape[-1]
+    if A.dim() < 3 or A.shape[-2] != d or B.shape != A.shape[:-1]:
+        raise ValueError("dense slot arrays are not square maps with matching offsets")
+    P = int(torch.Size(A.shape[1:-2]).numel())
+    st = lib.catopt_hip_aff_compose_slots(n, P, d, _ptr(A), _ptr(B), _ptr(f), _ptr(g), Lv, out0, _stream(A))
+    L.check("catopt_hip_aff_compose_slots", st)
+
+
 def ssm_scan(a: torch.Tensor, bx: torch.Tensor, c: torch.Tensor, x: torch.Tensor,
              h0: torch.Tensor | None, chunk_starts, *, schedule: int = L.SCAN_AUTO,
              return_state: bool = False):

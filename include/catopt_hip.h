@@ -387,6 +387,29 @@ int32_t catopt_hip_aff_scan(int64_t T, int64_t P, int64_t d, int64_t k,
                             int64_t workspace_bytes, void* stream);
 
 /*
+ * One level of a compose forest over slot arrays (fp32).  Slots hold
+ * affine maps: diagonal (A, B: [n_slots, S]) or dense (A: [n_slots, P, d,
+ * d] row-major, B: [n_slots, P, d]).  For j < L (f, g: device int64[L]):
+ *   slot[out0 + j] = compose(slot[f[j]], slot[g[j]])
+ *   diagonal: (fa * ga, fa * gb + fb), product and sum rounded separately
+ *   dense:    (fa @ ga, fa @ gb + fb)
+ * Every f[j], g[j] must lie in [0, out0): an index outside gives NaN in
+ * that output slot.  Requires 1 ≤ out0 ≤ n_slots and out0 + L ≤ n_slots.
+ * Replaces the level loop of the forest plan of BatchedOmdModule
+ * (omd_lower.py:849-866, plan 520-558) over _compose_pair
+ * (omd_lower.py:236-246): one launch per level instead of per-node
+ * affd_compose / aff_compose bindings (torch_bridge.py:1873-1900).
+ */
+int32_t catopt_hip_affd_compose_slots(int64_t n_slots, int64_t S, float* A,
+                                      float* B, const int64_t* f,
+                                      const int64_t* g, int64_t L,
+                                      int64_t out0, void* stream);
+int32_t catopt_hip_aff_compose_slots(int64_t n_slots, int64_t P, int64_t d,
+                                     float* A, float* B, const int64_t* f,
+                                     const int64_t* g, int64_t L,
+                                     int64_t out0, void* stream);
+
+/*
  * Elementwise helpers behind the generic evaluator's bindings when no
  * fused form applies: silu (torch_bridge.py:1159), mul (the "mul"
  * binding) and the paired silu·mul of SWIGLU_FUSE.  n elements,

@@ -498,11 +498,11 @@ def test_omd_plan_chain_and_seeds():
     assert len(p["stack_seeds"]) == 2 * nb and len(p["leaves"]) == nb
     # each block's stack reads prefix positions i·C … i·C + C - 1
     C = T // nb
-    assert sorted(tuple(s[2]) for s in p["stack_seeds"]) == sorted(
+    assert sorted(tuple(s[3]) for s in p["stack_seeds"]) == sorted(
         [tuple(range(i * C, (i + 1) * C)) for i in range(nb)] * 2)
     pd = build_omd_plan(forms.omd_scan_attention_form(8, 2, 3, 2, dense=True)[0].root)
     assert pd["map_mode"] == "chain" and pd["chain_domain"] == "dense" and pd["apply"] == "omd_applym"
-    # two unrelated compose trees: forest (generic map evaluation)
+    # two unrelated compose trees: forest (level-batched map evaluation)
     a = [Var(f"a{i}", TensorType((2,))) for i in range(4)]
     t1 = mk("affd_compose", mk("aff_diag", a[1], a[1]), mk("aff_diag", a[0], a[0]))
     t2 = mk("affd_compose", mk("aff_diag", a[3], a[3]), mk("aff_diag", a[2], a[2]))
@@ -511,6 +511,8 @@ def test_omd_plan_chain_and_seeds():
               mk("stack", mk("affd_b", t1), mk("affd_b", t2), dim=0))
     pf = build_omd_plan(mk("omd_apply", leaf, a[0]))
     assert pf["map_mode"] == "forest"
+    fd = pf["forest"]["diag"]
+    assert len(fd["leaves"]) == 4 and fd["n_slots"] == 6 and len(fd["gathers"]) == 1
     # not omd-shaped
     assert build_omd_plan(mk("om_apply", mk("om_elem", s, s))) is None
     assert not is_omd_term(mk("omd_apply", mk("omd_compose", leaf, s), a[0]))
@@ -549,4 +551,126 @@ def test_omd_plan_chain_with_other_bracketing():
               mk("stack", mk("affd_b", f1), mk("affd_b", f3), dim=0))
     p = build_omd_plan(mk("omd_apply", leaf, h))
     assert p["map_mode"] == "chain" and len(p["chain_leaves"]) == 4
-    assert [tuple(x[2]) for x in p["stack_seeds"]] == [(1, 3), (1, 3)]
+    assert [tuple(x[3]) for x in p["stack_seeds"]] == [(1, 3), (1, 3)]
+
+
+def _omd_over(amap, bmap, s_shape=(3, 2), h_shape=(2,)):
+    s, h = Var("s", TensorType(s_shape)), Var("h", TensorType(h_shape))
+    return mk("omd_apply", mk("omd_elem", s, amap, bmap), h)
+
+
+def test_omd_forest_plan_slots_and_levels():
+    """A balanced compose tree over 8 leaves, every internal node projected:
+    leaves take slots 0-7 in application order, each level's nodes the next
+    slots, and each level's gather names its operands' slots
+    (``omd_lower.py:520-558``)."""
+    from catopt_amd.executors import build_omd_plan
+
+    a = [Var(f"a{i}", TensorType((2,))) for i in range(8)]
+    lv = [mk("aff_diag", x, x) for x in a]
+    l1 = [mk("affd_compose", lv[2 * i + 1], lv[2 * i]) for i in range(4)]
+    l2 = [mk("affd_compose", l1[2 * i + 1], l1[2 * i]) for i in range(2)]
+    top = mk("affd_compose", l2[1], l2[0])
+    nodes = l1 + l2 + [top]
+    p = build_omd_plan(_omd_over(mk("stack", *[mk("affd_a", n) for n in nodes], dim=0),
+                                 mk("stack", *[mk("affd_b", n) for n in nodes], dim=0)))
+    assert p["map_mode"] == "forest" and set(p["forest"]) == {"diag"}
+    fd = p["forest"]["diag"]
+    assert fd["leaves"] == lv and fd["n_slots"] == 15
+    assert fd["gathers"] == [([1, 3, 5, 7], [0, 2, 4, 6]), ([9, 11], [8, 10]), ([13], [12])]
+    assert [fd["slot"][n] for n in nodes] == list(range(8, 15))
+    # both stacks read slots 8..14 in order from the diagonal store
+    assert [(ci, src, tuple(ix)) for _, ci, src, ix, _ in p["stack_seeds"]] == [
+        (0, ("forest", "diag"), tuple(range(8, 15))), (1, ("forest", "diag"), tuple(range(8, 15)))]
+    # a leaf gather: every leaf part is a variable, so none
+    assert fd["a_gather"] is None and fd["b_gather"] is None
+
+
+def test_omd_forest_plan_shares_subterms_and_mixes_carriers():
+    from catopt_amd.executors import build_omd_plan
+
+    a = [Var(f"a{i}", TensorType((2,))) for i in range(3)]
+    A = [Var(f"A{i}", TensorType((2, 2))) for i in range(2)]
+    lv = [mk("aff_diag", x, x) for x in a]
+    shared = mk("affd_compose", lv[1], lv[0])
+    t1 = mk("affd_compose", lv[2], shared)
+    t2 = mk("affd_compose", shared, lv[2])  # not a prefix of t1's sequence
+    dense = mk("aff_compose", mk("aff", A[1], a[1]), mk("aff", A[0], a[0]))
+    amap = mk("stack", mk("affd_a", t1), mk("affd_a", t2), dim=0)
+    p = build_omd_plan(_omd_over(amap, mk("add", mk("aff_b", dense), mk("affd_b", shared))))
+    assert p["map_mode"] == "forest" and set(p["forest"]) == {"diag", "dense"}
+    fd, fx = p["forest"]["diag"], p["forest"]["dense"]
+    # shared once: 3 leaves + shared + t1 + t2
+    assert fd["n_slots"] == 6 and fd["slot"][shared] == 3
+    assert fd["gathers"] == [([1], [0]), ([2, 3], [3, 2])]
+    assert fx["n_slots"] == 3 and fx["gathers"] == [([1], [0])]
+    srcs = {src for _, _, src, _ in p["proj_seeds"]}
+    assert srcs == {("forest", "diag"), ("forest", "dense")}
+
+
+def test_omd_forest_plan_declines():
+    """Plans the reference declines (``build_omd_plan`` returns None and the
+    generic module runs): a compose of the other carrier under a projection,
+    leaf shapes that break the carrier's contract or differ between leaves,
+    and a map leaf whose operands project another map."""
+    from catopt_amd.executors import build_omd_plan
+
+    a2, a3 = Var("a2", TensorType((2,))), Var("a3", TensorType((3,)))
+    A = Var("A", TensorType((2, 2)))
+    bm = Var("bm", TensorType((2,)))
+    dense = mk("aff_compose", mk("aff", A, a2), mk("aff", A, a2))
+    assert build_omd_plan(_omd_over(mk("affd_a", dense), bm)) is None
+    bad = mk("affd_compose", mk("aff_diag", a2, a3), mk("aff_diag", a2, a2))
+    assert build_omd_plan(_omd_over(mk("affd_a", bad), bm)) is None
+    mixed = mk("affd_compose", mk("aff_diag", a3, a3), mk("aff_diag", a2, a2))
+    assert build_omd_plan(_omd_over(mk("affd_a", mixed), bm)) is None
+    inner = mk("affd_compose", mk("aff_diag", a2, a2), mk("aff_diag", a2, a2))
+    nested = mk("affd_compose", mk("aff_diag", mk("affd_a", inner), a2), mk("aff_diag", a2, a2))
+    other = mk("affd_compose", mk("aff_diag", a2, bm), mk("aff_diag", bm, a2))
+    assert build_omd_plan(_omd_over(mk("stack", mk("affd_a", nested), mk("affd_a", other), dim=0), bm)) is None
+
+
+def test_omd_chain_plan_takes_opaque_leaves():
+    """A leaf that is any term evaluating to a pair (here a (2, d) input) may
+    sit in a prefix chain (``omd_lower.py:488-497``); its parts are read as
+    ``value[0]`` / ``value[1]``."""
+    from catopt_amd.executors import build_omd_plan
+
+    a = Var("a", TensorType((3,)))
+    M = Var("M", TensorType((2, 3)))
+    f1 = mk("affd_compose", mk("aff_diag", a, a), M)
+    p = build_omd_plan(_omd_over(mk("stack", mk("affd_a", M), mk("affd_a", f1), dim=0),
+                                 mk("stack", mk("affd_b", M), mk("affd_b", f1), dim=0), h_shape=(3,)))
+    assert p["map_mode"] == "chain" and p["chain_leaves"][0] is M
+    assert p["chain_a_gather"] is None
+
+
+@pytest.mark.parametrize("dense,bracket", [(False, "chain"), (False, "tree"), (True, "tree")])
+def test_omd_block_restart_form_is_attention_over_restarted_states(dense, bracket):
+    """The forest-plan form, run by the generic module on host fp64, is
+    softmax attention over scan states restarted from h at every key block
+    (float64 serial recurrences of the oracle)."""
+    from catopt_amd.executors import HipOmdModule
+
+    T, d, Tq, nb, dk = 16, 3, 5, 4, 4
+    ir, _ = forms.omd_block_restart_form(T, d, Tq, nb, dk, dense=dense, bracket=bracket)
+    mod = HipOmdModule(ir, {}, ops=cpu_table())
+    assert mod.map_mode == "forest"
+    g = torch.Generator().manual_seed(3)
+    q, k = torch.randn(Tq, dk, generator=g, dtype=torch.float64), torch.randn(T, dk, generator=g, dtype=torch.float64)
+    a = (torch.randn(T, d, d, generator=g, dtype=torch.float64) * 0.4 if dense
+         else torch.rand(T, d, generator=g, dtype=torch.float64))
+    x, h = torch.randn(T, d, generator=g, dtype=torch.float64), torch.randn(d, generator=g, dtype=torch.float64)
+    out = mod(q, k, a, x, h)
+    C = T // nb
+    blocks = []
+    for i in range(nb):
+        sl = slice(i * C, (i + 1) * C)
+        if dense:
+            blocks.append(oracle.serial_aff_scan(_np(a)[sl], _np(x)[sl], _np(h)[:, None])[..., 0])
+        else:
+            blocks.append(oracle.serial_affd_scan(_np(a)[sl], _np(x)[sl], _np(h)))
+    sc = _np(q) @ _np(k).T
+    w = np.exp(sc - sc.max(-1, keepdims=True))
+    ref = (w / w.sum(-1, keepdims=True)) @ np.concatenate(blocks)
+    assert oracle.verify_equiv(ref, _np(out), rtol=1e-12)["passed"]

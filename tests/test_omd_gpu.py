@@ -193,3 +193,86 @@ def test_omd_leaves_run_the_fused_kernel(dev):
     out = mod(*(t.to(dev) for t in ins))
     assert mod.fallbacks == 0 and mod.fused_leaves == nb
     _gate(_reference(*ins, False), out, TOL_F32)
+
+
+# ------------------------------------------------------------ forest plans
+
+
+def _restart_reference(q, k, a, x, h, blocks, dense):
+    qn, kn, an, xn, hn = (_np(t) for t in (q, k, a, x, h))
+    C = kn.shape[0] // blocks
+    parts = []
+    for i in range(blocks):
+        sl = slice(i * C, (i + 1) * C)
+        if dense:
+            parts.append(oracle.serial_aff_scan(an[sl], xn[sl], hn[:, None])[..., 0])
+        else:
+            parts.append(oracle.serial_affd_scan(an[sl], xn[sl], hn))
+    return _softmax_rows(qn @ kn.T) @ np.concatenate(parts)
+
+
+@pytest.mark.parametrize("dense,bracket", [(False, "chain"), (False, "tree"), (True, "chain"), (True, "tree")])
+def test_omd_forest_plan_block_restart(sink, dev, dense, bracket):
+    """Maps of several leaf sequences (states restarted at every key block):
+    the forest plan composes them level by level on the HIP slot kernels and
+    the leaves run the fused carrier kernel, no generic-module fallback."""
+    T, d, Tq, nb, dk = (64, 8, 24, 4, 16) if dense else (256, 32, 48, 8, 16)
+    ir, _ = forms.omd_block_restart_form(T, d, Tq, nb, dk, dense=dense, bracket=bracket)
+    ins = _inputs(T, d, Tq, dk, dense, 5)
+    print(f"forest dense={dense} bracket={bracket} T={T}", flush=True)
+    res = deliver(ir, {}, sink, tuple(t.to(dev) for t in ins))
+    assert res.stats["executor"] == "omd_batched" and res.stats["hip_kernel"]
+    mod = res.module
+    assert mod.map_mode == "forest"
+    out = mod(*[t.to(dev) for t in ins])
+    assert mod.fallbacks == 0 and mod.fused_leaves == nb
+    _gate(_restart_reference(*ins, nb, dense), out, TOL_F32)
+
+
+def test_compose_slots_kernels(dev):
+    """One launch per level over slot arrays.  Diagonal: bit-equal to the
+    serial torch evaluation of ``(fa * ga, fa * gb + fb)`` on the device (no
+    fused multiply-add).  Dense: ``(fa @ ga, fa @ gb + fb)`` against float64.
+    An operand slot at or past the level's first output gives NaN."""
+    from catopt_amd import kernels as K
+
+    rng = np.random.default_rng(11)
+    levels = [([1, 3, 5], [0, 2, 4]), ([7, 6], [6, 8]), ([10], [9])]
+    n = 12  # 6 leaves, then 3 + 2 + 1 nodes
+    # diagonal, a (2, 500) map per slot
+    A = torch.zeros(n, 2, 500, device=dev)
+    B = torch.zeros(n, 2, 500, device=dev)
+    A[:6] = torch.from_numpy(rng.uniform(0.5, 1.5, (6, 2, 500)).astype(np.float32)).to(dev)
+    B[:6] = torch.from_numpy(rng.standard_normal((6, 2, 500)).astype(np.float32)).to(dev)
+    RA, RB = A.clone(), B.clone()
+    out0 = 6
+    for f, g in levels:
+        fi = torch.tensor(f, device=dev)
+        gi = torch.tensor(g, device=dev)
+        K.compose_slots(A, B, fi, gi, out0, "diag")
+        for j, (a_, b_) in enumerate(zip(f, g)):
+            RA[out0 + j] = RA[a_] * RA[b_]
+            RB[out0 + j] = RA[a_] * RB[b_] + RB[a_]
+        out0 += len(f)
+    torch.cuda.synchronize()
+    assert torch.equal(A, RA) and torch.equal(B, RB)
+    # dense, P = 3 maps of 24 x 24 per slot
+    P, d = 3, 24
+    Ad = torch.zeros(n, P, d, d, device=dev)
+    Bd = torch.zeros(n, P, d, device=dev)
+    Ad[:6] = torch.from_numpy((rng.standard_normal((6, P, d, d)) / np.sqrt(d)).astype(np.float32)).to(dev)
+    Bd[:6] = torch.from_numpy(rng.standard_normal((6, P, d)).astype(np.float32)).to(dev)
+    ref_a, ref_b = list(_np(Ad[:6])), list(_np(Bd[:6]))
+    out0 = 6
+    for f, g in levels:
+        K.compose_slots(Ad, Bd, torch.tensor(f, device=dev), torch.tensor(g, device=dev), out0, "dense")
+        for a_, b_ in zip(f, g):
+            ref_a.append(ref_a[a_] @ ref_a[b_])
+            ref_b.append((ref_a[a_] @ ref_b[b_][..., None])[..., 0] + ref_b[a_])
+        out0 += len(f)
+    _gate(np.stack(ref_a), Ad, TOL_F32)
+    _gate(np.stack(ref_b), Bd, TOL_F32)
+    # an operand slot that is not yet written: NaN in that output only
+    K.compose_slots(A, B, torch.tensor([0, 9], device=dev), torch.tensor([1, 1], device=dev), 9, "diag")
+    torch.cuda.synchronize()
+    assert torch.equal(A[9], RA[0] * RA[1]) and bool(torch.isnan(A[10]).all()) and bool(torch.isnan(B[10]).all())
