@@ -21,13 +21,21 @@
 // wave (QB = 1).  That keeps a wave within 256 registers, so two waves share
 // each SIMD and one's softmax overlaps the other's MFMAs; QB = 2 (each K / V
 // fragment feeding two MFMAs) needs AGPRs and measured 1.33x slower, from
-// accumulator copies between the register files.  Waves raise their
-// priority around the MFMA blocks.  KV tiles of 64 keys are double buffered in LDS and
-// filled by direct global->LDS loads (dma16: no register
-// staging); K rows are 256 bytes with the 16-byte chunk index XOR-swizzled
-// by (key & 15), V rows with the transposing-read swizzle below.  A partial last tile zero-fills its missing V
-// rows.  Causal grids launch the longest query tiles first, skip tiles past
-// each wave's last key and apply the mask only on diagonal tiles.
+// accumulator copies between the register files.  KV tiles of 64 keys are
+// double buffered in LDS and filled by direct global->LDS loads through
+// buffer resources (no register staging; rows past the keys read as zeros);
+// K rows are 256 bytes with the 16-byte chunk index XOR-swizzled by
+// (key & 15), V rows with the transposing-read swizzle below.  Causal grids
+// launch the longest query tiles first, skip tiles past each wave's last key
+// and apply the mask only on diagonal tiles.
+//
+// Within a wave a tile runs as two key halves of 32, each its own online-
+// softmax step, so that the exponentials of one half issue between the MFMAs
+// of the other (the interleaving is fixed with sched_group_barrier).  On
+// MI355X that and reading all of a tile's K fragments before its first MFMA
+// each measured 1-2%; copies of the kernel with one part taken out put the
+// rest of the time in no single place (tile loads 12%, K or V fragment reads
+// 5-6% each, exponentials 4%, half the MFMAs 23%).
 //
 // Softmax runs in the exp2 domain: p = exp2((s - m) * c), c = scale·log2(e).
 // The running max is only moved (and Oᵀ, l rescaled) when a tile raises it
@@ -42,7 +50,7 @@ namespace catopt {
 namespace {
 
 constexpr int NT = 256;   // 4 waves
-constexpr int QB = 1;               // 32-query blocks per wave
+constexpr int QB = 1;               // 32-query blocks per wave (the tile loop assumes 1)
 constexpr int QW = 32 * QB;         // queries per wave
 constexpr int QT = 4 * QW;          // queries per workgroup
 constexpr int KVB = 64;   // keys per KV tile
@@ -81,6 +89,14 @@ template <int D>
 __device__ __forceinline__ int vtile_off(int key, int chunk) {
   return key * AttnLds<D>::ROW_BYTES + ((chunk ^ vswz<D>(key)) << 4);
 }
+
+// An empty asm use: the value must be computed before this point, which
+// keeps the compiler from sinking its computation out of an interleaved
+// region into a later block.
+__device__ __forceinline__ void pin(const bf16x8& x) {
+  asm volatile("" ::"v"(__builtin_bit_cast(u32x4, x)));
+}
+__device__ __forceinline__ void pin(float x) { asm volatile("" ::"v"(x)); }
 
 __device__ __forceinline__ s16x4 ds_read_tr(const char* lds_base, int byte_off) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -159,59 +175,35 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
   const int nkv = (int)((kv_end + KVB - 1) / KVB);
 
   // Fill one stage: K and V tiles of keys [kv0, kv0 + 64) by direct
-  // global->LDS loads.  Each thread owns SLOTS_PER_THREAD fixed 16-byte
-  // slots; their element offsets inside a tile are computed once (the host
-  // guarantees 64 rows of either stride fit in 31 bits), so a full tile
-  // costs a scalar base update per load.  A tail tile clamps rows past Tk
-  // to row Tk-1 (its V rows are zeroed afterwards).
+  // global->LDS loads through buffer resources over the tile's rows.  Each
+  // thread owns SLOTS_PER_THREAD fixed 16-byte slots whose byte offsets
+  // inside a tile are computed once (the host guarantees 64 rows of either
+  // stride fit in 31 bits); rows past Tk lie outside the resource and read
+  // as zeros, so a tail tile needs no clamping and its V rows past Tk are 0.
   // (literal array bounds: with a bound that depends on D the host pass
   // takes the arrays for variable-length ones and silently drops the
   // kernel's launch stub; 4 = SLOTS_PER_THREAD at D = 128, the largest)
   static_assert(AttnLds<D>::SLOTS_PER_THREAD <= 4, "slot arrays hold 4 entries");
-  int t_row[4], t_koff[4], t_voff[4], t_chunk8[4], t_vchunk8[4];
+  uint32_t t_koff[4], t_voff[4];
 #pragma unroll
   for (int i = 0; i < L::SLOTS_PER_THREAD; ++i) {
     const int s = i * NT + wave * 64 + lane;
     const int row = s / L::CH, cp = s % L::CH;
     const int chunk = cp ^ (row & (L::CH - 1) & 15);
     const int vchunk = cp ^ vswz<D>(row);
-    t_row[i] = row;
-    t_chunk8[i] = chunk * 8;
-    t_vchunk8[i] = vchunk * 8;
-    t_koff[i] = row * (int)kst + chunk * 8;
-    t_voff[i] = row * (int)vst + vchunk * 8;
+    t_koff[i] = (uint32_t)(row * (int)kst + chunk * 8) * 2u;
+    t_voff[i] = (uint32_t)(row * (int)vst + vchunk * 8) * 2u;
   }
   auto issue_tile = [&](int kvt, int stage) {
     const int kv0 = kvt * KVB;
-    char* kst_base = lds + stage * L::STAGE_BYTES;
-    const uint16_t* kt = k + (int64_t)kv0 * kst;
-    const uint16_t* vt = v + (int64_t)kv0 * vst;
-    if (kv0 + KVB <= Tk) {
+    const int64_t rows = Tk - kv0 < KVB ? Tk - kv0 : KVB;
+    const u32x4 kr = make_rsrc(k + (int64_t)kv0 * kst, (uint32_t)(((rows - 1) * kst + D) * 2));
+    const u32x4 vr = make_rsrc(v + (int64_t)kv0 * vst, (uint32_t)(((rows - 1) * vst + D) * 2));
+    const uint32_t sb = lds_u32(lds + stage * L::STAGE_BYTES) + wave * 64 * 16;
 #pragma unroll
-      for (int i = 0; i < L::SLOTS_PER_THREAD; ++i) {
-        const uint32_t dst = lds_u32(kst_base) + (i * NT + wave * 64) * 16;
-        dma16(kt + t_koff[i], dst);
-        dma16(vt + t_voff[i], dst + L::TILE_BYTES);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < L::SLOTS_PER_THREAD; ++i) {
-        int gk = kv0 + t_row[i];
-        gk = gk < Tk ? gk : Tk - 1;
-        const uint32_t dst = lds_u32(kst_base) + (i * NT + wave * 64) * 16;
-        dma16(k + (int64_t)gk * kst + t_chunk8[i], dst);
-        dma16(v + (int64_t)gk * vst + t_vchunk8[i], dst + L::TILE_BYTES);
-      }
-    }
-  };
-  // Zero the V rows of a tail tile that lie past Tk (called after the
-  // tile's loads have landed and a barrier).
-  auto zero_tail = [&](int kvt, int stage) {
-    const int kv0 = kvt * KVB;
-    char* vbase = lds + stage * L::STAGE_BYTES + L::TILE_BYTES;
-    for (int s = tid; s < L::SLOTS; s += NT) {
-      const int row = s / L::CH;
-      if (kv0 + row >= Tk) *reinterpret_cast<u32x4*>(vbase + s * 16) = u32x4{0, 0, 0, 0};
+    for (int i = 0; i < L::SLOTS_PER_THREAD; ++i) {
+      dma_buf(kr, t_koff[i], sb + i * NT * 16);
+      dma_buf(vr, t_voff[i], sb + i * NT * 16 + L::TILE_BYTES);
     }
   };
 
@@ -219,10 +211,6 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
     issue_tile(0, 0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (KVB > Tk) {
-      zero_tail(0, 0);
-      __syncthreads();
-    }
   }
 
   // one KV tile; the stage is a compile-time constant (the loop below runs
@@ -236,131 +224,173 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
     const int kv0 = kvt * KVB;
 
     if (kv0 < wave_end) {
-      // ---- Sᵀ = K Qᵀ for 64 keys x 64 queries
-      __builtin_amdgcn_s_setprio(1);
-      f32x16 sacc[2][QB];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) sacc[kb][qb][r] = 0.f;
-#pragma unroll
-      for (int j = 0; j < D / 16; ++j) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8*>(Ks + tile_off<D>(32 * kb + l32, 2 * j + g));
-#pragma unroll
-          for (int qb = 0; qb < QB; ++qb) sacc[kb][qb] = mfma32x32x16(a, qf[qb][j], sacc[kb][qb]);
-        }
-      }
-
-      __builtin_amdgcn_s_setprio(0);
-      // ---- mask (diagonal / tail / bool tiles only)
+      // The tile runs as two key halves of 32 (kb = 0, 1), each its own
+      // online-softmax step, so that the exponentials of one half issue
+      // between the MFMAs of the other in one instruction stream:
+      //   QK(0) | max(0) | QK(1) + exp(0) | max(1) | PV(0) + exp(1) | PV(1)
+      // (+: interleaved by sched_group_barrier).  A move of the reference
+      // max asked for by half 1 rescales Oᵀ after PV(0), whose probabilities
+      // are relative to the previous reference, and before PV(1).
       bool need_mask = kv0 + KVB > Tk;
       if (MASK == CATOPT_MASK_CAUSAL) need_mask = need_mask || (int64_t)kv0 + KVB - 1 > (int64_t)qw0 + causal_off;
       if (MASK == CATOPT_MASK_BOOL || MASK == CATOPT_MASK_BIAS) need_mask = true;
-      if (need_mask) {
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          const int qrow = qw0 + 32 * qb + l32;
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              // Branch-free: every lane evaluates every predicate (the mask
-              // byte is read at a clamped, always-valid address) and the
-              // score is replaced by a select.
-              const int key = kv0 + 32 * kb + acc_row(r, g);
-              bool keep = key < Tk;
-              if (MASK == CATOPT_MASK_CAUSAL) keep = keep & ((int64_t)key <= (int64_t)qrow + causal_off);
-              float add = 0.f;
-              if (MASK == CATOPT_MASK_BOOL || MASK == CATOPT_MASK_BIAS) {
-                const int qc = qrow < Tq ? qrow : Tq - 1;
-                const int kc = key < Tk ? key : Tk - 1;
-                const int64_t mi = (int64_t)qc * mask_ld + kc;
-                if (MASK == CATOPT_MASK_BOOL) keep = keep & (static_cast<const uint8_t*>(mask)[mi] != 0);
-                // the bias is in units of the scaled score; the running
-                // scores here are q·k, scaled at the exponential
-                if (MASK == CATOPT_MASK_BIAS) add = static_cast<const float*>(mask)[mi] * inv_scale;
-                keep = keep & (qrow < Tq);
-              }
-              sacc[kb][qb][r] = keep ? sacc[kb][qb][r] + add : -__builtin_inff();
-            }
-          }
-        }
-      }
+      const int qrow = qw0 + l32;
 
-      // ---- online softmax (lazy rescale), per 32-query block
-      bf16x8 pf[2][QB][2];  // [kb][qb][u]
+      bf16x8 kf[2][D / 16], vf[2][D / 16];
+      auto read_k = [&](int kb) {
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        float mt = -__builtin_inff();
+        for (int j = 0; j < D / 16; ++j)
+          kf[kb][j] = *reinterpret_cast<const bf16x8*>(Ks + tile_off<D>(32 * kb + l32, 2 * j + g));
+      };
+      // Vᵀ fragments of key half kb.  Lane: group G = lane / 16, j = lane %
+      // 16 -> keys key0 + j / 4 and key0 + 8 + j / 4, d block 4 (j % 4).
+      auto read_v = [&](int kb) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[kb][qb][r]);
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-        m_true[qb] = fmaxf(m_true[qb], mt);
-        // move the reference max only when this tile exceeds it by kLazy (log2 units)
-        const bool move = (mt - m_run[qb]) * c > kLazy;
-        if (__builtin_amdgcn_ballot_w64(move) != 0) {
-          const float m_new = fmaxf(m_run[qb], mt);
-          const float alpha = (m_run[qb] == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f((m_run[qb] - m_new) * c);
-          l_run[qb] *= alpha;
-#pragma unroll
-          for (int db = 0; db < D / 32; ++db)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) oacc[db][qb][r] *= alpha;
-          m_run[qb] = m_new;
-        }
-        const float mc = (m_run[qb] == -__builtin_inff()) ? 0.f : m_run[qb] * c;
-        float lsum = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][qb][r], c, -mc));
-            lsum += p;
-            pf[kb][qb][r >> 3][r & 7] = static_cast<__bf16>(p);
-          }
-        }
-        l_run[qb] += lsum;
-      }
-
-      // ---- Oᵀ += Vᵀ Pᵀ
-      __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-      for (int db = 0; db < D / 32; ++db) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+        for (int db = 0; db < D / 32; ++db) {
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
-            // lane: group G = lane/16, j = lane%16 -> key kA + j/4 (+8), d block 4*(j%4)
             const int G = lane >> 4, jj = lane & 15;
             const int key0 = 32 * kb + 16 * u + 4 * (G >> 1) + (jj >> 2);
             const int d = 32 * db + 16 * (G & 1) + 4 * (jj & 3);
             const int chunk = d >> 3, half = (d & 7) * 2;
             const s16x4 lo = ds_read_tr(Vs, vtile_off<D>(key0, chunk) + half);
             const s16x4 hi = ds_read_tr(Vs, vtile_off<D>(key0 + 8, chunk) + half);
-            const bf16x8 a = __builtin_bit_cast(
+            vf[kb][2 * db + u] = __builtin_bit_cast(
                 bf16x8, u32x4{__builtin_bit_cast(u32x2, lo)[0], __builtin_bit_cast(u32x2, lo)[1],
                               __builtin_bit_cast(u32x2, hi)[0], __builtin_bit_cast(u32x2, hi)[1]});
-#pragma unroll
-            for (int qb = 0; qb < QB; ++qb) oacc[db][qb] = mfma32x32x16(a, pf[kb][qb][u], oacc[db][qb]);
           }
         }
+      };
+      // Sᵀ of key half kb (32 keys x 32 queries)
+      auto qk = [&](int kb, f32x16& s) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = 0.f;
+#pragma unroll
+        for (int j = 0; j < D / 16; ++j) s = mfma32x32x16(kf[kb][j], qf[0][j], s);
+      };
+      // Oᵀ += Vᵀ Pᵀ over key half kb
+      auto pv = [&](int kb, const bf16x8* p) {
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) oacc[db][0] = mfma32x32x16(vf[kb][2 * db + u], p[u], oacc[db][0]);
+      };
+      // mask (diagonal / tail / bool / bias tiles only), branch-free: every
+      // lane evaluates every predicate (the mask byte is read at a clamped,
+      // always-valid address) and the score is replaced by a select
+      auto apply_mask = [&](int kb, f32x16& s) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kv0 + 32 * kb + acc_row(r, g);
+          bool keep = key < Tk;
+          if (MASK == CATOPT_MASK_CAUSAL) keep = keep & ((int64_t)key <= (int64_t)qrow + causal_off);
+          float add = 0.f;
+          if (MASK == CATOPT_MASK_BOOL || MASK == CATOPT_MASK_BIAS) {
+            const int qc = qrow < Tq ? qrow : Tq - 1;
+            const int kc = key < Tk ? key : Tk - 1;
+            const int64_t mi = (int64_t)qc * mask_ld + kc;
+            if (MASK == CATOPT_MASK_BOOL) keep = keep & (static_cast<const uint8_t*>(mask)[mi] != 0);
+            // the bias is in units of the scaled score; the running
+            // scores here are q·k, scaled at the exponential
+            if (MASK == CATOPT_MASK_BIAS) add = static_cast<const float*>(mask)[mi] * inv_scale;
+            keep = keep & (qrow < Tq);
+          }
+          s[r] = keep ? s[r] + add : -__builtin_inff();
+        }
+      };
+      // row max of a half (both lane halves), the true max, and the lazy
+      // move of the reference max; returns the factor for Oᵀ (1: no move)
+      auto half_max = [&](const f32x16& s) -> float {
+        float mt = -__builtin_inff();
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[r]);
+        {  // max with the other lane half, on the VALU (an LDS shuffle would
+           // wait behind the fragment reads in flight)
+          const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, mt),
+                                                           __builtin_bit_cast(uint32_t, mt), false, false);
+          mt = fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]), __builtin_bit_cast(float, (uint32_t)sw[1]));
+        }
+        m_true[0] = fmaxf(m_true[0], mt);
+        // move the reference max only when this half exceeds it by kLazy (log2 units)
+        float alpha = 1.f;
+        if (__builtin_amdgcn_ballot_w64((mt - m_run[0]) * c > kLazy) != 0) {
+          const float m_new = fmaxf(m_run[0], mt);
+          alpha = (m_run[0] == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f((m_run[0] - m_new) * c);
+          l_run[0] *= alpha;
+          m_run[0] = m_new;
+        }
+        return alpha;
+      };
+      auto rescale = [&](float alpha) {
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[db][0][r] *= alpha;
+      };
+      // p = exp2(s c - m c) as the bf16 B operand of PV, and its row sum
+      auto half_exp = [&](const f32x16& s, bf16x8* p) {
+        const float mc = (m_run[0] == -__builtin_inff()) ? 0.f : m_run[0] * c;
+        float lsum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c, -mc));
+          lsum += e;
+          p[r >> 3][r & 7] = static_cast<__bf16>(e);
+        }
+        l_run[0] += lsum;
+      };
+
+      f32x16 s0, s1;
+      bf16x8 p0[2], p1[2];
+      read_k(0);
+      read_k(1);
+      __builtin_amdgcn_s_setprio(1);
+      qk(0, s0);
+      __builtin_amdgcn_s_setprio(0);
+      if (need_mask) apply_mask(0, s0);
+      const float a0 = half_max(s0);
+      if (a0 != 1.f) rescale(a0);
+      // QK(1) + exp(0), and the Vᵀ fragments of half 0
+      __builtin_amdgcn_sched_barrier(0);
+      qk(1, s1);
+      half_exp(s0, p0);
+      read_v(0);
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // VALU
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // DS read
       }
+      pin(p0[0]);
+      pin(p0[1]);
+      pin(l_run[0]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (need_mask) apply_mask(1, s1);
+      const float a1 = half_max(s1);
+      // PV(0) + exp(1), and the Vᵀ fragments of half 1
+      __builtin_amdgcn_sched_barrier(0);
+      pv(0, p0);
+      half_exp(s1, p1);
+      read_v(1);
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // VALU
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // DS read
+      }
+      pin(p1[0]);
+      pin(p1[1]);
+      pin(l_run[0]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (a1 != 1.f) rescale(a1);
+      __builtin_amdgcn_s_setprio(1);
+      pv(1, p1);
     }
 
     __builtin_amdgcn_s_setprio(0);
     if (kvt + 1 < nkv) {
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
-      if ((kvt + 2) * KVB > Tk) {
-        zero_tail(kvt + 1, cur ^ 1);
-        __syncthreads();
-      }
     }
   };
   for (int kvt = 0; kvt < nkv; kvt += 2) {

@@ -101,4 +101,27 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_wave) {
                : "m0");
 }
 
+// One 1 KB global->LDS load through a buffer resource: lane l's 16 bytes at
+// byte `voff` of the buffer land at LDS byte address lds + 16 l (lds is
+// wave-uniform; it goes to M0).  A load past the resource's range returns
+// zeros.  The s_nop is the one wait state the hardware needs between an SALU
+// write of M0 and an LDS-DMA load reading it (the compiler cannot insert it
+// inside inline asm; without it the load can take the previous M0 and land in
+// another load's place).  Inline asm for the reason given at dma16.
+__device__ __forceinline__ void dma_buf(u32x4 rsrc, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :: "v"(voff), "s"(rsrc), "s"(lds) : "m0", "memory");
+}
+
+// Buffer resource (raw, stride 0) over `bytes` bytes from `base`.
+__device__ __forceinline__ u32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  u32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane((uint32_t)b);
+  r.y = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  r.z = __builtin_amdgcn_readfirstlane(bytes);
+  r.w = 0x00020000;
+  return r;
+}
+
 }  // namespace catopt

@@ -86,27 +86,6 @@ __device__ __forceinline__ constexpr int swz(int row, int chunk) {
   return row * ROW_BYTES + ((chunk ^ ((row >> 1) & 7)) << 4);
 }
 
-// One 1 KB global->LDS load: lane l's 16 bytes at byte `voff` of the buffer
-// land at LDS byte address lds + 16 l.  The s_nop is the one wait state the
-// hardware needs between an SALU write of M0 and an LDS-DMA load reading it
-// (the compiler cannot insert it inside inline asm; without it the load can
-// take the previous M0 and land in another load's place).
-__device__ __forceinline__ void dma(u32x4 rsrc, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-               :: "v"(voff), "s"(rsrc), "s"(lds) : "m0", "memory");
-}
-
-// Buffer resource (raw, stride 0) over `bytes` bytes from `base`.
-__device__ __forceinline__ u32x4 make_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t b = reinterpret_cast<uint64_t>(base);
-  u32x4 r;
-  r.x = __builtin_amdgcn_readfirstlane((uint32_t)b);
-  r.y = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
-  r.z = __builtin_amdgcn_readfirstlane(bytes);
-  r.w = 0x00020000;
-  return r;
-}
-
 // s_waitcnt with lgkmcnt(0) and vmcnt <= n (gfx9 encoding; expcnt not waited on).
 template <int n>
 __device__ __forceinline__ void wait_vm_lgkm0() {
@@ -300,7 +279,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_nt(
       wf[i] = *reinterpret_cast<const bf16x8*>(ws + wrow(i) * ROW_BYTES + frag[h]);
       xf[2 * i] = *reinterpret_cast<const bf16x8*>(xs + 32 * i * ROW_BYTES + frag[h]);
       xf[2 * i + 1] = *reinterpret_cast<const bf16x8*>(xs + (32 * i + 16) * ROW_BYTES + frag[h]);
-      dma(ls.rsrc, ls.off(ga, i, lchunk8), dst + blk + i * 1024);
+      dma_buf(ls.rsrc, ls.off(ga, i, lchunk8), dst + blk + i * 1024);
     }
     ls.advance(ga, wq, lane, lchunk8);
   };
@@ -391,10 +370,10 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_nt(
   };
 
   // ---- prologue: stage 0 (each wave its W and X rows) and X of stage 1
-  for (int i = 0; i < DMA_PER_PHASE; ++i) dma(st[0].rsrc, st[0].off(ga, i, lchunk8), w_slot(0, grp) + blk + i * 1024);
+  for (int i = 0; i < DMA_PER_PHASE; ++i) dma_buf(st[0].rsrc, st[0].off(ga, i, lchunk8), w_slot(0, grp) + blk + i * 1024);
   st[0].advance(ga, wq, lane, lchunk8);
   for (int p = 0; p < 2; ++p) {
-    for (int i = 0; i < DMA_PER_PHASE; ++i) dma(st[1].rsrc, st[1].off(ga, i, lchunk8), x_slot(p, 1 - grp) + blk + i * 1024);
+    for (int i = 0; i < DMA_PER_PHASE; ++i) dma_buf(st[1].rsrc, st[1].off(ga, i, lchunk8), x_slot(p, 1 - grp) + blk + i * 1024);
     st[1].advance(ga, wq, lane, lchunk8);
   }
   zero_acc();
