@@ -101,6 +101,15 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_wave) {
                : "m0");
 }
 
+// Direct global->LDS load of 4 bytes per lane (lane l's word lands at
+// lds_wave + 4 l), as dma16: inline asm, so the compiler neither waits for it
+// before unrelated LDS accesses nor counts it; callers wait with s_waitcnt
+// vmcnt before the barrier that publishes the data.
+__device__ __forceinline__ void dma4(const void* gptr, uint32_t lds_wave) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(gptr), "s"(lds_wave)
+               : "m0");
+}
+
 // One 1 KB global->LDS load through a buffer resource: lane l's 16 bytes at
 // byte `voff` of the buffer land at LDS byte address lds + 16 l (lds is
 // wave-uniform; it goes to M0).  A load past the resource's range returns

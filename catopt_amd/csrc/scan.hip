@@ -389,6 +389,153 @@ __global__ __launch_bounds__(kThreads, 2) void ssm_stream_lds(
   if (hf && dok) *reinterpret_cast<f32x4*>(hf + sidx) = h;
 }
 
+// --------------------------------------------------- register-staged streaming
+// The streaming schedule for a per-state a (N = 16) with a held in registers:
+// each thread's 16-byte slices of a for RSU steps go straight into one of
+// two register sets while the other set's steps run; the small x, b and c
+// streams go through LDS (one copy per workgroup) by direct loads issued
+// before a's, and y leaves through LDS as whole rows.  Every wave issues the
+// same memory operations in every stage with no branch around them, so the
+// waits the compiler derives for a are exact, and the wait at the end of a
+// stage leaves the RSU newest loads (the next stage's a) in flight across
+// the barrier: two stages of a (2 x RSU x 4 KB per workgroup) stay in
+// flight and no stage drains the memory pipeline.  On gfx9 stores count in
+// vmcnt too, which is why y is not stored step by step under a lane mask.
+// Steps past the last whole stage run unpipelined.  (The LDS-staged kernel
+// above waits for all its loads at every stage, which measured 5-14% slower
+// at C5's shape.)
+#ifndef CATOPT_SSM_RSU
+#define CATOPT_SSM_RSU 8
+#endif
+constexpr int RSU = CATOPT_SSM_RSU;  // steps per stage of the register-staged scan
+
+template <int N>
+struct SsmSmall {
+  static constexpr int TPD = N / 4, DPW = kThreads / TPD;
+  static constexpr int X_BYTES = RSU * DPW * 4;
+  static constexpr int V_BYTES = RSU * N * 4;   // b or c
+  static constexpr int STAGE = X_BYTES + 2 * V_BYTES;
+  static constexpr int Y_BYTES = RSU * DPW * 4;
+  static constexpr int BYTES = 2 * STAGE + 2 * Y_BYTES;
+  static constexpr int XPT = RSU * DPW / kThreads;         // x loads (and y stores) per thread
+  static constexpr int VPT = 2 * RSU * N / kThreads;       // b and c loads per thread
+  static_assert(RSU * DPW % kThreads == 0 && 2 * RSU * N % kThreads == 0, "whole waves per small stream");
+  static_assert(RSU * N % 64 == 0, "b and c slots in whole waves");
+};
+
+template <int N>
+__global__ __launch_bounds__(kThreads, 2) void ssm_stream_reg(
+    const float* __restrict__ a, const float* __restrict__ bx, const float* __restrict__ c,
+    const float* __restrict__ x, const float* __restrict__ h0, int64_t T, int64_t D,
+    float* __restrict__ y, float* __restrict__ hf) {
+  using L = SsmSmall<N>;
+  __shared__ __attribute__((aligned(16))) char lds[L::BYTES];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t b = blockIdx.y;
+  const int64_t d0 = (int64_t)blockIdx.x * L::DPW;
+  const int ch = tid / L::TPD, n0 = (tid % L::TPD) * 4;
+  const int64_t d = d0 + ch;
+  const bool dok = d < D;
+  const int64_t a_lane = (((dok ? d : D - 1) * N) + n0);
+  const int64_t nfull = T / RSU;
+  // this thread's small-stream slots: x (u, channel) for two slots; b (waves
+  // 0, 1) or c (waves 2, 3) for one (u, n) slot, clamped to valid rows
+  int xu[L::XPT], xc[L::XPT];
+#pragma unroll
+  for (int i = 0; i < L::XPT; ++i) {
+    const int s = i * kThreads + tid;
+    xu[i] = s / L::DPW;
+    xc[i] = (int)(d0 + s % L::DPW < D ? s % L::DPW : D - 1 - d0);
+  }
+
+  const uint32_t lds0 = lds_u32(lds);
+  auto issue_small = [&](int64_t st, int stage) {
+    const uint32_t xb = lds0 + stage * L::STAGE;
+    const int64_t t0 = st * RSU;
+#pragma unroll
+    for (int i = 0; i < L::XPT; ++i)
+      dma4(x + (b * T + t0 + xu[i]) * D + d0 + xc[i], xb + (i * kThreads + wave * 64) * 4);
+    // b then c, one 4-byte slot per lane: slots [0, RSU*N) of b, then of c
+#pragma unroll
+    for (int i = 0; i < L::VPT; ++i) {
+      const int s = i * kThreads + tid;
+      const bool is_c = s >= RSU * N;              // wave-uniform: RSU*N is a multiple of 64
+      const int vs = is_c ? s - RSU * N : s;
+      dma4((is_c ? c : bx) + (b * T + t0 + vs / N) * N + vs % N,
+           __builtin_amdgcn_readfirstlane(xb + L::X_BYTES + (is_c ? L::V_BYTES : 0) + (vs & ~63) * 4));
+    }
+  };
+  auto load_a = [&](int64_t st, f32x4* ra) {
+    const int64_t t0 = st * RSU;
+#pragma unroll
+    for (int u = 0; u < RSU; ++u)
+      ra[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(a + ((b * T + t0 + u) * D) * N + a_lane));
+  };
+
+  f32x4 h = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int64_t sidx = (b * D + (dok ? d : 0)) * N + n0;
+  if (h0 && dok) h = *reinterpret_cast<const f32x4*>(h0 + sidx);
+  auto compute = [&](int stage, const f32x4* ra, char* yb) {
+    const char* xb = lds + stage * L::STAGE;
+    const char* vb = xb + L::X_BYTES;
+#pragma unroll
+    for (int u = 0; u < RSU; ++u) {
+      const f32x4 bv = *reinterpret_cast<const f32x4*>(vb + (u * N + n0) * 4);
+      const f32x4 cv = *reinterpret_cast<const f32x4*>(vb + L::V_BYTES + (u * N + n0) * 4);
+      const float xv = *reinterpret_cast<const float*>(xb + (u * L::DPW + ch) * 4);
+      h = ra[u] * h + bv * xv;
+      const f32x4 chv = cv * h;
+      const float r = lane_reduce<N>(chv[0] + chv[1] + chv[2] + chv[3]);
+      if (n0 == 0) *reinterpret_cast<float*>(yb + (u * L::DPW + ch) * 4) = r;
+    }
+  };
+  // y rows of a stage from LDS: row u, channels d0 .. d0 + DPW - 1
+  auto store_y = [&](int64_t st, const char* yb) {
+#pragma unroll
+    for (int i = 0; i < L::XPT; ++i) {
+      // a channel past D (last, partial workgroup) writes channel D - 1's
+      // value to it again: no lane mask around the store
+      const int u = (i * kThreads + tid) / L::DPW;
+      const int cc = xc[i];  // the clamped channel of slot i
+      y[(b * T + st * RSU + u) * D + d0 + cc] = *reinterpret_cast<const float*>(yb + (u * L::DPW + cc) * 4);
+    }
+  };
+  char* ybuf0 = lds + 2 * L::STAGE;
+  char* ybuf1 = ybuf0 + L::Y_BYTES;
+  auto step = [&](int64_t st, int buf, f32x4* cur, f32x4* nxt) {
+    const int64_t sn = st + 1 < nfull ? st + 1 : nfull - 1;  // the last stage reloads itself
+    issue_small(sn, buf ^ 1);
+    load_a(sn, nxt);
+    char* yb = buf ? ybuf1 : ybuf0;
+    compute(buf, cur, yb);
+    __builtin_amdgcn_s_waitcnt((RSU & 15) | (7 << 4) | ((RSU >> 4) << 14));  // vmcnt <= RSU, lgkmcnt 0
+    __syncthreads();
+    store_y(st, yb);
+  };
+  f32x4 ra0[RSU], ra1[RSU];
+  if (nfull > 0) {
+    issue_small(0, 0);
+    load_a(0, ra0);
+    __builtin_amdgcn_s_waitcnt((RSU & 15) | (7 << 4) | ((RSU >> 4) << 14));
+    __syncthreads();
+    for (int64_t st = 0; st < nfull; st += 2) {
+      step(st, 0, ra0, ra1);
+      if (st + 1 < nfull) step(st + 1, 1, ra1, ra0);
+    }
+  }
+  // steps past the last whole stage
+  for (int64_t t = nfull * RSU; t < T; ++t) {
+    SsmStep<N, true> sp;
+    ssm_load(sp, a, bx, c, x, b, t, T, D, dok ? d : 0, n0);
+    h = sp.a * h + sp.bx * sp.x;
+    const f32x4 chv = sp.c * h;
+    const float r = lane_reduce<N>(chv[0] + chv[1] + chv[2] + chv[3]);
+    if (dok && n0 == 0) y[(b * T + t) * D + d] = r;
+  }
+  if (hf && dok) *reinterpret_cast<f32x4*>(hf + sidx) = h;
+}
+
 // Lanes that fill the GPU: 256 CUs x 8 waves x 64 lanes.
 constexpr int64_t kFillThreads = 256LL * 8 * 64;
 
@@ -421,6 +568,13 @@ int32_t ssm_launch(int64_t B, int64_t T, int64_t D, const float* a, const float*
   static_assert(SsmLayout<N>::TPD == N / 4, "ssm_threads assumes four states per thread");
   const bool chunked = ssm_chunked(B, D, N, nc, schedule);
   if (gx > 0x7fffffff || B > 65535 || nc > 65535) return CATOPT_E_UNSUPPORTED;
+  if constexpr (N == 16) {
+    if (!chunked && APS) {
+      ssm_stream_reg<N><<<dim3((uint32_t)gx, (uint32_t)B), dim3(kThreads), 0, s>>>(a, bx, c, x, h0, T, D, y, hf);
+      CATOPT_LAUNCH_CHECK();
+      return CATOPT_OK;
+    }
+  }
   if (!chunked && APS) {
     static bool attr_done = false;
     if (!attr_done) {

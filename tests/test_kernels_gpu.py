@@ -361,3 +361,25 @@ def test_empty_inputs(dev):
     e = torch.zeros(0, 1, device=dev)
     mc, lc, ac = K.om_compose((e, e, torch.zeros(0, 4, device=dev)), (e, e, torch.zeros(0, 4, device=dev)))
     assert mc.shape == (0, 1) and ac.shape == (0, 4)
+
+
+@pytest.mark.parametrize("nbytes", [16, 4096, (1 << 20) + 48, 64 << 20])
+def test_hbm_read_reads_every_word(dev, nbytes):
+    """The read stream's sink is written only when some lane's XOR of the
+    words it read equals the sentinel: with one sentinel word in zeros, at the
+    start, the middle or the end of the buffer, the sink is written (that word
+    was read); with none, it is not."""
+    SENT = 0x9E3779B9
+    n32 = nbytes // 4
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    buf = torch.zeros(n32, dtype=torch.int32, device=dev)
+    K.hbm_read(buf, sink)
+    torch.cuda.synchronize()
+    assert int(sink.item()) == 0
+    for pos in sorted({0, n32 // 2, n32 - 1}):
+        buf.zero_()
+        buf[pos] = torch.tensor(SENT, dtype=torch.int64).to(torch.int32)
+        sink.zero_()
+        K.hbm_read(buf, sink)
+        torch.cuda.synchronize()
+        assert int(sink.item()) & 0xFFFFFFFF == SENT, (nbytes, pos)
