@@ -74,6 +74,7 @@ constexpr int OFF_X = OFF_SF + 2 * SF_BYTES;       // two exchange buffers (chun
 constexpr int LDS_BYTES = OFF_X + 2 * X_BYTES;
 static_assert(NSTAGE >= 2 && LDS_BYTES <= 160 * 1024, "LDS ring does not fit");
 constexpr int LOADS_PER_CHUNK = 9;  // global->LDS instructions per thread per chunk
+constexpr int OUT_STORES = 4;       // global stores of one chunk's output per thread (waves kb = 0)
 
 // s_waitcnt: vmcnt <= n, lgkmcnt = 0, expcnt not waited on (gfx9 encoding).
 template <int n>
@@ -316,9 +317,13 @@ __global__ __launch_bounds__(NT, 1) void retention_scan(
     for (int r4 = 0; r4 < 4; ++r4)
       *reinterpret_cast<u32x2*>(lds + sf_own + (1 - par) * SF_BYTES + r4 * 512) =
           u32x2{pack_bf16x2(S[4 * r4], S[4 * r4 + 1]), pack_bf16x2(S[4 * r4 + 2], S[4 * r4 + 3])};
-    // loads complete in issue order: all but the newest NSTAGE-2 groups means
-    // chunk ci+1's tiles have landed (earlier stores were issued before them)
-    wait_vm_lgkm0<LOADS_PER_CHUNK * (NSTAGE - 2)>();
+    // vmcnt counts loads and stores in issue order: chunk ci+1's tiles have
+    // landed once no more than chunk ci+2's loads (issued at the top of this
+    // chunk) and the output stores issued after them remain
+    if (KB == 0 && ci > 0)
+      wait_vm_lgkm0<LOADS_PER_CHUNK * (NSTAGE - 2) + OUT_STORES>();
+    else
+      wait_vm_lgkm0<LOADS_PER_CHUNK * (NSTAGE - 2)>();
     __syncthreads();  // next chunk's tiles, S fragments and this chunk's exchange in place
   };
   auto run = [&](auto kb_tag, auto diag_tag) {
