@@ -367,9 +367,12 @@ RETENTION_HEAD_DIM = 128
 def retention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma: torch.Tensor,
               scale: float = 1.0) -> torch.Tensor:
     """``scale * Σ_{s<=t} γ_h^(t-s) (q_t·k_s) v_s`` for ``q, k (B,H,T,dk)``,
-    ``v (B,H,T,dv)`` bf16, ``dk, dv <= 128`` (below 128 they run zero-padded
-    to the kernel's 128: zero columns leave q·k unchanged and add zero output
-    columns, dropped)."""
+    ``v (B,H,T,dv)`` bf16, ``dk, dv <= 128``.  Below 128 the heads run
+    zero-padded to the kernel's 128 (zero columns leave q·k unchanged and add
+    zero output columns, dropped); a ``T`` that is not a multiple of the
+    kernel's 64-step chunk runs zero-padded at the end of the time axis (the
+    sum is causal, so the padded steps change no output row before them;
+    their rows are dropped)."""
     _need_device(q, k, v, gamma)
     lib = L.load()
     if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
@@ -378,14 +381,16 @@ def retention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma: torch.Te
         raise ValueError("retention operands must be q, k (B, H, T, dk) and v (B, H, T, dv)")
     B, H, T, d = q.shape
     dv = v.shape[-1]
-    if max(d, dv) > RETENTION_HEAD_DIM or T % RETENTION_CHUNK:
-        raise NotImplementedError(f"HIP retention needs dk, dv <= {RETENTION_HEAD_DIM} and "
-                                  f"T % {RETENTION_CHUNK} == 0")
-    if d < RETENTION_HEAD_DIM or dv < RETENTION_HEAD_DIM:
+    if max(d, dv) > RETENTION_HEAD_DIM:
+        raise NotImplementedError(f"HIP retention needs dk, dv <= {RETENTION_HEAD_DIM}")
+    if T == 0 or B * H == 0:
+        return torch.zeros_like(v)
+    pk, pv, pt = RETENTION_HEAD_DIM - d, RETENTION_HEAD_DIM - dv, (-T) % RETENTION_CHUNK
+    if pk or pv or pt:
         pad = torch.nn.functional.pad
-        q, k = (pad(t, (0, RETENTION_HEAD_DIM - d)) if d < RETENTION_HEAD_DIM else t for t in (q, k))
-        v = pad(v, (0, RETENTION_HEAD_DIM - dv)) if dv < RETENTION_HEAD_DIM else v
-        return retention(q, k, v, gamma, scale)[..., :dv]
+        q, k = (pad(t, (0, pk, 0, pt)) for t in (q, k))
+        v = pad(v, (0, pv, 0, pt))
+        return retention(q, k, v, gamma, scale)[..., :T, :dv]
     d = RETENTION_HEAD_DIM
     g = gamma.to(torch.float32).reshape(-1).contiguous()
     if g.numel() != H:

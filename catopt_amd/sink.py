@@ -140,7 +140,8 @@ class HipSink:
             ("om_decayed_chunked", ExecutorSpec(
                 "om_decayed_chunked", planned(HipChunkedDecayModule), is_decayed_term,
                 lambda m: bool(getattr(m, "is_batched", False)),
-                (frozenset({"concat", "om_decayed"}), frozenset({"add", "mul", "matmul", "split"}),
+                (frozenset({"concat", "om_decayed"}),
+                 frozenset({"add", "mul", "div", "matmul", "split", "transpose", "unsqueeze"}),
                  frozenset({"decay", "decay_vec"})))),
             ("scan", ExecutorSpec(
                 "scan", planned(HipScanModule), is_scan_term,
