@@ -528,10 +528,11 @@ def build_om_plan(root: Any, eval_mod: HipIRModule) -> dict | None:
     plan_leaves = []
     for leaf in leaves:
         if is_op(leaf, "om", 3):
-            plan_leaves.append({"kind": "om", "m": leaf.args[0], "l": leaf.args[1], "a": leaf.args[2]})
+            plan_leaves.append({"kind": "om", "term": leaf, "m": leaf.args[0], "l": leaf.args[1],
+                                "a": leaf.args[2]})
             continue
         s, v = leaf.args
-        lf: dict = {"kind": "scores", "s": s, "v": v}
+        lf: dict = {"kind": "scores", "term": leaf, "s": s, "v": v}
         sc = parse_score(s)
         # the kernels track the row max of q·k and scale it, which is the max
         # of the scaled scores only for a positive scale
@@ -657,8 +658,13 @@ class HipOMModule(HipExecutorBase, nn.Module):
             if o is not None:
                 return o
         carriers, out_dtype = [], None
+        # a leaf shared in the DAG runs once and enters the reduction once per
+        # occurrence (the multiplicity repeat of om_lower.py:642-655)
+        done: dict = {}
         for lf in leaves:
-            f, dt = self._carrier(lf, ev)
+            if lf["term"] not in done:
+                done[lf["term"]] = self._carrier(lf, ev)
+            f, dt = done[lf["term"]]
             carriers.append(f)
             out_dtype = dt if out_dtype is None else torch.promote_types(out_dtype, dt)
         carriers = _broadcast_carriers(carriers)
