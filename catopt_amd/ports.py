@@ -20,6 +20,7 @@ the records with the same field names and meaning instead of importing them:
 from __future__ import annotations
 
 import enum
+import math
 from dataclasses import dataclass, field
 from typing import Any, Callable, Protocol, runtime_checkable
 
@@ -86,8 +87,10 @@ class LowerResult:
 
 
 class FailureClass(str, enum.Enum):
-    """Failure buckets (failures.py:34-60)."""
+    """Failure buckets (failures.py:34-47); ``OK`` is the no-failure
+    sentinel and :func:`classify` never returns it."""
 
+    OK = "ok"
     OOM = "oom"
     TIMEOUT = "timeout"
     KERNEL = "kernel"
@@ -96,27 +99,38 @@ class FailureClass(str, enum.Enum):
     UNKNOWN = "unknown"
 
 
+def is_nonfinite(value: float) -> bool:
+    """A NaN or infinite measurement (failures.py:125-135): the NONFINITE
+    check a caller applies to a measured result."""
+    return not math.isfinite(value)
+
+
 def classify(exc: BaseException) -> FailureClass:
-    """Bucket an exception the way failures.py:62-123 does."""
+    """Bucket an exception with the precedence of failures.py:74-122, first
+    match wins: a process-control signal is re-raised; ``MemoryError`` or an
+    "out of memory" / "oom" message is OOM; ``TimeoutError`` or a "timed
+    out" / "timeout" message is TIMEOUT; a message naming a device as
+    unavailable is UNAVAILABLE (it outranks KERNEL, so "no CUDA device"
+    reads as a feasibility gap); a "cuda" / "device-side" / "kernel"
+    message is KERNEL; anything else UNKNOWN.  This library's own errors
+    classify by type first: a missing or mismatched library is UNAVAILABLE,
+    a failed entry point KERNEL; a HIP runtime error text ("hip error",
+    "hiperror…") counts as a kernel message like a CUDA one."""
     from . import _lib
 
+    if isinstance(exc, (KeyboardInterrupt, SystemExit)):
+        raise exc
     if isinstance(exc, _lib.HipExtensionMissing):
         return FailureClass.UNAVAILABLE
     if isinstance(exc, _lib.HipKernelError):
         return FailureClass.KERNEL
-    if isinstance(exc, MemoryError):
+    msg = str(exc).lower()
+    if isinstance(exc, MemoryError) or "out of memory" in msg or "oom" in msg:
         return FailureClass.OOM
-    if isinstance(exc, TimeoutError):
+    if isinstance(exc, TimeoutError) or "timed out" in msg or "timeout" in msg:
         return FailureClass.TIMEOUT
-    text = f"{type(exc).__name__}: {exc}".lower()
-    if "out of memory" in text or "outofmemory" in text:
-        return FailureClass.OOM
-    if "timed out" in text or "timeout" in text:
-        return FailureClass.TIMEOUT
-    if "nan" in text and "finite" in text:
-        return FailureClass.NONFINITE
-    if "hip" in text or "cuda" in text or "kernel" in text:
-        return FailureClass.KERNEL
-    if "not available" in text or "unavailable" in text:
+    if "device" in msg and ("not available" in msg or "unavailable" in msg or "no cuda" in msg):
         return FailureClass.UNAVAILABLE
+    if "cuda" in msg or "device-side" in msg or "kernel" in msg or "hip error" in msg or "hiperror" in msg:
+        return FailureClass.KERNEL
     return FailureClass.UNKNOWN

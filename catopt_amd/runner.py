@@ -36,13 +36,16 @@ class HipGraphRunner:
         stats["cuda_graph"] = False
         xs = tuple(example_input) if isinstance(example_input, (tuple, list)) else (example_input,)
         capture = getattr(module, "capture_cuda_graph", None)
+        # the capture copies every input into a static device buffer, so all
+        # of them (not only the first, as runners.py:66-72 checks) must be
+        # device tensors; a planned executor whose plan is None declines
+        # inside its own capture_cuda_graph
         if capture is None or not xs or not all(isinstance(t, torch.Tensor) and t.device.type == "cuda" for t in xs):
-            return module
-        if getattr(module, "_plan", None) is None:
             return module
         try:
             capture(*xs)
-            stats["cuda_graph"] = bool(getattr(module, "is_graph_captured", False))
+            # a module reporting its capture state is taken at its report
+            stats["cuda_graph"] = bool(getattr(module, "is_graph_captured", True))
         except Exception as exc:
             stats["cuda_graph_failure"] = classify(exc)
             module.drop_cuda_graph()
