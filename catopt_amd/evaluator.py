@@ -186,8 +186,12 @@ class HipIRModule(nn.Module):
         self._buf_names: dict[str, str] = {}
         values = dict(param_values or {})
         for p in ir.params.values() if isinstance(ir.params, dict) else ir.params:
-            if p.name not in values:
-                raise KeyError(f"no value given for Param {p.name!r}")
+            shape = getattr(getattr(p, "typ", None), "shape", None)
+            if p.name not in values and shape is not None:
+                # no value given: a random init, unknown extents taken as 1
+                # (torch_bridge.py:2722-2764); a Param of unknown rank stays
+                # unbound and raises when evaluated
+                values[p.name] = torch.randn(*[1 if d is None else int(d) for d in shape]) * 0.02
         for name, v in values.items():
             t = torch.as_tensor(v)
             if device is not None:
@@ -228,6 +232,39 @@ class HipIRModule(nn.Module):
         # picked up), straight from the buffer dict rather than through
         # nn.Module.__getattr__, which costs microseconds per name
         return _BufferParams(self._buffers, self._buf_names)
+
+    # The parameters live in non-persistent buffers under attribute-safe
+    # names; the state dict speaks the IR's Param names instead, as the
+    # reference's modules do (torch_bridge.py:2722-2764: one entry per live
+    # Param, fused ones included).  Loading copies into the existing buffers,
+    # so a captured graph, which baked their addresses, sees the new values.
+
+    def _save_to_state_dict(self, destination, prefix, keep_vars):
+        for name, attr in self._buf_names.items():
+            t = self._buffers[attr]
+            destination[prefix + name] = t if keep_vars else t.detach()
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
+                              unexpected_keys, error_msgs):
+        for name, attr in self._buf_names.items():
+            key = prefix + name
+            if key not in state_dict:
+                missing_keys.append(key)
+                continue
+            buf, v = self._buffers[attr], state_dict[key]
+            if not isinstance(v, torch.Tensor) or tuple(v.shape) != tuple(buf.shape):
+                error_msgs.append(f"size mismatch for {key}: copying a param with shape "
+                                  f"{tuple(getattr(v, 'shape', ()))}, the shape in current model is "
+                                  f"{tuple(buf.shape)}.")
+                continue
+            with torch.no_grad():
+                buf.copy_(v)
+        if strict:
+            for key in state_dict:
+                if key.startswith(prefix):
+                    head = key[len(prefix):].split(".", 1)
+                    if (head[0] not in self._modules) if len(head) > 1 else (head[0] not in self._buf_names):
+                        unexpected_keys.append(key)
 
     def _pv(self, t: Any) -> torch.Tensor | None:
         if _is_param(t) and t.name in self._buf_names:

@@ -248,3 +248,34 @@ def test_ssm_readout_executor(sink, dev, N, per_state, dtype):
         ins = inputs()
     mod = res.module
     assert mod.fallbacks == 0 and (mod.fused_readouts > 0) == (N != 3)
+
+
+def test_load_state_dict_reaches_a_captured_graph(sink, dev):
+    # parameters load in place, so a graph that baked their addresses
+    # replays with the new values: the generic module (C1's fused chain) and
+    # a planned executor (the extracted decayed form, its projections inside)
+    from tests.decayed_terms import DecayedTerms
+
+    torch.manual_seed(3)
+    layers = [torch.nn.Linear(64, 64) for _ in range(3)]
+    vals = {}
+    for i, lyr in enumerate(layers):
+        vals[f"W{i + 1}"], vals[f"b{i + 1}"] = lyr.weight.detach().to(dev), lyr.bias.detach().to(dev)
+    ir, _ = forms.weight_chain_form(3, 64, 16)
+    x = torch.randn(16, 64, device=dev)
+    b = DecayedTerms(B=1, K=4, C=64, D=64, heads=2)
+    dvals, dx = b.values(dtype=torch.bfloat16, seed=4, gamma_dtype=torch.float32)
+    cases = [(ir, vals, x), (b.ir(b.root()), {n: t.to(dev) for n, t in dvals.items()}, dx.to(dev))]
+    for ir_, vals_, x_ in cases:
+        res = deliver(ir_, vals_, sink, (x_,), runner=HipGraphRunner())
+        mod = res.module
+        assert res.stats["cuda_graph"] is True and mod.is_graph_captured
+        before = mod(x_).clone()
+        sd = mod.state_dict()
+        mod.load_state_dict({k: v * 0.5 for k, v in sd.items()})
+        replayed = mod(x_).clone()
+        mod.drop_cuda_graph()
+        eager = mod(x_)
+        torch.cuda.synchronize()
+        assert not torch.allclose(replayed.float(), before.float())
+        _gate(_np(eager), replayed, 1e-6)
