@@ -456,6 +456,10 @@ class HipIRModule(nn.Module):
         return getattr(self, "_graph", None) is not None
 
     def capture_cuda_graph(self, *example_inputs: torch.Tensor, warmup: int = 3) -> "HipIRModule":
+        """Record the forward into a hipGraph; returns ``self`` (a no-op
+        without a device)."""
+        if not torch.cuda.is_available():
+            return self
         self._graph, self._graph_inputs, self._graph_out, self._graph_sig = record_graph(
             self._forward_impl, example_inputs, warmup)
         return self

@@ -65,8 +65,10 @@ class HipExecutorBase:
         return self.eval_mod._param_map
 
     def capture_cuda_graph(self, *example_inputs: torch.Tensor, warmup: int = 3):
-        """Record the planned forward into a hipGraph; returns ``self``."""
-        if self._plan is None:
+        """Record the planned forward into a hipGraph; returns ``self``.  A
+        no-op without a device or without a plan; host inputs on a machine
+        with a device raise ``ValueError`` (executors/base.py:180-220)."""
+        if self._plan is None or not torch.cuda.is_available():
             return self
         self._graph, self._graph_inputs, self._graph_out, self._graph_sig = record_graph(
             self._forward_impl, example_inputs, warmup)

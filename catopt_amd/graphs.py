@@ -21,7 +21,7 @@ def record_graph(fn: Callable, example_inputs: tuple, warmup: int = 3) -> tuple:
 
     Returns ``(graph, static_inputs, static_output, signature)``."""
     if not all(isinstance(t, torch.Tensor) and t.device.type == "cuda" for t in example_inputs):
-        raise ValueError("graph capture requires device inputs")
+        raise ValueError("graph capture requires device inputs (CUDA/HIP tensors)")
     static_ins = [t.detach().clone() for t in example_inputs]
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
