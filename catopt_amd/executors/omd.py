@@ -780,7 +780,16 @@ class HipOmdModule(HipExecutorBase, nn.Module):
                 raise _Decline()
             e = (m, lv, num)
             if state is not None and (state[0].shape != m.shape or state[2].shape != num.shape):
-                raise _Decline()
+                # carriers that broadcast against each other (a leaf of one
+                # query row beside a leaf of several): compose at the common
+                # shape, as the serial _omd_compose broadcasts
+                # (omd_lower.py:1006-1011); shapes that do not broadcast raise
+                # and the generic module runs
+                ms = torch.broadcast_shapes(state[0].shape, m.shape)
+                ns = torch.broadcast_shapes(state[2].shape, num.shape)
+                state = (state[0].expand(ms).contiguous(), state[1].expand(ms).contiguous(),
+                         state[2].expand(ns).contiguous())
+                e = (m.expand(ms).contiguous(), lv.expand(ms).contiguous(), num.expand(ns).contiguous())
             state = e if state is None else _om_compose(state, e)
         m, lv, num = state
         fa = num[..., :width].reshape(*num.shape[:-1], *tail)
