@@ -218,3 +218,73 @@ def test_decode_step_in_a_hip_graph(dev):
         for x, y in zip(st_out, eager):
             assert torch.equal(x, y), rep
         _gate(_dense(q.cpu(), [k0.cpu(), kn.cpu()], [v0.cpu(), vn.cpu()]), om_apply_state(st_out), TOL_BF16)
+
+
+def _chunked_kv_ir(B, H, Tq, d, dv, Tkv, C):
+    n = Tkv // C
+    q = Var("q", TensorType((B, H, Tq, d)))
+    Kv = Var("K", TensorType((B, H, n * C, d)))
+    Vv = Var("V", TensorType((B, H, n * C, dv)))
+    leaves = [mk("om_elem", mk("matmul", q, mk("transpose", mk("chunk", Kv, chunks=n, dim=-2, index=i),
+                                                dim0=-2, dim1=-1)),
+                 mk("chunk", Vv, chunks=n, dim=-2, index=i)) for i in range(n)]
+    return IR(mk("om_apply", _balanced(leaves)), [q, Kv, Vv])
+
+
+def _peak_bytes(fn):
+    """Device bytes allocated during ``fn`` beyond what was live before."""
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    fn()
+    torch.cuda.synchronize()
+    return torch.cuda.max_memory_allocated() - base
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_streaming_peak_memory_is_flat_in_the_key_count(dev, dtype):
+    # the reference's test_om_stream.py:368-401 shapes: the fold's working
+    # set tracks the block, not the key count (8 blocks, then 16)
+    B, H, Tq, d, dv, C = 1, 8, 32, 64, 64, 2048
+    peaks = []
+    for Tkv in (16384, 32768):
+        mod = to_streaming_om_module(_chunked_kv_ir(B, H, Tq, d, dv, Tkv, C))
+        q = torch.randn(B, H, Tq, d, device=dev).to(dtype)
+        K = torch.randn(B, H, Tkv, d, device=dev).to(dtype)
+        V = torch.randn(B, H, Tkv, dv, device=dev).to(dtype)
+        mod(q, K, V)  # first call outside the measurement (library workspaces)
+        peaks.append(_peak_bytes(lambda: mod(q, K, V)))
+        del q, K, V
+    s1, s2 = peaks
+    assert s2 < s1 * 1.5 + 4 * 2 ** 20, peaks
+    # and far below one block-set of scores over every key
+    assert s2 < B * H * Tq * 32768 * 4 // 4, peaks
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_streaming_where_the_full_scores_would_be_half_a_gib(dev, dtype):
+    # the reference's test_om_stream.py:404-426: T_kv = 262144, whose full
+    # score matrix is 512 MiB in fp32; the fold needs about one block
+    B, H, Tq, d, dv, C = 1, 8, 64, 64, 64, 4096
+    Tkv = 262144
+    mod = to_streaming_om_module(_chunked_kv_ir(B, H, Tq, d, dv, Tkv, C))
+    q = (torch.randn(B, H, Tq, d, device=dev) * 0.125).to(dtype)
+    K = torch.randn(B, H, Tkv, d, device=dev).to(dtype)
+    V = torch.randn(B, H, Tkv, dv, device=dev).to(dtype)
+    mod(q, K, V)  # first call outside the measurement (library workspaces)
+    out = None
+
+    def run():
+        nonlocal out
+        out = mod(q, K, V)
+
+    peak = _peak_bytes(run)
+    score_bytes = B * H * Tq * Tkv * 4
+    assert peak < score_bytes // 8, (peak, score_bytes)
+    # the result on a sample of heads and rows against the dense softmax
+    for h in (0, 5):
+        s = q[0, h, ::16].double() @ K[0, h].double().T
+        ref = torch.softmax(s, dim=-1) @ V[0, h].double()
+        rep = oracle.verify_equiv(ref.cpu().numpy(), _np(out[0, h, ::16]), rtol=TOL_BF16 if dtype == torch.bfloat16 else TOL_F32)
+        assert rep["passed"], rep
