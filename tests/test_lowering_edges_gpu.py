@@ -172,3 +172,20 @@ def test_omd_packaging_leaf_and_broadcasting_leaves(sink, dev):
     params2 = {"s1": _rand((3, 4), 1), "s2": _rand((1, 4), 2), "a1": _rand((4, d), 3), "b1": _rand((4, d), 4),
                "a2": _rand((4, d), 5), "b2": _rand((4, d), 6)}
     _check(sink, dev, ir2, params2, [_rand((d,), 7)], torch.float32, "omd_batched")
+
+
+def test_a_bare_affine_compose_root_returns_the_map(sink, dev):
+    # no apply above the tree (tests/test_scan_batched.py:271-302): not a
+    # scan root; the generic module returns the composed (A, b) pair,
+    # (A, x1) ∘ (A, x0) = (A A, A x0 + x1)
+    d = 8
+    A, x = Param("p_a", TensorType((d, d))), Var("x", TensorType((4, d)))
+    bare = mk("aff_compose", mk("aff", A, mk("select", x, dim=0, index=1)), mk("aff", A, mk("select", x, dim=0, index=0)))
+    Av, xv = _rand((d, d), 1, 0.3), _rand((4, d), 2)
+    res = deliver(IR(bare, [x]), {"p_a": Av.float().to(dev)}, sink, (xv.float().to(dev),))
+    assert not getattr(res.module, "is_batched", False)
+    out = res.module(xv.float().to(dev))
+    assert isinstance(out, tuple) and len(out) == 2
+    for r, o in zip((Av @ Av, Av @ xv[0] + xv[1]), out):
+        rep = oracle.verify_equiv(r.numpy(), o.detach().cpu().double().numpy(), rtol=1e-5)
+        assert rep["passed"], rep
