@@ -79,11 +79,16 @@ class VerifyReport:
 
 @dataclass
 class LowerResult:
-    """A delivered module, its stats and the verify outcome (pipeline.py:217)."""
+    """A delivered module, its stats and the verify outcome
+    (pipeline.py:217-241); unpacks as ``(module, stats)``."""
 
     module: Any
     stats: dict = field(default_factory=dict)
     verified: Any = None
+
+    def __iter__(self):
+        yield self.module
+        yield self.stats
 
 
 class FailureClass(str, enum.Enum):

@@ -24,7 +24,16 @@ import torch
 
 from .ports import classify
 
-__all__ = ["HipGraphRunner"]
+__all__ = ["HipGraphRunner", "IdentityRunner"]
+
+
+class IdentityRunner:
+    """The default delivery: the routed executor as it is."""
+
+    name = "identity"
+
+    def apply(self, module: torch.nn.Module, example_input: Any, stats: dict) -> torch.nn.Module:
+        return module
 
 
 class HipGraphRunner:

@@ -49,6 +49,7 @@ from .executors import (
 )
 from .ir import IR
 from .ports import ExecutorSpec, LowerResult, VerifyReport, classify
+from .runner import IdentityRunner
 
 __all__ = ["HipSink", "verify_equiv", "verify_module", "route_spec", "lower_extracted", "deliver"]
 
@@ -226,8 +227,13 @@ def deliver(ir: IR, params: dict | None, sink: Any, example_inputs: Any = None, 
         stats["hip_calls"] = L.call_count() - n_hip
         stats["torch_fallback_ops"] = torch_fallback_count() - n_torch
         stats["hip_kernel"] = stats["hip_calls"] > 0
-    if runner is not None and example_inputs is not None:
-        stats["runner"] = getattr(runner, "name", type(runner).__name__)
+    # the runner's name is recorded even when no input lets it run
+    # (optimize.py:2340-2372: identity by default, the member names of a chain)
+    if runner is None:
+        runner = IdentityRunner()
+    names = getattr(runner, "names", None)
+    stats["runner"] = list(names) if names is not None else getattr(runner, "name", type(runner).__name__)
+    if example_inputs is not None:
         module = runner.apply(module, example_inputs, stats)
     verified = None
     if verify_ir is not None and example_inputs is not None:

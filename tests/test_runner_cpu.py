@@ -88,3 +88,30 @@ def test_failure_classes_follow_the_reference_precedence():
     with pytest.raises(SystemExit):
         classify(SystemExit(1))
     assert is_nonfinite(float("nan")) and is_nonfinite(float("-inf")) and not is_nonfinite(1.0)
+
+
+def test_delivery_records_its_runner_and_unpacks():
+    # optimize.py:2340-2372 and pipeline.py:238-241: the runner's name is
+    # always recorded (identity by default, member names for a chain), and
+    # the result unpacks as (module, stats)
+    from catopt_amd import forms
+    from catopt_amd.runner import IdentityRunner
+    from catopt_amd.sink import HipSink, deliver
+    from tests.cpu_table import cpu_table
+
+    sink = HipSink(device="cpu", ops=cpu_table())
+    ir, _ = forms.scan_final_form(4, (2,))
+    res = deliver(ir, {}, sink)
+    mod, stats = res
+    assert mod is res.module and stats is res.stats
+    assert stats["runner"] == "identity" and stats["lowering"] == "batched"
+    assert IdentityRunner().apply(mod, None, {}) is mod
+
+    class Chain:
+        names = ("identity", "hip_graph")
+
+        def apply(self, module, x, stats):
+            return module
+
+    assert deliver(ir, {}, sink, runner=Chain()).stats["runner"] == ["identity", "hip_graph"]
+    assert deliver(ir, {}, sink, runner=Capturable()).stats["runner"] == "Capturable"
