@@ -17,7 +17,9 @@ scan's states (``omd``), which are not among C1-C5.
 Per form:
   * ``ms_per_step``  — HIP events on torch's current stream (the stream the
     kernels are launched on) around K back-to-back steps, after W warmup
-    steps, bracketed by ``torch.cuda.synchronize()``;
+    steps, bracketed by ``torch.cuda.synchronize()``; the form's setup ends
+    with about 100 ms of its own steps (``settle``) so the clocks are level
+    under the load before the warm-up starts;
   * ``roofline``     — the form's dominant kernel timed alone the same way:
     algorithmic flops (MFMA-bound) or bytes (HBM-bound) per launch divided by
     its average launch duration, against MI355X's published peak;
@@ -69,6 +71,26 @@ def time_events(fn, steps: int, warmup: int) -> float:
     t1.record()
     torch.cuda.synchronize()
     return t0.elapsed_time(t1) / steps
+
+
+SETTLE_MS = 100.0
+
+
+def settle(fn, ms: float, max_steps: int = 10000) -> int:
+    """Run ``fn`` until about ``ms`` of device time has passed (untimed):
+    the steps that bring the clocks to their level under this load."""
+    import torch
+
+    n, t0 = 0, time.perf_counter()
+    while n < max_steps:
+        fn()
+        n += 1
+        if n & 7 == 0:
+            torch.cuda.synchronize()
+            if (time.perf_counter() - t0) * 1e3 >= ms:
+                break
+    torch.cuda.synchronize()
+    return n
 
 
 def time_graph_replays(fn, n: int = 30, warmup: int = 5) -> dict:
@@ -773,6 +795,11 @@ def measure(form: Form, dev, steps: int, warmup: int, cpu_budget: float | None) 
     log(f"{form.name}: setup")
     form.setup(dev)
     torch.cuda.synchronize()
+    # end the setup with about SETTLE_MS of the form's own steps, so the
+    # clocks have settled under this load before the W warm-up steps and the
+    # K timed ones (a few warm-up steps of a sub-millisecond step leave the
+    # first timed steps up to 10% slow)
+    settle_steps = settle(form.step, SETTLE_MS)
     log(f"{form.name}: timing {steps} steps after {warmup} warmup")
     w0 = time.perf_counter()
     ms = time_events(form.step, steps, warmup)
@@ -805,6 +832,7 @@ def measure(form: Form, dev, steps: int, warmup: int, cpu_budget: float | None) 
             "work_per_launch": form.dom_work,
         },
         "wall_ms_incl_warmup": round(wall_ms, 2),
+        "settle": {"ms": SETTLE_MS, "steps": settle_steps},
     }
     # the step replayed from a hipGraph (median / IQR over 30 replays)
     try:
