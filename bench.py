@@ -789,7 +789,8 @@ FORMS = {f.name: f for f in (C1WeightChain, C2SwiGLU, C3Attention, C4Retention, 
 HEADLINE = "c2"
 
 
-def measure(form: Form, dev, steps: int, warmup: int, cpu_budget: float | None) -> dict:
+def measure(form: Form, dev, steps: int, warmup: int, cpu_budget: float | None,
+            settle_ms: float = SETTLE_MS) -> dict:
     import torch
 
     log(f"{form.name}: setup")
@@ -799,7 +800,7 @@ def measure(form: Form, dev, steps: int, warmup: int, cpu_budget: float | None) 
     # clocks have settled under this load before the W warm-up steps and the
     # K timed ones (a few warm-up steps of a sub-millisecond step leave the
     # first timed steps up to 10% slow)
-    settle_steps = settle(form.step, SETTLE_MS)
+    settle_steps = settle(form.step, settle_ms) if settle_ms > 0 else 0
     log(f"{form.name}: timing {steps} steps after {warmup} warmup")
     w0 = time.perf_counter()
     ms = time_events(form.step, steps, warmup)
@@ -832,7 +833,7 @@ def measure(form: Form, dev, steps: int, warmup: int, cpu_budget: float | None) 
             "work_per_launch": form.dom_work,
         },
         "wall_ms_incl_warmup": round(wall_ms, 2),
-        "settle": {"ms": SETTLE_MS, "steps": settle_steps},
+        "settle": {"ms": settle_ms, "steps": settle_steps},
     }
     # the step replayed from a hipGraph (median / IQR over 30 replays)
     try:
@@ -866,6 +867,8 @@ def main(argv=None) -> int:
     ap.add_argument("--cpu-budget", type=float, default=10.0,
                     help="seconds of CPU oracle work for the headline form (others get a third)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                    help="untimed steps of each form before its warm-up (0: none; counter passes)")
     args = ap.parse_args(argv)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -894,7 +897,7 @@ def main(argv=None) -> int:
     forms = {}
     for n in names:
         budget = None if args.no_cpu else (args.cpu_budget if n == HEADLINE else args.cpu_budget / 3)
-        forms[n] = measure(FORMS[n](), dev, args.steps, args.warmup, budget)
+        forms[n] = measure(FORMS[n](), dev, args.steps, args.warmup, budget, args.settle_ms)
         log(f"{n}: {forms[n]['value']} {forms[n]['unit']} ({forms[n]['ms_per_step']} ms/step, "
             f"roofline frac {forms[n]['roofline']['frac']})")
 
