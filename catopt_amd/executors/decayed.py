@@ -52,7 +52,8 @@ from ..ir import IR, is_op
 from .base import HipExecutorBase
 from .om import _peel_scale, _qk_product, _transposed_operand
 
-__all__ = ["HipChunkedDecayModule", "build_decayed_plan", "is_decayed_term"]
+__all__ = ["HipChunkedDecayModule", "build_decayed_plan", "is_decayed_chunked_term", "is_decayed_term",
+           "to_chunked_decayed_module"]
 
 
 def _flat(t: Any, op: str, dim: int | None = None) -> list:
@@ -313,6 +314,12 @@ class HipChunkedDecayModule(HipExecutorBase, nn.Module):
     def n_chunks(self) -> int:
         return 0 if self._plan is None else self._plan["K"]
 
+    @property
+    def n_blocks(self) -> int:
+        """Output chunks of the delivered form, 0 when not batched (the
+        reference's name, decayed_lower.py:423-426)."""
+        return self.n_chunks
+
     def _forward_impl(self, *xs: Any) -> Any:
         p = self._plan
         if p is None:
@@ -353,3 +360,13 @@ def _kernel_args(q, k, v, g, p):
     if g.numel() != H:
         return None
     return q, k, v, g.to(torch.float32).contiguous(), lead
+
+
+#: The reference's probe name (decayed_lower.py:371-373).
+is_decayed_chunked_term = is_decayed_term
+
+
+def to_chunked_decayed_module(ir: IR, param_values: dict | None = None, **kw) -> HipChunkedDecayModule:
+    """Always a :class:`HipChunkedDecayModule` (check ``is_batched``),
+    ``decayed_lower.py:727-731``."""
+    return HipChunkedDecayModule(ir, param_values, **kw)

@@ -63,7 +63,8 @@ from ..evaluator import HipIRModule, _is_param, _is_var, eval_term
 from ..ir import IR, Op, is_op, postorder
 from .base import HipExecutorBase
 
-__all__ = ["HipOMModule", "build_om_plan", "is_om_term", "mask_kwargs", "om_leaves", "parse_score"]
+__all__ = ["HipOMModule", "build_om_plan", "is_om_apply_term", "is_om_term", "mask_kwargs", "om_leaves",
+           "parse_score", "to_batched_om_module"]
 
 
 def is_om_term(term: Any) -> bool:
@@ -583,6 +584,18 @@ class HipOMModule(HipExecutorBase, nn.Module):
         return 0 if self._plan is None else len(self._plan["leaves"])
 
     @property
+    def n_blocks(self) -> int:
+        """om carrier leaves, 0 when not batched (om_lower.py:596-599)."""
+        return self.n_leaves
+
+    @property
+    def n_levels(self) -> int:
+        """Compose levels of the pairwise reduction (⌈log2 leaves⌉), 0 when
+        not batched or for one leaf (om_lower.py:591-594)."""
+        n = self.n_leaves
+        return 0 if n <= 1 else (n - 1).bit_length()
+
+    @property
     def leaf_kinds(self) -> list[str]:
         """Plan class of each leaf ("attn", "scores" or "om")."""
         return [] if self._plan is None else [lf["kind"] for lf in self._plan["leaves"]]
@@ -676,3 +689,17 @@ class HipOMModule(HipExecutorBase, nn.Module):
             carriers = nxt
         _, lsum, acc = carriers[0]
         return (acc / lsum).to(out_dtype)
+
+
+#: The reference's probe name (om_lower.py:106-113).
+is_om_apply_term = is_om_term
+
+
+def to_batched_om_module(ir: IR, param_values: dict | None = None, fused: bool | str = False,
+                         **kw) -> HipOMModule:
+    """Always a :class:`HipOMModule` (check ``is_batched``), ``om_lower.py:838-868``.
+    ``fused`` is accepted for the reference's signature: it selects a
+    torch.compile'd reduction there, and here every leaf and combine already
+    runs on the HIP kernels, so it changes nothing."""
+    del fused
+    return HipOMModule(ir, param_values, **kw)

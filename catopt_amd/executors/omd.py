@@ -69,7 +69,7 @@ from .base import HipExecutorBase
 from .om import _peel_scale, parse_score
 from .scan import prefix_chunk_table
 
-__all__ = ["HipOmdModule", "build_omd_plan", "is_omd_term", "to_batched_omd_module"]
+__all__ = ["HipOmdModule", "build_omd_plan", "is_omd_apply_term", "is_omd_term", "to_batched_omd_module"]
 
 #: projection op -> (component, carrier)
 _PROJ = {"affd_a": (0, "diag"), "affd_b": (1, "diag"), "aff_A": (0, "dense"), "aff_b": (1, "dense")}
@@ -815,3 +815,7 @@ class _Decline(Exception):
 def to_batched_omd_module(ir: IR, param_values: dict | None = None, **kw) -> HipOmdModule:
     """Always a :class:`HipOmdModule` (check ``is_batched``), ``omd_lower.py:1022-1033``."""
     return HipOmdModule(ir, param_values, **kw)
+
+
+#: The reference's probe name (omd_lower.py:154-170).
+is_omd_apply_term = is_omd_term

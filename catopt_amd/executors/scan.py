@@ -80,7 +80,9 @@ from .base import HipExecutorBase
 __all__ = [
     "HipScanModule",
     "build_scan_plan",
+    "is_scan_apply_term",
     "is_scan_term",
+    "to_batched_scan_module",
     "prefix_chunk_table",
     "affd_leaves",
     "map_leaves",
@@ -611,3 +613,17 @@ class HipScanModule(HipExecutorBase, nn.Module):
         if h.dim() == 1:
             return hf.reshape(d).to(out_dtype)
         return hf.reshape(*pshape, d, k).to(out_dtype)
+
+
+#: The reference's probe name (scan_lower.py:200-214).
+is_scan_apply_term = is_scan_term
+
+
+def to_batched_scan_module(ir: IR, param_values: dict | None = None, *, fused: bool | str = False,
+                           **kw) -> HipScanModule:
+    """Always a :class:`HipScanModule` (check ``is_batched``), ``scan_lower.py:837-870``.
+    ``fused`` is accepted for the reference's signature (its shrinking-tensor
+    reduction under torch.compile); the scans here are single kernels, so it
+    changes nothing."""
+    del fused
+    return HipScanModule(ir, param_values, **kw)

@@ -137,3 +137,43 @@ def test_the_constant_cache_rekeys_on_dtype():
         b = mod._cached(("k",), args[0], make, dtype=torch.float64)
         assert b is not a and len(made) == 2 and mod._const_cache[("k",)] is b
         assert np.array_equal(b.numpy(), [0.0, 1.0])
+
+
+def test_the_reference_constructor_and_probe_names():
+    # code written against catopt's executors finds the same entry points:
+    # to_batched_*_module / to_chunked_decayed_module always return the
+    # executor (check is_batched); the is_*_term probes; n_blocks / n_levels
+    from catopt_amd import executors as E
+    from catopt_amd.ir import IR, Op, TensorType, Var
+
+    b = DecayedTerms()
+    vals, _ = b.values()
+    dec = E.to_chunked_decayed_module(b.ir(b.root()), vals, ops=cpu_table())
+    assert isinstance(dec, HipChunkedDecayModule) and dec.is_batched and dec.n_blocks == b.K
+    assert E.is_decayed_chunked_term(b.root()) and not E.is_decayed_chunked_term(b.q)
+    ir, _ = forms.causal_attention_form(1, 2, 8, 16, mask="cmask")
+    om = E.to_batched_om_module(ir, {}, fused=True, ops=cpu_table())
+    assert isinstance(om, HipOMModule) and om.is_batched and (om.n_blocks, om.n_levels) == (1, 0)
+    assert E.is_om_apply_term(ir.root)
+    q = Var("q", TensorType((8, 4)))
+    ks = [Var(f"k{i}", TensorType((4, 4))) for i in range(5)]
+    leaves = [Op.make("om_elem", Op.make("matmul", q, Op.make("transpose", k, dim0=-2, dim1=-1)), k) for k in ks]
+    tree = leaves[0]
+    for lf in leaves[1:]:
+        tree = Op.make("om_compose", tree, lf)
+    om5 = E.to_batched_om_module(IR(Op.make("om_apply", tree), [q, *ks]), {}, ops=cpu_table())
+    assert (om5.n_blocks, om5.n_levels) == (5, 3)
+    ir, _ = forms.scan_final_form(6, (3,))
+    sc = E.to_batched_scan_module(ir, {}, fused=True, ops=cpu_table())
+    assert isinstance(sc, HipScanModule) and sc.is_batched and sc.n_levels > 0
+    assert E.is_scan_apply_term(ir.root)
+    ir, _ = forms.omd_scan_attention_form(16, 4, 5, 2, 3)
+    assert E.is_omd_apply_term(ir.root) and E.to_batched_omd_module(ir, {}, ops=cpu_table()).is_batched
+    x = Var("x", TensorType((4,)))
+    relu = IR(Op.make("relu", x), [x])
+    for make in (E.to_batched_om_module, E.to_batched_scan_module, E.to_chunked_decayed_module,
+                 E.to_batched_omd_module):
+        m = make(relu, {}, ops=cpu_table())
+        assert not m.is_batched
+        assert torch.equal(m(torch.full((4,), -1.0)), torch.zeros(4))
+    assert dec.n_blocks == b.K and E.to_chunked_decayed_module(relu, {}, ops=cpu_table()).n_blocks == 0
