@@ -10,7 +10,11 @@ the MI355X path:
   diagonal-affine scan ops when they arrive stacked;
 * layout and glue ops (``split``, ``chunk``, ``concat``, ``unsqueeze``,
   ``transpose``, ``masked_fill`` …) are views or small device ops through
-  torch, which here is only the owner of device memory and streams.
+  torch, which here is only the owner of device memory and streams;
+* the rest of the reference's core table (norms, clamps, comparisons,
+  cumulative and indexed ops, creators, casts) are torch device ops from
+  :mod:`catopt_amd.device_ops`, so terms whose leaf operands use them stay
+  deliverable.
 
 Argument meaning follows the reference's core table
 (``packages/catopt-torch/src/catopt_torch/torch_bridge.py:1146-1902``) and
@@ -31,6 +35,7 @@ import torch
 import torch.nn.functional as F
 
 from . import kernels as K
+from .device_ops import DEVICE_OPS
 
 __all__ = ["HIP_BINDINGS", "HipOpTable", "attr_of", "om_elem_dense", "torch_fallback_count"]
 
@@ -345,6 +350,9 @@ def _scalar_like(v):
 
 
 HIP_BINDINGS: dict[str, Callable] = {
+    # ---- the device ops around the delivered forms (norms, clamps, gathers,
+    #      creators, casts …); the entries below take precedence
+    **DEVICE_OPS,
     # ---- GEMM family and norms (HIP kernels)
     "linear": _linear,
     "matmul": _matmul,
@@ -412,7 +420,6 @@ HIP_BINDINGS: dict[str, Callable] = {
     "tril": lambda t, *a, **kw: torch.tril(t, int(attr_of(kw, "diagonal", default=0))),
     # ---- layout (views)
     "transpose": _transpose,
-    "permute": lambda t, *a, **kw: t.permute(*attr_of(kw, "dims", default=())),
     "reshape": lambda x, *a, **kw: x.reshape(tuple(kw["shape"]) if "shape" in kw else (-1,)),
     "view": lambda x, *a, **kw: x.reshape(tuple(kw["shape"]) if "shape" in kw else (-1,)),
     "contiguous": lambda x, *a, **kw: x.contiguous(),
