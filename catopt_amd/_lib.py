@@ -44,6 +44,7 @@ SIGNATURES: dict[str, tuple] = {
          _f32, _i32, _i64, _p, _i64, _i32, _p, _pi64, _p, _p, _p],
     ),
     "catopt_hip_om_rows": (_i32, [_i32, _i64, _i64, _p, _i64, _i32, _p, _p, _p, _i64, _p]),
+    "catopt_hip_omd_fold_apply": (_i32, [_i64, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p, _p]),
     "catopt_hip_om_compose": (_i32, [_i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p]),
     "catopt_hip_retention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
     "catopt_hip_retention_fwd": (

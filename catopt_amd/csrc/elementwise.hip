@@ -178,6 +178,69 @@ __global__ __launch_bounds__(kThreads) void decay_vec_kernel(int64_t H, int64_t 
   }
 }
 
+// The om combine of L carriers over the leading axis followed by the
+// diagonal deferred-affine readout:
+//   M = max_i m[i, r] (NaN-propagating), w_i = isfinite(m_i) ? exp(m_i − M) : 0,
+//   out[r, c] = (Σ_i w_i num[i, r, c] · h[c] + Σ_i w_i num[i, r, d + c]) / Σ_i w_i l[i, r].
+// One wave per row (rows grid-strided over the waves).  Lane i holds leaf
+// i's m, l and weight (64 leaves per pass), so the row statistics are one
+// load each and a wave reduction; the numerators are read with the lanes
+// over the columns (contiguous row segments), each leaf's weight broadcast
+// from its lane, the leaf loop unrolled so its loads are in flight together.
+constexpr int kFoldWaves = kThreads / 64;
+
+__device__ __forceinline__ float wave_nan_max(float v) {
+  for (int o = 32; o > 0; o >>= 1) v = nan_max(v, __shfl_xor(v, o));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__global__ __launch_bounds__(kThreads) void omd_fold_apply_kernel(
+    int64_t L, int64_t rows, int64_t d, const float* __restrict__ m, const float* __restrict__ l,
+    const float* __restrict__ num, int64_t ldn, int64_t num_sb, const float* __restrict__ h,
+    float* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  for (int64_t r = (int64_t)blockIdx.x * kFoldWaves + (threadIdx.x >> 6); r < rows;
+       r += (int64_t)gridDim.x * kFoldWaves) {
+    float mx = -__builtin_inff();
+    for (int64_t j0 = 0; j0 < L; j0 += 64) {
+      const int64_t j = j0 + lane;
+      mx = nan_max(mx, j < L ? m[j * rows + r] : -__builtin_inff());
+    }
+    mx = wave_nan_max(mx);
+    const float* nrow0 = num + r * ldn;
+    for (int64_t c0 = 0; c0 < d; c0 += 64) {
+      const int64_t c = c0 + lane;
+      const bool on = c < d;
+      float ls = 0.f, fa = 0.f, fb = 0.f;
+      for (int64_t j0 = 0; j0 < L; j0 += 64) {
+        const int64_t j = j0 + lane;
+        // a leaf with no finite score weighs 0 (an empty carrier's l and a
+        // are 0, so it adds nothing)
+        const float mj = j < L ? m[j * rows + r] : -__builtin_inff();
+        const float w = __builtin_isfinite(mj) ? __expf(mj - mx) : 0.f;
+        ls += j < L ? l[j * rows + r] * w : 0.f;
+        const int n = (int)(L - j0 < 64 ? L - j0 : 64);
+        const float* nblk = nrow0 + j0 * num_sb;
+#pragma unroll 16
+        for (int t = 0; t < n; ++t) {
+          const float wt = __shfl(w, t);
+          if (on) {
+            fa += nblk[t * num_sb + c] * wt;
+            fb += nblk[t * num_sb + d + c] * wt;
+          }
+        }
+      }
+      ls = wave_sum(ls);
+      if (on) out[r * d + c] = (fa * h[c] + fb) / ls;
+    }
+  }
+}
+
 }  // namespace
 }  // namespace catopt
 
@@ -207,6 +270,21 @@ extern "C" int32_t catopt_hip_om_compose(int64_t rows, int64_t dv, const float* 
     CATOPT_LAUNCH_CHECK();
   }
   om_compose_ml_kernel<<<grid_for(rows), kThreads, 0, s>>>(rows, m1, l1, m2, l2, m, l);
+  CATOPT_LAUNCH_CHECK();
+  return CATOPT_OK;
+}
+
+extern "C" int32_t catopt_hip_omd_fold_apply(int64_t L, int64_t rows, int64_t d, const float* m,
+                                             const float* l, const float* num, int64_t ldn,
+                                             int64_t num_sb, const float* h, float* out,
+                                             void* stream) {
+  if (L < 1 || rows < 0 || d < 0 || ldn < 2 * d || num_sb < (rows > 0 ? (rows - 1) * ldn + 2 * d : 0))
+    return CATOPT_E_INVAL;
+  if (rows == 0 || d == 0) return CATOPT_OK;
+  if (!m || !l || !num || !h || !out) return CATOPT_E_INVAL;
+  const int64_t blocks = (rows + kFoldWaves - 1) / kFoldWaves;
+  omd_fold_apply_kernel<<<dim3((uint32_t)(blocks < 65536 ? blocks : 65536)), kThreads, 0,
+                          static_cast<hipStream_t>(stream)>>>(L, rows, d, m, l, num, ldn, num_sb, h, out);
   CATOPT_LAUNCH_CHECK();
   return CATOPT_OK;
 }

@@ -45,7 +45,10 @@ Execution on the device:
   kernel over the concatenated numerator ``[fa | fb]`` (the omd combine is
   om's applied to each part, ``xcarrier.py:407-440``; the ``isfinite``
   guard of fully masked blocks is in the kernel);
-* the readout on the device.
+* the readout on the device; when every leaf's carrier came from one
+  carrier launch and the fibre is diagonal, the combine over the leaf axis
+  and the readout ``(fa ⊙ h + fb) / l`` are one ``catopt_hip_omd_fold_apply``
+  pass (``fused_omd_levels``, om_fused.py:151-164).
 
 Carriers are fp32 (bf16 operands are widened); the result has the promoted
 operand dtype.  Other dtypes, host tensors, and shape surprises run the
@@ -540,10 +543,13 @@ class HipOmdModule(HipExecutorBase, nn.Module):
             if A.shape != B.shape:
                 raise ValueError("diagonal chain parts differ in shape")
             S = A[0].numel()
-            a2 = torch.cat([A.reshape(T, S), A.reshape(T, S)], dim=1)
-            u2 = torch.cat([torch.zeros_like(B.reshape(T, S)), B.reshape(T, S)], dim=1)
-            h2 = torch.cat([torch.ones(S, dtype=A.dtype, device=A.device),
-                            torch.zeros(S, dtype=A.dtype, device=A.device)])
+            a2 = A.reshape(T, S).repeat(1, 2)                           # [a | a]
+            u2 = torch.nn.functional.pad(B.reshape(T, S), (S, 0))      # [0 | b]
+            hkey = ("h2", S, A.dtype, A.device)
+            h2 = self._tables.get(hkey)                                 # [1 | 0], built once
+            if h2 is None:
+                h2 = self._tables[hkey] = torch.cat([torch.ones(S, dtype=A.dtype, device=A.device),
+                                                     torch.zeros(S, dtype=A.dtype, device=A.device)])
             states, _ = K.affd_scan(a2, u2, h2, table, states=True)
             return states[:, :S].reshape(A.shape), states[:, S:].reshape(B.shape)
         # dense: A (T, *P, d, d), B (T, *P, d)
@@ -668,8 +674,8 @@ class HipOmdModule(HipExecutorBase, nn.Module):
             V = Vall[:L * C].view(L, C, -1)
         else:
             V = torch.stack([Vall[s:s + C] for s, _ in blocks])
-        m, lv, num = K.attn_carrier_f32(q, kall.reshape(L, C, -1), V, float(p["scores"][0]["scale"]))
-        return self._fold(m, lv, num), wa, tail, [q.dtype, kall.dtype]
+        carriers = K.attn_carrier_f32(q, kall.reshape(L, C, -1), V, float(p["scores"][0]["scale"]))
+        return carriers, wa, tail, [q.dtype, kall.dtype]
 
     def _batched_leaves(self, ev) -> tuple | None:
         """Every leaf a ``scale · q k_iᵀ`` score over one shared ``q`` with key
@@ -700,8 +706,8 @@ class HipOmdModule(HipExecutorBase, nn.Module):
             Vs.append(V)
         if shape[1][-1] > 256:
             return None
-        m, lv, num = K.attn_carrier_f32(q, torch.stack(ks), torch.stack(Vs), float(scs[0]["scale"]))
-        return self._fold(m, lv, num), shape[2], shape[3], [q.dtype] + [k.dtype for k in ks[:1]]
+        carriers = K.attn_carrier_f32(q, torch.stack(ks), torch.stack(Vs), float(scs[0]["scale"]))
+        return carriers, shape[2], shape[3], [q.dtype] + [k.dtype for k in ks[:1]]
 
     def _forward_impl(self, *xs: Any) -> Any:
         p = self._plan
@@ -739,15 +745,24 @@ class HipOmdModule(HipExecutorBase, nn.Module):
         state = None
         width = tail = None
         self.fused_leaves = 0
+        self.fused_readout = False
         batched = self._batched_blocks(ev, Pa, Pb) if Pa is not None else None
         if batched is None:
             if stores:
                 self._seed(memo, stores)  # the leaves read their coefficient stacks through the memo
             batched = self._batched_leaves(ev)
         if batched is not None:
-            state, width, tail, sdts = batched
+            carriers, width, tail, sdts = batched
             dtypes += sdts
             self.fused_leaves = len(p["leaves"])
+            if p["apply"] == "omd_apply" and tail == (width,) and carriers[2].shape[-1] == 2 * width:
+                # every leaf's carrier in one stack: the combine over the
+                # leaf axis and the diagonal readout run as one kernel
+                h = ev(p["h"])
+                if _kernel_dtype(h) and h.dim() == 1 and h.shape[0] == width:
+                    self.fused_readout = True
+                    return K.omd_fold_apply(*carriers, h.float()).to(_promote(h.dtype, dtypes))
+            state = self._fold(*carriers)
         for lf, sc in zip(() if batched is not None else p["leaves"], p["scores"]):
             if lf.op == "omd_elem":
                 a, b = ev(lf.args[1]), ev(lf.args[2])
@@ -797,15 +812,20 @@ class HipOmdModule(HipExecutorBase, nn.Module):
         h = ev(p["h"])
         if not _kernel_dtype(h):
             raise _Decline()
-        out_dtype = h.dtype
-        for dt in dtypes:
-            out_dtype = torch.promote_types(out_dtype, dt)
+        out_dtype = _promote(h.dtype, dtypes)
         hf = h.float()
         if p["apply"] == "omd_apply":
             out = (fa * hf + fb) / lv
         else:
             out = (K.matmul(fa, hf) + fb) / lv
         return out.to(out_dtype)
+
+
+def _promote(dt: torch.dtype, dtypes: list) -> torch.dtype:
+    """The result dtype: ``h``'s promoted with every operand's."""
+    for other in dtypes:
+        dt = torch.promote_types(dt, other)
+    return dt
 
 
 class _Decline(Exception):

@@ -570,6 +570,28 @@ def attn_carrier_f32(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: f
     return m.reshape(*lead, Tq, 1), lv.reshape(*lead, Tq, 1), a.reshape(*lead, Tq, dv)
 
 
+def omd_fold_apply(m: torch.Tensor, lv: torch.Tensor, num: torch.Tensor, h: torch.Tensor) -> torch.Tensor:
+    """The om combine of ``L`` carriers over axis 0 followed by the diagonal
+    readout ``(fa ⊙ h + fb) / l`` (``fused_omd_levels``, om_fused.py:151-164),
+    one pass: ``m, lv (L, Tq[, 1])``, ``num (L, Tq, 2d)`` = ``[fa | fb]``,
+    ``h (d,)``, all fp32 on the device; returns ``(Tq, d)`` fp32."""
+    _need_device(m, lv, num, h)
+    lib = L.load()
+    Lc, Tq, W = num.shape
+    d = h.shape[-1]
+    if h.dim() != 1 or W != 2 * d or m.numel() != Lc * Tq or lv.numel() != Lc * Tq or \
+            any(t.dtype != torch.float32 for t in (m, lv, num, h)):
+        raise ValueError(f"omd_fold_apply: m{tuple(m.shape)} l{tuple(lv.shape)} num{tuple(num.shape)} "
+                         f"h{tuple(h.shape)} do not fit")
+    m2, l2, h1, num = m.reshape(Lc, Tq).contiguous(), lv.reshape(Lc, Tq).contiguous(), h.contiguous(), \
+        num.contiguous()
+    out = torch.empty((Tq, d), dtype=torch.float32, device=num.device)
+    st = lib.catopt_hip_omd_fold_apply(Lc, Tq, d, _ptr(m2), _ptr(l2), _ptr(num), num.stride(1), num.stride(0),
+                                       _ptr(h1), _ptr(out), _stream(num))
+    L.check("catopt_hip_omd_fold_apply", st)
+    return out
+
+
 def aff_scan(A: torch.Tensor, b: torch.Tensor, h0: torch.Tensor, chunk_starts, *,
              schedule: int = L.SCAN_AUTO, states: bool = True):
     """Dense affine scan over the leading axis: ``X_t = A_t X_{t-1} + b_t 1ᵀ``.

@@ -356,6 +356,26 @@ int32_t catopt_hip_attn_carrier_f32(int64_t batch, int64_t Tq, int64_t Tk,
                                     int64_t num_sb, int64_t ldn, void* stream);
 
 /*
+ * The om combine of L carriers of one query block followed by the diagonal
+ * deferred-affine readout, in one pass (fp32):
+ *   M = max_i m_i (NaN-propagating, as amax), w_i = isfinite(m_i) ?
+ *   exp(m_i − M) : 0, then out[r, c] = (Σ w_i fa_i[r, c] · h[c] +
+ *   Σ w_i fb_i[r, c]) / Σ w_i l_i[r]
+ * with fa_i, fb_i the two halves of num_i = [fa | fb].  m, l: [L, rows]
+ * contiguous; num: [L, rows, ≥ 2d] (leaf stride num_sb, row stride ldn);
+ * h: [d]; out: [rows, d] contiguous.  A row with no finite score in any
+ * carrier is NaN (0 / 0), as the unclamped omd_apply gives it.
+ * Replaces the level reduction and readout of BatchedOmdModule
+ * (omd_lower.py:900-945 into fused_omd_levels, om_fused.py:151-164) when
+ * every leaf's carrier comes from one catopt_hip_attn_carrier_f32 launch.
+ */
+int32_t catopt_hip_omd_fold_apply(int64_t L, int64_t rows, int64_t d,
+                                  const float* m, const float* l,
+                                  const float* num, int64_t ldn,
+                                  int64_t num_sb, const float* h, float* out,
+                                  void* stream);
+
+/*
  * Dense affine scan over T steps of P slots, each carrying a d x k state
  * (fp32, 1 ≤ d ≤ 64, k ≥ 1):
  *   X_t[p] = A_t[p] · X_{t-1}[p] + b_t[p] 1ᵀ,   X_{-1} = h0 (NULL = 0)

@@ -191,8 +191,45 @@ def test_omd_leaves_run_the_fused_kernel(dev):
     ins = _inputs(T, d, Tq, dk, False, 6)
     mod = HipOmdModule(ir, {})
     out = mod(*(t.to(dev) for t in ins))
-    assert mod.fallbacks == 0 and mod.fused_leaves == nb
+    assert mod.fallbacks == 0 and mod.fused_leaves == nb and mod.fused_readout
     _gate(_reference(*ins, False), out, TOL_F32)
+
+
+@pytest.mark.parametrize("L,Tq,d", [(16, 300, 64), (1, 7, 5), (5, 33, 128)])
+def test_omd_fold_apply_matches_the_serial_fold(dev, L, Tq, d):
+    """``catopt_hip_omd_fold_apply`` against the oracle's serial
+    ``omd_compose`` fold and ``omd_apply`` in float64: carriers with an
+    empty row in some leaves (m = -inf, l = 0, a = 0), a row empty in every
+    leaf (NaN: 0 / 0), and carrier maxima far apart (weights that underflow
+    to 0 beside 1)."""
+    from catopt_amd import kernels as K
+
+    rng = np.random.default_rng(L * 100 + d)
+    m = rng.standard_normal((L, Tq)) * 30
+    lv = rng.uniform(1.0, 5.0, (L, Tq))
+    fa, fb = rng.standard_normal((L, Tq, d)), rng.standard_normal((L, Tq, d))
+    h = rng.standard_normal(d)
+    dead = [0] + ([Tq - 1] if Tq > 1 else [])
+    m[0, Tq // 2] = -np.inf  # empty in leaf 0 only (all leaves when L = 1)
+    lv[0, Tq // 2], fa[0, Tq // 2], fb[0, Tq // 2] = 0, 0, 0
+    m[:, dead], lv[:, dead], fa[:, dead], fb[:, dead] = -np.inf, 0, 0, 0
+    f32 = lambda z: np.asarray(z, np.float32).astype(np.float64)  # noqa: E731
+    m, lv, fa, fb, h = (f32(z) for z in (m, lv, fa, fb, h))
+    carriers = [(m[i][:, None], lv[i][:, None], fa[i], fb[i]) for i in range(L)]
+    acc = carriers[0]
+    for c in carriers[1:]:
+        acc = oracle.omd_compose(acc, c)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        ref = oracle.omd_apply(acc, h)
+    assert np.isnan(ref[0]).all()
+    num = torch.from_numpy(np.concatenate([fa, fb], -1).astype(np.float32)).to(dev)
+    t = lambda z: torch.from_numpy(z.astype(np.float32)).to(dev)  # noqa: E731
+    out = K.omd_fold_apply(t(m), t(lv), num, t(h))
+    assert out.shape == (Tq, d)
+    on = _np(out)
+    assert np.array_equal(np.isnan(on), np.isnan(ref))
+    fin = ~np.isnan(ref)
+    _gate(np.where(fin, ref, 0), torch.from_numpy(np.where(fin, on, 0)), TOL_F32)
 
 
 # ------------------------------------------------------------ forest plans
