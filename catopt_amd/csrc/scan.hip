@@ -96,10 +96,25 @@ __global__ __launch_bounds__(kThreads) void scan_carry(const float* __restrict__
   const int64_t s = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (s >= S) return;
   float cin = h0 ? h0[s] : 0.f;
-  for (int64_t c = 0; c < nc; ++c) {
-    const float p = ws_p[c * S + s], h = ws_h[c * S + s];
-    ws_h[c * S + s] = cin;
-    cin = p * cin + h;
+  // the chunk summaries do not depend on the carry: load a batch of them
+  // before the batch's stores (which the compiler cannot reorder across
+  // ws_h's loads), so a batch costs one memory latency, not one per chunk
+  constexpr int kBatch = 16;
+  for (int64_t c0 = 0; c0 < nc; c0 += kBatch) {
+    const int n = (int)(nc - c0 < kBatch ? nc - c0 : kBatch);
+    float p[kBatch], h[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i)
+      if (i < n) {
+        p[i] = ws_p[(c0 + i) * S + s];
+        h[i] = ws_h[(c0 + i) * S + s];
+      }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i)
+      if (i < n) {
+        ws_h[(c0 + i) * S + s] = cin;
+        cin = p[i] * cin + h[i];
+      }
   }
   if (hf) hf[s] = cin;
 }
