@@ -667,7 +667,7 @@ class HipOmdModule(HipExecutorBase, nn.Module):
         T = Pa.shape[0]
         tail = tuple(Pa.shape[1:]) if Pa.dim() >= 3 else (Pa.shape[-1],)  # the fibre test of _omd_elem
         wa = Pa[0].numel()
-        Vall = torch.cat([Pa.reshape(T, -1), Pb.reshape(T, -1)], dim=1)
+        Vall = _side_by_side(Pa.reshape(T, -1), Pb.reshape(T, -1))
         if Vall.shape[1] > 256:
             return None
         if blocks == [(i * C, C) for i in range(L)]:
@@ -819,6 +819,18 @@ class HipOmdModule(HipExecutorBase, nn.Module):
         else:
             out = (K.matmul(fa, hf) + fb) / lv
         return out.to(out_dtype)
+
+
+def _side_by_side(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """``cat([a, b], dim=1)`` of two ``(T, ·)`` arrays; a view when ``b``'s
+    columns already follow ``a``'s in one row-major buffer (the diagonal
+    prefix scan writes ``[∏a | prefix b]`` that way)."""
+    T, wa = a.shape
+    w = wa + b.shape[1]
+    if a.dtype == b.dtype and a.stride() == (w, 1) and b.stride() == (w, 1) and \
+            b.data_ptr() == a.data_ptr() + wa * a.element_size():
+        return a.as_strided((T, w), (w, 1))
+    return torch.cat([a, b], dim=1)
 
 
 def _promote(dt: torch.dtype, dtypes: list) -> torch.dtype:

@@ -177,3 +177,14 @@ def test_the_reference_constructor_and_probe_names():
         assert not m.is_batched
         assert torch.equal(m(torch.full((4,), -1.0)), torch.zeros(4))
     assert dec.n_blocks == b.K and E.to_chunked_decayed_module(relu, {}, ops=cpu_table()).n_blocks == 0
+
+
+def test_side_by_side_is_a_view_only_when_the_columns_already_follow():
+    from catopt_amd.executors.omd import _side_by_side
+
+    st = torch.randn(6, 10)
+    a, b = st[:, :4], st[:, 4:]
+    v = _side_by_side(a, b)
+    assert torch.equal(v, st) and v.data_ptr() == st.data_ptr()
+    for x, y in ((st[:, 4:], st[:, :4]), (torch.randn(6, 3), torch.randn(6, 2)), (st[:, :4], st[:, 5:])):
+        assert torch.equal(_side_by_side(x, y), torch.cat([x, y], dim=1))
