@@ -467,6 +467,7 @@ class HipOmdModule(HipExecutorBase, nn.Module):
         self._inputs = list(ir.inputs)
         self._const_cache: dict = {}
         self._tables: dict = {}
+        self._identity_gathers: dict = {}
         self.fallbacks = 0
         self._plan = build_omd_plan(self.eval_mod._root)
         self.fused_leaves = 0  # leaves run by the fused carrier kernel on the last call
@@ -501,7 +502,13 @@ class HipOmdModule(HipExecutorBase, nn.Module):
             if g is not None:
                 base, dim, idx = g
                 bt = ev(base)
-                if idx == list(range(bt.shape[dim])):
+                # whether the gather is the identity, decided once per plan
+                # entry and extent (the comparison walks T indices)
+                key = (id(g), bt.shape[dim])
+                ident = self._identity_gathers.get(key)
+                if ident is None:
+                    ident = self._identity_gathers[key] = idx == list(range(bt.shape[dim]))
+                if ident:
                     t = bt.movedim(dim, 0)
                 else:
                     t = bt.index_select(dim, self._index(idx, bt)).movedim(dim, 0)
