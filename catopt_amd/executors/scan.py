@@ -367,6 +367,7 @@ class HipScanModule(HipExecutorBase, nn.Module):
         self.eval_mod = eval_mod if eval_mod is not None else HipIRModule(ir, param_values, device=device, ops=ops)
         self._inputs = list(ir.inputs)
         self._const_cache: dict = {}
+        self._gather_kinds: dict = {}
         self.fallbacks = 0
         self.fused_readouts = 0  # calls whose read-out ran inside the SSM kernel
         self.schedule = L.SCAN_AUTO if schedule is None else schedule
@@ -393,10 +394,19 @@ class HipScanModule(HipExecutorBase, nn.Module):
         base = ev(base_t)
         if not isinstance(base, torch.Tensor) or not -base.dim() <= dim < base.dim():
             return None
-        if idx == list(range(T)) and base.shape[dim] == T:
+        # how the steps sit in the base is decided once per read and extent
+        # (each test walks the T indices): in order, gathered, or out of range
+        kind_key = (id(spec), base.shape[dim])
+        kind = self._gather_kinds.get(kind_key)
+        if kind is None:
+            n = base.shape[dim]
+            kind = "ident" if idx == list(range(T)) and n == T else \
+                "select" if all(-n <= i < n for i in idx) else "out"
+            self._gather_kinds[kind_key] = kind
+        if kind == "ident":
             out = base.movedim(dim, 0)
-        elif all(-base.shape[dim] <= i < base.shape[dim] for i in idx):
-            ix = self._cached(("idx", key, tuple(idx)), base,
+        elif kind == "select":
+            ix = self._cached(("idx", key, id(spec)), base,
                               lambda t: torch.tensor(idx, dtype=torch.long, device=t.device),
                               dtype=torch.long)
             out = base.index_select(dim, ix).movedim(dim, 0)
