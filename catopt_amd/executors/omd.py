@@ -482,7 +482,10 @@ class HipOmdModule(HipExecutorBase, nn.Module):
     # ------------------------------------------------------------ prefix maps
 
     def _index(self, idx: list, like: torch.Tensor) -> torch.Tensor:
-        return self._cached(("idx", tuple(idx)), like,
+        """The device copy of a plan's index list, keyed by the list itself
+        (plan lists live as long as the module; hashing T entries per call
+        would cost more than the gather)."""
+        return self._cached(("idx", id(idx), len(idx)), like,
                             lambda x: torch.tensor(idx, dtype=torch.long, device=x.device), dtype=torch.long)
 
     @staticmethod
