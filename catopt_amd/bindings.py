@@ -36,6 +36,7 @@ import torch.nn.functional as F
 
 from . import kernels as K
 from .device_ops import DEVICE_OPS
+from .planes import fit_plane, shared_plane
 
 __all__ = ["HIP_BINDINGS", "HipOpTable", "attr_of", "om_elem_dense", "torch_fallback_count"]
 
@@ -280,9 +281,10 @@ def _sdpa(q, k, v, *a, **kw):
     """``scaled_dot_product_attention`` (torch_bridge.py:1225-1245: a
     positional mask, attrs ``arg3``..``arg6`` = attn_mask, dropout_p,
     is_causal, scale).  bf16 ``(…, T, d)`` operands with one leading shape,
-    head dims up to 128, no dropout, a positive scale and at most one of
-    ``is_causal`` / a mask that is one ``(Tq, Tk)`` plane shared over the
-    leading axes run the fused attention kernel (a bool mask keeps, a float
+    head dims up to 128, no dropout, a positive scale, a head extent
+    within one launch (a larger batch runs as several), and at most one of ``is_causal`` / a mask
+    that is one plane shared over the leading axes and broadcasting to
+    ``(Tq, Tk)`` run the fused attention kernel (a bool mask keeps, a float
     one adds; ``is_causal`` keeps ``j <= i``; a fully masked row is 0, as
     torch gives it); any other call runs torch's op."""
     mask = a[0] if a else attr_of(kw, "attn_mask", "arg3", default=None)
@@ -295,9 +297,12 @@ def _sdpa(q, k, v, *a, **kw):
         sc = 1.0 / math.sqrt(q.shape[-1]) if scale is None else float(scale)
         if math.isfinite(sc) and sc > 0:
             lead = q.shape[:-2]
-            q4, k4, v4 = (t.reshape(-1, 1, *t.shape[-2:]) for t in (q, k, v))
-            o = K.attention(q4, k4, v4, sc, empty_rows="zero", **kw_mask)
-            return o.reshape(*lead, o.shape[-2], o.shape[-1])
+            # (B, H) of a 4-D call; a 3-D call's leading axis is the batch
+            q4, k4, v4 = (t if t.dim() == 4 else t.unsqueeze(1) if t.dim() == 3 else t[None, None]
+                          for t in (q, k, v))
+            if K.attention_grid_ok(q4):
+                o = K.attention(q4, k4, v4, sc, empty_rows="zero", **kw_mask)
+                return o.reshape(*lead, o.shape[-2], o.shape[-1])
     _fell_back()
     return F.scaled_dot_product_attention(q, k, v, attn_mask=mask, dropout_p=dropout, is_causal=causal,
                                           scale=None if scale is None else float(scale))
@@ -319,17 +324,13 @@ def _sdpa_kernel_mask(q, k, v, mask, causal, dropout) -> dict | None:
         return {"causal": True, "causal_off": 0} if causal else {}
     if causal or not isinstance(mask, torch.Tensor) or mask.dim() < 2:
         return None
-    tq, tk = q.shape[-2], k.shape[-2]
-    if mask.shape[-2:] != (tq, tk):
+    if mask.dtype != torch.bool and not mask.dtype.is_floating_point:
         return None
-    m3 = mask.reshape(-1, tq, tk)
-    if m3.shape[0] != 1 and not bool((m3 == m3[:1]).all()):
+    plane = shared_plane(mask)
+    plane = None if plane is None else fit_plane(plane, q.shape[-2], k.shape[-2])
+    if plane is None:
         return None
-    if mask.dtype == torch.bool:
-        return {"mask": m3[0]}
-    if mask.dtype.is_floating_point:
-        return {"bias": m3[0]}
-    return None
+    return {"mask": plane} if mask.dtype == torch.bool else {"bias": plane}
 
 
 def _split_sizes(t, kw):

@@ -135,8 +135,13 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
   const int l32 = lane & 31, g = lane >> 5;
   const int q0 = qt * QT;
   const int qw0 = q0 + wave * QW;  // first query of this wave
-  const float c = scale * 1.4426950408889634f;
-  const float inv_scale = 1.0f / scale;
+  // Scores run in raw q·k units, scaled at the exponential by c.  The bias
+  // mode instead forms torch's scaled score scale·q·k + bias in the mask
+  // step (dividing the bias by the scale instead overflows a finfo.min
+  // bias to -inf), and its exponentials use c = log2(e).
+  constexpr bool kScaledScores = MASK == CATOPT_MASK_BIAS;
+  const float c = kScaledScores ? 1.4426950408889634f : scale * 1.4426950408889634f;
+  const float m_unit = kScaledScores ? 1.f : scale;  // natural-log units of the scaled score
 
   // Q fragments (MFMA B operand) for the wave's two 32-query blocks.
   bf16x8 qf[QB][D / 16];
@@ -290,12 +295,13 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
             const int kc = key < Tk ? key : Tk - 1;
             const int64_t mi = (int64_t)qc * mask_ld + kc;
             if (MASK == CATOPT_MASK_BOOL) keep = keep & (static_cast<const uint8_t*>(mask)[mi] != 0);
-            // the bias is in units of the scaled score; the running
-            // scores here are q·k, scaled at the exponential
-            if (MASK == CATOPT_MASK_BIAS) add = static_cast<const float*>(mask)[mi] * inv_scale;
+            if (MASK == CATOPT_MASK_BIAS) add = static_cast<const float*>(mask)[mi];
             keep = keep & (qrow < Tq);
           }
-          s[r] = keep ? s[r] + add : -__builtin_inff();
+          if (kScaledScores)
+            s[r] = keep ? __builtin_fmaf(s[r], scale, add) : -__builtin_inff();
+          else
+            s[r] = keep ? s[r] : -__builtin_inff();
         }
       };
       // row max of a half (both lane halves), the true max, and the lazy
@@ -329,11 +335,16 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
       };
       // p = exp2(s c - m c) as the bf16 B operand of PV, and its row sum
       auto half_exp = [&](const f32x16& s, bf16x8* p) {
-        const float mc = (m_run[0] == -__builtin_inff()) ? 0.f : m_run[0] * c;
+        const float mr = (m_run[0] == -__builtin_inff()) ? 0.f : m_run[0];
+        const float mc = mr * c;
         float lsum = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c, -mc));
+          // scaled scores may sit near -FLT_MAX (a finfo.min bias), where
+          // s·c - m·c as one fma leaves m·c's rounding error (or overflow);
+          // the difference s - m is exact there
+          const float e = kScaledScores ? __builtin_amdgcn_exp2f((s[r] - mr) * c)
+                                        : __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c, -mc));
           lsum += e;
           p[r >> 3][r & 7] = static_cast<__bf16>(e);
         }
@@ -427,7 +438,7 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
     }
     if (g == 0) {
       const int64_t mi = (b * H + h) * (int64_t)Tq + qrow;
-      if (m_out) m_out[mi] = m_true[qb] * scale;  // natural-log units of the scaled score
+      if (m_out) m_out[mi] = m_true[qb] * m_unit;  // natural-log units of the scaled score
       if (l_out) l_out[mi] = l_tot;
     }
   }

@@ -219,17 +219,20 @@ __global__ __launch_bounds__(kThreads) void omd_fold_apply_kernel(
       float ls = 0.f, fa = 0.f, fb = 0.f;
       for (int64_t j0 = 0; j0 < L; j0 += 64) {
         const int64_t j = j0 + lane;
-        // a leaf with no finite score weighs 0 (an empty carrier's l and a
-        // are 0, so it adds nothing)
+        // a leaf with no finite score is left out by select, not weighted
+        // by 0: its l and numerators may be inf or NaN (torch.where in the
+        // reference's reduce)
         const float mj = j < L ? m[j * rows + r] : -__builtin_inff();
-        const float w = __builtin_isfinite(mj) ? __expf(mj - mx) : 0.f;
-        ls += j < L ? l[j * rows + r] * w : 0.f;
+        const bool fin = __builtin_isfinite(mj);
+        const float w = fin ? __expf(mj - mx) : 0.f;
+        ls += (j < L && fin) ? l[j * rows + r] * w : 0.f;
         const int n = (int)(L - j0 < 64 ? L - j0 : 64);
         const float* nblk = nrow0 + j0 * num_sb;
 #pragma unroll 16
         for (int t = 0; t < n; ++t) {
           const float wt = __shfl(w, t);
-          if (on) {
+          const bool ft = __shfl((int)fin, t) != 0;
+          if (on && ft) {
             fa += nblk[t * num_sb + c] * wt;
             fb += nblk[t * num_sb + d + c] * wt;
           }

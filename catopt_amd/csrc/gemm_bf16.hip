@@ -357,7 +357,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_nt(
         const int n = nb + 16 * (q & 1) + 8 * (q >> 1);
         if (m >= M || n >= N) continue;
         uint16_t* dst = C + (int64_t)m * ldc + n;
-        if (vec_store && (ldc % 8 == 0) && n + 7 < N) {
+        if (vec_store && n + 7 < N) {
           *reinterpret_cast<u32x4*>(dst) = u32x4{pk[0][0], pk[0][1], pk[1][0], pk[1][1]};
         } else {
           const uint32_t wv[4] = {pk[0][0], pk[0][1], pk[1][0], pk[1][1]};
@@ -457,8 +457,9 @@ int32_t launch(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb,
     if (dev >= 0 && dev < 64) cu_count[dev] = n_cu;
   }
   const int64_t grid = nblocks < n_cu ? nblocks : n_cu;
-  // 8-byte stores of four columns need 8-byte aligned rows of C
-  const int vec_store = (ldc % 4 == 0) && (sC % 4 == 0) && ((reinterpret_cast<uintptr_t>(C) & 7) == 0);
+  // the epilogue's 16-byte stores of eight columns need every row of every
+  // batch of C 16-byte aligned; otherwise it stores columns one by one
+  const int vec_store = (ldc % 8 == 0) && (sC % 8 == 0) && aligned16(C);
   gemm_bf16_nt<EPI><<<dim3((uint32_t)grid, (uint32_t)batch), dim3(NT), LDS_BYTES, s>>>(
       A, lda, B, ldb, bias, bias2, C, ldc, M, N, K, tiles_m, tiles_n, sA, sB, sC, vec_store);
   CATOPT_LAUNCH_CHECK();

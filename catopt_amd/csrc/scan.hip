@@ -708,18 +708,28 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-// This device's address of `scratch`, looked up once per device with that
-// device current (the caller's current device: the stream's).
-int32_t affd_scratch(void** out) {
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
+// The address of `scratch` on the stream's device, looked up once per
+// device with that device current (made current for the lookup when the
+// caller's current device is another one, then restored).
+int32_t affd_scratch(hipStream_t stream, void** out) {
+  hipDevice_t dev = -1;
+  hipError_t e = hipStreamGetDevice(stream, &dev);
   if (e != hipSuccess) return set_hip_error(e);
   if (dev < 0 || dev >= kMaxDevices) return CATOPT_E_UNSUPPORTED;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    e = hipGetDevice(&cur);
+    if (e != hipSuccess) return set_hip_error(e);
+    if (cur != dev) {
+      e = hipSetDevice(dev);
+      if (e != hipSuccess) return set_hip_error(e);
+    }
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    const hipError_t back = cur != dev ? hipSetDevice(cur) : hipSuccess;
     if (e != hipSuccess) return set_hip_error(e);
+    if (back != hipSuccess) return set_hip_error(back);
     if (!p) return CATOPT_E_HIP;
     g_scratch_ptr[dev] = p;
   }
@@ -756,7 +766,7 @@ extern "C" int32_t catopt_hip_affd_scan_noalloc(int64_t T, int64_t S, const floa
   if (affd_chunked(S, n_chunks, schedule)) {
     // reject before touching the device: the chunked workspace must fit
     if (catopt_hip_scan_workspace_bytes(S, n_chunks) > kAffdScratchBytes) return CATOPT_E_WORKSPACE;
-    st = affd_scratch(&ws);
+    st = affd_scratch(static_cast<hipStream_t>(stream), &ws);
     if (st != CATOPT_OK) return st;
   }
   return affd_scan_body(T, S, a, lda, u, ldu, h0, chunk_starts, n_chunks, schedule, states, h_final,

@@ -61,6 +61,7 @@ from .. import kernels as K
 from ..bindings import attr_of, scalar_value
 from ..evaluator import HipIRModule, _is_param, _is_var, eval_term
 from ..ir import IR, Op, is_op, postorder
+from ..planes import fit_plane, shared_plane
 from .base import HipExecutorBase
 
 __all__ = ["HipOMModule", "build_om_plan", "is_om_apply_term", "is_om_term", "mask_kwargs", "om_leaves",
@@ -354,17 +355,6 @@ def _cmask_causal_off(M: Any) -> int | None:
     return qstart - kstart - int(t.attrs.get("off", 0) or 0)
 
 
-def _shared_plane(t: torch.Tensor) -> torch.Tensor | None:
-    """The one ``(Tq, Tk)`` plane ``t`` holds over its leading axes, or
-    ``None`` when they carry different planes."""
-    if not isinstance(t, torch.Tensor) or t.dim() < 2:
-        return None
-    t3 = t.reshape(-1, *t.shape[-2:])
-    if t3.shape[0] != 1 and not bool(((t3 == t3[:1]) | (t3.isnan() & t3[:1].isnan())).all()):
-        return None
-    return t3[0]
-
-
 def _const_value(t: Any, eval_mod: HipIRModule) -> torch.Tensor | None:
     """The value of a weight-only mask term at construction: a (folded)
     Param, or any other parameter-only subtree (``split`` / ``slice`` /
@@ -386,15 +376,21 @@ def _const_value(t: Any, eval_mod: HipIRModule) -> torch.Tensor | None:
 
 
 def _keep_const(lf: dict, keep: torch.Tensor) -> None:
-    off = _triangle_offset(~keep)
-    if off is not None:
-        lf["mask_kind"], lf["causal_off"] = "causal", -off
-        return
-    plane = _shared_plane(keep)
+    """A weight-only keep-mask: its one plane over the leading axes, marked
+    ``causal`` when that plane is a triangle.  The plane keeps its own shape
+    (``(1, Tk)`` for a key-padding mask): :func:`mask_kwargs` fits it to the
+    score at call time, and a triangle counts as one only when it spans the
+    score's ``(Tq, Tk)``."""
+    plane = shared_plane(keep)
     if plane is None:
         lf["mask_kind"] = "scores"  # a per-batch mask
+        return
+    plane = plane.contiguous()
+    off = _triangle_offset(~plane)
+    if off is not None:
+        lf["mask_kind"], lf["causal_off"], lf["keep"] = "causal", -off, plane
     else:
-        lf["mask_kind"], lf["keep"] = "bool_const", plane.contiguous()
+        lf["mask_kind"], lf["keep"] = "bool_const", plane
 
 
 def _bias_const(lf: dict, bias: torch.Tensor) -> None:
@@ -402,7 +398,7 @@ def _bias_const(lf: dict, bias: torch.Tensor) -> None:
     if bool(((vals == 0) | (vals == float("-inf"))).all()):
         _keep_const(lf, vals == 0)  # a 0 / -inf bias is a keep-mask
         return
-    plane = _shared_plane(vals)
+    plane = shared_plane(vals)
     if plane is None:
         lf["mask_kind"] = "scores"
     else:
@@ -448,37 +444,55 @@ def _classify_mask(lf: dict, eval_mod: HipIRModule) -> bool:
     return True
 
 
-def mask_kwargs(lf: dict, ev) -> dict | None:
-    """Attention-kernel mask arguments of an ``attn`` leaf; ``None`` when the
-    call's mask is not one ``(Tq, Tk)`` plane shared over the leading axes
-    (the leaf then takes the score path)."""
+def _const_fit(lf: dict, key: str, arg: str, tq: int, tk: int) -> dict | None:
+    """``{arg: plane}`` for a weight-only plane fitted to ``(tq, tk)``,
+    cached per score shape; ``None`` when it does not broadcast to it."""
+    cache = lf.setdefault("_fit", {})
+    ck = (key, tq, tk)
+    if ck not in cache:
+        cache[ck] = fit_plane(lf[key], tq, tk)
+    plane = cache[ck]
+    return None if plane is None else {arg: plane}
+
+
+def mask_kwargs(lf: dict, ev, tq: int, tk: int) -> dict | None:
+    """Attention-kernel mask arguments of an ``attn`` leaf whose score is
+    ``(…, tq, tk)``; ``None`` when the call's mask is not one plane shared
+    over the leading axes that broadcasts to ``(tq, tk)`` (the leaf then
+    takes the score path)."""
     kind = lf["mask_kind"]
     if kind == "none":
         return {}
     if kind == "causal":
-        return {"causal": True, "causal_off": lf["causal_off"]}
+        keep = lf.get("keep")
+        if keep is None or tuple(keep.shape) == (tq, tk):
+            return {"causal": True, "causal_off": lf["causal_off"]}
+        return _const_fit(lf, "keep", "mask", tq, tk)  # a triangle of another shape broadcasts
     if kind == "bool_const":
-        return {"mask": lf["keep"]}
+        return _const_fit(lf, "keep", "mask", tq, tk)
     if kind == "bias_const":
-        return {"bias": lf["bias_plane"]}
+        return _const_fit(lf, "bias_plane", "bias", tq, tk)
     if kind == "runtime":
         masked = ev(lf["mask"])
         if not isinstance(masked, torch.Tensor) or masked.dtype != torch.bool:
             return None
-        plane = _shared_plane(masked)
-        return None if plane is None else {"mask": torch.logical_not(plane)}
+        plane = shared_plane(masked)
+        plane = None if plane is None else fit_plane(torch.logical_not(plane), tq, tk)
+        return None if plane is None else {"mask": plane}
     if kind == "bias_runtime":
         b = ev(lf["bias_term"])
         if not isinstance(b, torch.Tensor):
             return None
-        plane = _shared_plane(b)
+        if b.dtype == torch.bool:
+            if not lf["attnbias"]:
+                return None
+        elif not b.dtype.is_floating_point:
+            return None
+        plane = shared_plane(b)
+        plane = None if plane is None else fit_plane(plane, tq, tk)
         if plane is None:
             return None
-        if b.dtype == torch.bool:
-            return {"mask": plane} if lf["attnbias"] else None
-        if not b.dtype.is_floating_point:
-            return None
-        return {"bias": plane}
+        return {"mask": plane} if b.dtype == torch.bool else {"bias": plane}
     return None
 
 
@@ -513,6 +527,10 @@ def _as_bhtd(q, k, v):
     lead = tuple(q.shape[:-2])
     if k.shape[:-2] != q.shape[:-2] or v.shape[:-2] != q.shape[:-2] or k.shape[-2] != v.shape[-2]:
         return None, None, None, None
+    # a 3-D operand's leading axis is the batch (the kernel splits a batch
+    # past one launch's grid; its head extent must fit one launch)
+    if q.dim() == 3:
+        q, k, v = q.unsqueeze(1), k.unsqueeze(1), v.unsqueeze(1)
     while q.dim() < 4:
         q, k, v = q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0)
     return q, k, v, lead
@@ -610,11 +628,11 @@ class HipOMModule(HipExecutorBase, nn.Module):
                 return None
             self.kernel_leaves += 1
             return K.attn_carrier_f32(q, k, v, float(lf["scale"])), v.dtype
-        mask_kw = mask_kwargs(lf, ev)
+        mask_kw = mask_kwargs(lf, ev, q.shape[-2], k.shape[-2])
         if mask_kw is None:
             return None
         q4, k4, v4, lead = _as_bhtd(q, k, v)
-        if q4 is None:
+        if q4 is None or not K.attention_grid_ok(q4):
             return None
         self.kernel_leaves += 1
         if normalize:

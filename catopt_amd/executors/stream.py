@@ -86,7 +86,7 @@ def _carrier_qk(q, k, v, scale: float = 1.0, **mask_kw) -> tuple | None:
     if not _in_envelope(q, k, v):
         return None
     q4, k4, v4, lead = _as_bhtd(q, k, v)
-    if q4 is None:
+    if q4 is None or not K.attention_grid_ok(q4):
         return None
     a, m, lv = K.attention(q4, k4, v4, scale, normalize=False, return_ml=True, **mask_kw)
     tq, dv = a.shape[-2], a.shape[-1]
@@ -219,7 +219,7 @@ class HipStreamingOMModule(nn.Module):
                 e = None
                 if lf["kind"] == "qk":
                     q, k, v = ev(lf["q"]), ev(lf["k"]), ev(lf["v"])
-                    mkw = mask_kwargs(lf, ev)
+                    mkw = mask_kwargs(lf, ev, q.shape[-2], k.shape[-2])
                     if mkw is not None:
                         e = _carrier_qk(q, k, v, lf["scale"], **mkw)
                     if e is not None:

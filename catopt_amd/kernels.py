@@ -222,6 +222,18 @@ def _bhtd(t: torch.Tensor) -> tuple[torch.Tensor, list[int]]:
 ATTENTION_MAX_HEAD_DIM = 128
 
 
+#: Largest batch and head extents of one ``catopt_hip_attn_fwd`` launch
+#: (CATOPT_E_UNSUPPORTED beyond them).  :func:`attention` splits a larger
+#: batch into several launches; the head extent must fit one.
+ATTENTION_MAX_GRID_AXIS = 65535
+
+
+def attention_grid_ok(q4: torch.Tensor) -> bool:
+    """Whether :func:`attention` takes a ``(B, H, T, d)`` operand: any batch
+    extent, a head extent within one launch."""
+    return q4.dim() == 4 and q4.shape[1] <= ATTENTION_MAX_GRID_AXIS
+
+
 def attention(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -300,12 +312,18 @@ def attention(
         mode = L.MASK_BIAS
     elif causal:
         mode = L.MASK_CAUSAL
-    st = lib.catopt_hip_attn_fwd(
-        L.BF16, B, H, Tq, Tk, d, dv, _ptr(q), L.i64_array(qs), _ptr(k), L.i64_array(ks),
-        _ptr(v), L.i64_array(vs), float(scale), mode, int(causal_off), _ptr(mask_u8), mask_ld,
-        (2 if empty_rows == "zero" else 1) if normalize else 0, _ptr(o), L.i64_array([o.stride(0), o.stride(1), o.stride(2)]),
-        _ptr(m), _ptr(l), _stream(q))
-    L.check("catopt_hip_attn_fwd", st)
+    os_ = L.i64_array([o.stride(0), o.stride(1), o.stride(2)])
+    qs, ks, vs = L.i64_array(qs), L.i64_array(ks), L.i64_array(vs)
+    norm = (2 if empty_rows == "zero" else 1) if normalize else 0
+    # one launch per run of at most ATTENTION_MAX_GRID_AXIS batch entries:
+    # every operand, and the (B, H, Tq) statistics, advance by whole batches
+    for b0 in range(0, B, ATTENTION_MAX_GRID_AXIS):
+        nb = min(B - b0, ATTENTION_MAX_GRID_AXIS)
+        st = lib.catopt_hip_attn_fwd(
+            L.BF16, nb, H, Tq, Tk, d, dv, _ptr(q[b0:]), qs, _ptr(k[b0:]), ks, _ptr(v[b0:]), vs,
+            float(scale), mode, int(causal_off), _ptr(mask_u8), mask_ld, norm, _ptr(o[b0:]), os_,
+            _ptr(m[b0:] if m is not None else None), _ptr(l[b0:] if l is not None else None), _stream(q))
+        L.check("catopt_hip_attn_fwd", st)
     if return_ml:
         return o, m.unsqueeze(-1), l.unsqueeze(-1)
     return o

@@ -18,7 +18,13 @@
  *     and returned by catopt_hip_last_hip_error().
  *   - No entry point allocates device memory.  Workspace comes from the
  *     caller, sized by the matching *_workspace_bytes query.
- *   - Entry points are stateless and reentrant.
+ *   - State kept across calls: each kernel's maximum dynamic LDS is set on
+ *     its first launch and the device's CU count is read once; both sit in
+ *     function-static caches (idempotent; a concurrent first call writes
+ *     the same values).  catopt_hip_affd_scan_noalloc uses a file-scope
+ *     device array that each GPU holds until the process ends (see its
+ *     entry).  Entry points are otherwise reentrant, and calls that share
+ *     no output buffer may overlap on different streams.
  */
 #ifndef CATOPT_HIP_H
 #define CATOPT_HIP_H

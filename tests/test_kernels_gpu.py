@@ -140,6 +140,30 @@ def test_matmul_broadcast_batch(dev):
     _gate(_np(A) @ _np(B), y, TOL_BF16)
 
 
+@pytest.mark.parametrize("c_off,sc_pad", [(0, 4), (4, 0), (4, 4)])
+def test_matmul_bf16_c_rows_not_16_byte_aligned(dev, c_off, sc_pad):
+    # a batch stride of C that is 4 elements off a multiple of 8, or C itself
+    # 8 bytes off a 16-byte boundary: the epilogue stores column by column
+    # (its 16-byte stores need every row of every batch 16-byte aligned);
+    # the elements around each C[b] stay untouched
+    nb, M, N, Kd = 3, 64, 128, 96
+    A = _rand((nb, M, Kd), torch.bfloat16, 70).to(dev)
+    Bt = _rand((nb, N, Kd), torch.bfloat16, 71).to(dev)  # B given as Nx K rows: transB = 1
+    sC = M * N + sc_pad
+    buf = torch.full((c_off + nb * sC + 8,), 7.0, dtype=torch.bfloat16, device=dev)
+    lib = L.load()
+    st = lib.catopt_hip_matmul(L.BF16, nb, M, N, Kd, A.data_ptr(), Kd, M * Kd, 0, Bt.data_ptr(), Kd, N * Kd,
+                               1, buf.data_ptr() + 2 * c_off, N, sC, K._stream(A))
+    L.check("catopt_hip_matmul", st)
+    ref = _np(A) @ np.swapaxes(_np(Bt), 1, 2)
+    host = buf.float().cpu()
+    for b in range(nb):
+        _gate(ref[b], host[c_off + b * sC: c_off + b * sC + M * N].reshape(M, N).double().numpy(), TOL_BF16)
+        gap = host[c_off + b * sC + M * N: c_off + (b + 1) * sC]
+        assert bool((gap == 7.0).all())
+    assert bool((host[:c_off] == 7.0).all()) and bool((host[c_off + nb * sC:] == 7.0).all())
+
+
 # ------------------------------------------------------------------ attention
 
 

@@ -236,14 +236,48 @@ def test_runtime_mask_kwargs_take_one_shared_plane():
     T = 8
     lf = {"mask_kind": "bias_runtime", "bias_term": "b", "attnbias": True}
     keep = torch.rand(T, T) < 0.5
-    assert torch.equal(mask_kwargs(lf, lambda t: keep.expand(2, 3, T, T))["mask"], keep)
+    assert torch.equal(mask_kwargs(lf, lambda t: keep.expand(2, 3, T, T), T, T)["mask"], keep)
     bias = torch.randn(T, T)
-    assert torch.equal(mask_kwargs(lf, lambda t: bias)["bias"], bias)
-    assert mask_kwargs(lf, lambda t: torch.randn(2, T, T)) is None  # differs over the batch
+    assert torch.equal(mask_kwargs(lf, lambda t: bias, T, T)["bias"], bias)
+    assert mask_kwargs(lf, lambda t: torch.randn(2, T, T), T, T) is None  # differs over the batch
     lf2 = dict(lf, attnbias=False)
-    assert mask_kwargs(lf2, lambda t: keep) is None  # add(s, bool) is not a mask
+    assert mask_kwargs(lf2, lambda t: keep, T, T) is None  # add(s, bool) is not a mask
     lf3 = {"mask_kind": "runtime", "mask": "m"}
-    assert torch.equal(mask_kwargs(lf3, lambda t: ~keep)["mask"], keep)
+    assert torch.equal(mask_kwargs(lf3, lambda t: ~keep, T, T)["mask"], keep)
+    # a key-padding plane (one query row) broadcasts over the score's rows
+    pad = torch.tensor([[True, True, True, False, False, False, False, False]])
+    got = mask_kwargs(lf3, lambda t: ~pad.reshape(1, 1, 1, T), T, T)["mask"]
+    assert got.shape == (T, T) and torch.equal(got, pad.expand(T, T))
+    # planes that do not broadcast to the score's (Tq, Tk) take the score path
+    assert mask_kwargs(lf3, lambda t: ~keep[:4], T, T) is None
+    assert mask_kwargs(lf, lambda t: torch.randn(T, T + 1), T, T) is None
+
+
+def test_const_planes_fit_the_score_shape_at_call_time():
+    """A weight-only plane with one query row is never read as a triangle of
+    that one row: a 0/-inf bias keeping keys 0..2 of 8 keeps keys 0..2 for
+    every query row, and a (T, T) triangle is causal only for a (T, T)
+    score."""
+    from catopt_amd.executors.om import _bias_const, _keep_const
+    T = 8
+    bias = torch.full((1, 1, 1, T), float("-inf"))
+    bias[..., :3] = 0.0
+    lf: dict = {}
+    _bias_const(lf, bias)
+    kw = mask_kwargs(lf, None, T, T)
+    assert "causal" not in kw and torch.equal(kw["mask"], (bias[0, 0] == 0).expand(T, T))
+    assert mask_kwargs(lf, None, 1, T) == {"causal": True, "causal_off": 2}  # one row: the same set
+    tri = torch.ones(T, T, dtype=torch.bool).tril()
+    lf = {}
+    _keep_const(lf, tri)
+    assert lf["mask_kind"] == "causal" and mask_kwargs(lf, None, T, T) == {"causal": True, "causal_off": 0}
+    assert mask_kwargs(lf, None, T, T + 1) is None  # the plane is (T, T)
+    lf = {}
+    _keep_const(lf, torch.rand(T, 1) < 0.5)  # a row mask broadcasts over the keys
+    assert mask_kwargs(lf, None, T, 5)["mask"].shape == (T, 5)
+    lf = {}
+    _bias_const(lf, torch.randn(1, T))
+    assert lf["mask_kind"] == "bias_const" and mask_kwargs(lf, None, 3, T)["bias"].shape == (3, T)
 
 
 def test_every_om_tree_plans_and_host_calls_run_the_generic_module():

@@ -33,11 +33,12 @@ def _table(T, n):
     return torch.tensor(starts, dtype=torch.int64)
 
 
-def _run(lib, noalloc, a, u, h0, cs, nc, schedule, dev):
+def _run(lib, noalloc, a, u, h0, cs, nc, schedule, dev, stream=None):
     T, S = u.shape
     states = torch.full((T, S), float("nan"), device=dev)
     hf = torch.full((S,), float("nan"), device=dev)
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    torch.cuda.synchronize(dev)  # inputs in place before a side stream reads them
+    stream = (stream or torch.cuda.current_stream(dev)).cuda_stream
     if noalloc:
         st = lib.catopt_hip_affd_scan_noalloc(T, S, a.data_ptr(), S, u.data_ptr(), S, h0.data_ptr(),
                                               cs.data_ptr(), nc, schedule, states.data_ptr(), hf.data_ptr(),
@@ -90,3 +91,17 @@ def test_noalloc_rejects_a_workspace_beyond_its_array(dev):
     ref_states, ref_hf = _run(lib, False, a, u, h0, cs2, T2, L.SCAN_CHUNKED, dev)
     assert torch.equal(got_states, ref_states) and torch.equal(got_hf, ref_hf)
     assert np.isfinite(got_hf.cpu().numpy()).all()
+
+
+def test_noalloc_on_a_side_stream(dev):
+    # the scratch address is resolved on the stream's device (here a stream
+    # of default priority other than the current one)
+    lib = L.load()
+    side = torch.cuda.Stream(device=dev)
+    T, S, n = 2000, 800, 40
+    a, u, h0 = _inputs(T, S, 4, dev)
+    cs = _table(T, n).to(dev)
+    nc = cs.numel() - 1
+    ref_states, ref_hf = _run(lib, False, a, u, h0, cs, nc, L.SCAN_CHUNKED, dev)
+    got_states, got_hf = _run(lib, True, a, u, h0, cs, nc, L.SCAN_CHUNKED, dev, stream=side)
+    assert torch.equal(got_states, ref_states) and torch.equal(got_hf, ref_hf)
