@@ -117,9 +117,11 @@ __device__ __forceinline__ void dma4(const void* gptr, uint32_t lds_wave) {
 // write of M0 and an LDS-DMA load reading it (the compiler cannot insert it
 // inside inline asm; without it the load can take the previous M0 and land in
 // another load's place).  Inline asm for the reason given at dma16.
+// `lds` goes through readfirstlane: under SGPR pressure the compiler may hold
+// a uniform value in a VGPR, which an "s" operand cannot take.
 __device__ __forceinline__ void dma_buf(u32x4 rsrc, uint32_t voff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-               :: "v"(voff), "s"(rsrc), "s"(lds) : "m0", "memory");
+               :: "v"(voff), "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(lds)) : "m0", "memory");
 }
 
 // Buffer resource (raw, stride 0) over `bytes` bytes from `base`.

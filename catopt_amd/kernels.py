@@ -385,36 +385,35 @@ RETENTION_HEAD_DIM = 128
 def retention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma: torch.Tensor,
               scale: float = 1.0) -> torch.Tensor:
     """``scale * Σ_{s<=t} γ_h^(t-s) (q_t·k_s) v_s`` for ``q, k (B,H,T,dk)``,
-    ``v (B,H,T,dv)`` bf16, ``dk, dv <= 128``.  Below 128 the heads run
-    zero-padded to the kernel's 128 (zero columns leave q·k unchanged and add
-    zero output columns, dropped); a ``T`` that is not a multiple of the
-    kernel's 64-step chunk runs zero-padded at the end of the time axis (the
-    sum is causal, so the padded steps change no output row before them;
-    their rows are dropped)."""
+    ``v (B,H,T,dv)`` bf16, ``dk, dv <= 128``.  The kernel reads a head dim
+    ``d`` (a multiple of 8) and any ``T`` in place: columns past ``d`` and
+    rows past ``T`` of its 64-step chunks load as zeros and are never stored.
+    When ``dk`` and ``dv`` differ, or are not multiples of 8, the narrower
+    operands run zero-padded to the common width (zero columns leave q·k
+    unchanged and add zero output columns, dropped)."""
     _need_device(q, k, v, gamma)
     lib = L.load()
     if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
         raise NotImplementedError("HIP retention runs on bf16 operands")
     if q.dim() != 4 or q.shape != k.shape or v.dim() != 4 or v.shape[:3] != q.shape[:3]:
         raise ValueError("retention operands must be q, k (B, H, T, dk) and v (B, H, T, dv)")
-    B, H, T, d = q.shape
+    B, H, T, dk = q.shape
     dv = v.shape[-1]
-    if max(d, dv) > RETENTION_HEAD_DIM:
+    if max(dk, dv) > RETENTION_HEAD_DIM:
         raise NotImplementedError(f"HIP retention needs dk, dv <= {RETENTION_HEAD_DIM}")
     if T == 0 or B * H == 0:
         return torch.zeros_like(v)
-    pk, pv, pt = RETENTION_HEAD_DIM - d, RETENTION_HEAD_DIM - dv, (-T) % RETENTION_CHUNK
-    if pk or pv or pt:
+    d = -(-max(dk, dv, 8) // 8) * 8
+    if dk != d or dv != d:
         pad = torch.nn.functional.pad
-        q, k = (pad(t, (0, pk, 0, pt)) for t in (q, k))
-        v = pad(v, (0, pv, 0, pt))
-        return retention(q, k, v, gamma, scale)[..., :T, :dv]
-    d = RETENTION_HEAD_DIM
+        q, k = (pad(t, (0, d - dk)) for t in (q, k))
+        v = pad(v, (0, d - dv))
+        return retention(q, k, v, gamma, scale)[..., :dv]
     g = gamma.to(torch.float32).reshape(-1).contiguous()
     if g.numel() != H:
         raise ValueError("gamma must hold one rate per head")
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-    o = torch.empty_like(q)
+    o = torch.empty_like(v)
     wsb = lib.catopt_hip_retention_workspace_bytes(B, H, T, d, RETENTION_CHUNK)
     if wsb < 0:
         raise ValueError("retention workspace query rejected the shape")
