@@ -636,8 +636,11 @@ extern "C" int64_t catopt_hip_retention_workspace_bytes(int64_t B, int64_t H, in
   if (B < 0 || H < 0 || T < 0 || !dims_ok(d, d) || chunk != CH) return -1;
   const int64_t BH = B * H, nch = (T + CH - 1) / CH;
   if (BH == 0 || nch == 0) return 0;
-  int n_cu = 0;
-  if (cu_count_of_current_device(&n_cu) != CATOPT_OK) return -1;
+  // the current device's segment count; without a device, the most any
+  // device can take (the bound on segments alone)
+  int n_cu = 0, dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    n_cu = 0x3fffffff;
   const int P = n_segments(BH, nch, n_cu);
   if (P == 1) return 0;
   return BH * 2 * P * WFLOATS * (int64_t)sizeof(float);  // two state pieces per range

@@ -62,9 +62,17 @@ def test_version_and_status_text(lib):
 
 
 def test_workspace_queries(lib):
-    # retention: single pass, the carried state lives in registers; rejects other d / chunk
-    assert lib.catopt_hip_retention_workspace_bytes(4, 16, 8192, 128, 64) == 0
-    assert lib.catopt_hip_retention_workspace_bytes(1, 1, 64, 96, 64) == -1
+    # retention: two 64 KB fp32 state pieces per (b·h, segment) before the
+    # output pass, segments chosen from the CU count (without a device, the
+    # bound: 8 segments); head dims are multiples of 8 up to 128, chunk 64
+    piece = 128 * 128 * 4
+    ws = lib.catopt_hip_retention_workspace_bytes(4, 16, 8192, 128, 64)
+    assert ws % (4 * 16 * 2 * piece) == 0 and 0 < ws <= 4 * 16 * 2 * 8 * piece
+    assert lib.catopt_hip_retention_workspace_bytes(1, 1, 1024, 96, 64) > 0
+    assert lib.catopt_hip_retention_workspace_bytes(1, 1, 64, 96, 64) == 0  # one chunk: one segment
+    assert lib.catopt_hip_retention_workspace_bytes(64, 16, 64, 128, 64) == 0  # one segment: no pieces
+    assert lib.catopt_hip_retention_workspace_bytes(1, 1, 64, 100, 64) == -1
+    assert lib.catopt_hip_retention_workspace_bytes(1, 1, 64, 136, 64) == -1
     assert lib.catopt_hip_retention_workspace_bytes(1, 1, 64, 128, 32) == -1
     assert lib.catopt_hip_scan_workspace_bytes(10, 3) == 2 * 10 * 3 * 4
     assert lib.catopt_hip_scan_workspace_bytes(-1, 3) == -1
