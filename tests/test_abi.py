@@ -105,8 +105,13 @@ def test_host_argument_checks(lib):
     assert lib.catopt_hip_linear(L.BF16, 4, 4, 4, None, 4, None, 4, None, None, 9, None, 4, None) == L.E_INVAL
     assert lib.catopt_hip_linear(7, 4, 4, 4, None, 4, None, 4, None, None, 0, None, 4, None) == L.E_UNSUPPORTED
     assert lib.catopt_hip_linear(L.F32, 0, 4, 4, None, 4, None, 4, None, None, 0, None, 4, None) == L.OK
-    assert lib.catopt_hip_retention_fwd(L.BF16, 1, 1, 100, 128, 64, None, None, None, None, 1.0,
+    # retention: a head dim off the multiples of 8 is outside the kernel; a
+    # ragged T is inside it (rows past T load as zeros), so null operands
+    # are the error there
+    assert lib.catopt_hip_retention_fwd(L.BF16, 1, 1, 100, 100, 64, None, None, None, None, 1.0,
                                         None, None, 0, None) == L.E_UNSUPPORTED
+    assert lib.catopt_hip_retention_fwd(L.BF16, 1, 1, 100, 128, 64, None, None, None, None, 1.0,
+                                        None, None, 0, None) == L.E_INVAL
     zeros = (C.c_int64 * 3)(0, 0, 0)
     assert lib.catopt_hip_attn_fwd(L.BF16, 1, 1, 8, 8, 96, 96, None, zeros, None, zeros, None, zeros,
                                    1.0, L.MASK_CAUSAL, 0, None, 0, 1, None, zeros, None, None,
