@@ -7,7 +7,9 @@ attention kernel's XCD remap in causal mode.  Here
 those branches run, as do the persistent GEMM's multi-round tile streams
 (C2's GEMMs), and C2–C5 are delivered through ``HipSink`` at their full
 shapes, with every output element of sampled tiles compared against the
-numpy oracle in float64:
+numpy oracle in float64 (the pinned parity), and every output element of
+C2–C5 compared against an independent fp32 torch computation on the device
+(the whole-output tests at the end):
 
 * C2 (x[8,2048,4096] bf16): the first and the last 256-row M-tile, all
   4096 output columns (every N-tile of both GEMMs);
@@ -235,4 +237,137 @@ def test_c5_full_shape_last_batch_and_channels(sink, dev):
         got = _np(y[b:b + 1, :, sl])
         _gate(ys, got, TOL_F32)
         _gate(ys[:, 12288:], got[:, 12288:], TOL_F32)
+    del a
+
+
+# ------------------------------------------- whole outputs at full shapes
+#
+# Every output element of C2–C5 against an independent fp32 torch
+# computation on the device, written from each model's definition (not from
+# the kernels' algebra), chunked to bound memory: C2 fp32 rms_norm and
+# matmuls per block of rows; C3 fp32 masked softmax attention per block of
+# heads; C4 the quadratic decayed form per head (both chunk lengths the
+# delivered K-way form takes); C5 the serial recurrence over every lane.
+# The gate is the verify metric over the whole output, max|Δ| / max|ref|,
+# taken across all blocks (the sampled oracle slices above stay the pinned
+# parity).
+
+
+class _WholeGate:
+    """max|Δ| and max|ref| accumulated over blocks of one output."""
+
+    def __init__(self):
+        self.dmax = 0.0
+        self.rmax = 0.0
+
+    def add(self, ref: torch.Tensor, out: torch.Tensor) -> None:
+        out = out.float()
+        assert bool(torch.isfinite(out).all()), "non-finite output"
+        self.dmax = max(self.dmax, (out - ref).abs().max().item())
+        self.rmax = max(self.rmax, ref.abs().max().item())
+
+    def check(self, tol: float) -> float:
+        rel = self.dmax / (self.rmax + 1e-8)
+        print(f"[whole-output] max_rel={rel:.3e} (gate {tol:g})", flush=True)
+        assert rel <= tol, (rel, self.dmax, self.rmax)
+        return rel
+
+
+def test_c2_whole_output(sink, dev):
+    D, F = 4096, 11008
+    g = torch.Generator(device=dev).manual_seed(1)
+    bf = torch.bfloat16
+    x = torch.randn(8, 2048, D, device=dev, generator=g).to(bf)
+    vals = {
+        "gamma": (1 + 0.02 * torch.randn(D, device=dev, generator=g)).to(bf),
+        "W_gate": (0.02 * torch.randn(F, D, device=dev, generator=g)).to(bf),
+        "W_up": (0.02 * torch.randn(F, D, device=dev, generator=g)).to(bf),
+        "W_down": (0.02 * torch.randn(D, F, device=dev, generator=g)).to(bf),
+    }
+    ir, _ = forms.swiglu_block_form((8, 2048), D, F)
+    res = deliver(ir, vals, sink, (x,))
+    y = res.module(x).reshape(-1, D)
+    gam, wg, wu, wd = (vals[n].float() for n in ("gamma", "W_gate", "W_up", "W_down"))
+    x2 = x.reshape(-1, D)
+    gate = _WholeGate()
+    for r0 in range(0, x2.shape[0], 2048):
+        xs = x2[r0:r0 + 2048].float()
+        h = xs * torch.rsqrt(xs.pow(2).mean(-1, keepdim=True) + 1e-6) * gam
+        ref = (torch.nn.functional.silu(h @ wg.T) * (h @ wu.T)) @ wd.T
+        gate.add(ref, y[r0:r0 + 2048])
+    gate.check(TOL_BF16)
+
+
+def test_c3_whole_output(sink, dev):
+    B, H, T, d = 4, 32, 4096, 128
+    g = torch.Generator(device=dev).manual_seed(1)
+    q, k, v = (torch.randn((B, H, T, d), device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
+    ir, _ = forms.causal_attention_form(B, H, T, d, mask="param")
+    mask = torch.ones(T, T, dtype=torch.bool, device=dev).tril()
+    res = deliver(ir, {"mask": mask}, sink, (q, k, v))
+    o = res.module(q, k, v)
+    gate = _WholeGate()
+    keep = torch.ones(T, T, dtype=torch.bool, device=dev).tril()
+    for b in range(B):
+        for h0 in range(0, H, 8):
+            qs, ks, vs = (t[b, h0:h0 + 8].float() for t in (q, k, v))
+            s = (qs @ ks.transpose(-1, -2).contiguous()) / math.sqrt(d)
+            ref = torch.softmax(s.masked_fill(~keep, float("-inf")), dim=-1) @ vs
+            gate.add(ref, o[b, h0:h0 + 8])
+            del s, ref
+    gate.check(TOL_BF16)
+
+
+@pytest.mark.parametrize("C", [64, 128])
+def test_c4_whole_output(sink, dev, C):
+    B, H, T, d = 4, 16, 8192, 128
+    g = torch.Generator(device=dev).manual_seed(1)
+    sd = 1 / math.sqrt(d)
+    q, k, v = ((torch.randn((B, H, T, d), device=dev, generator=g) * sd).to(torch.bfloat16) for _ in range(3))
+    gamma = torch.tensor([1 - 2.0 ** (-5 - h / 2) for h in range(H)], dtype=torch.float32, device=dev)
+    ir, _ = forms.retention_kway_form(B, H, T, d, C)
+    res = deliver(ir, {"gamma": gamma}, sink, (q, k, v))
+    assert res.module.n_chunks == T // C and res.module.fallbacks == 0
+    o = res.module(q, k, v)
+    gate = _WholeGate()
+    pos = torch.arange(T, device=dev, dtype=torch.float32)
+    R = 2048  # query rows per block: o[t] = Σ_{s<=t} γ^(t-s) (q_t·k_s) v_s
+    for h in range(H):
+        lg = math.log2(float(gamma[h]))
+        for r0 in range(0, T, R):
+            t = pos[r0:r0 + R, None]
+            s = pos[None, :r0 + R]
+            dec = torch.where(s <= t, torch.exp2((t - s) * lg), torch.zeros((), device=dev))
+            for b in range(B):
+                qs = q[b, h, r0:r0 + R].float()
+                ks, vs = k[b, h, :r0 + R].float(), v[b, h, :r0 + R].float()
+                ref = ((qs @ ks.T) * dec) @ vs
+                gate.add(ref, o[b, h, r0:r0 + R])
+            del dec
+    gate.check(TOL_BF16)
+
+
+def test_c5_whole_output(sink, dev):
+    B, D, N, T = 16, 2048, 16, 16384
+    g = torch.Generator(device=dev).manual_seed(1)
+    a = torch.randn((B, T, D, N), device=dev, generator=g).neg_().sigmoid_()  # exp(-softplus(z))
+    bx = torch.randn((B, T, N), device=dev, generator=g)
+    c = torch.randn((B, T, N), device=dev, generator=g)
+    x = torch.randn((B, T, D), device=dev, generator=g)
+    h0 = torch.zeros((B, D, N), device=dev)
+    ir, _ = forms.diag_ssm_form(B, T, D, N)
+    res = deliver(ir, {}, sink, (a, bx, c, x, h0))
+    y = res.module(a, bx, c, x, h0)
+    # h_t = a_t ⊙ h_{t-1} + x_t ⊗ bx_t, y_t = h_t · c_t, every lane, serially
+    gate = _WholeGate()
+    h = h0.clone()
+    blk = 512
+    ref = torch.empty((B, blk, D), device=dev)
+    for t0 in range(0, T, blk):
+        for i in range(blk):
+            t = t0 + i
+            h = a[:, t] * h + x[:, t, :, None] * bx[:, t, None, :]
+            ref[:, i] = (h * c[:, t, None, :]).sum(-1)
+        gate.add(ref, y[:, t0:t0 + blk])
+    gate.check(TOL_F32)
     del a

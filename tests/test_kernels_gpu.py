@@ -286,6 +286,22 @@ def test_retention_narrow_heads(dev, dk, dv):
     _gate(ref, o, TOL_BF16)
 
 
+@pytest.mark.parametrize("B,H,T,d", [(1, 3, 1000, 64), (2, 2, 200, 120), (1, 5, 4100, 128), (3, 1, 70, 8)])
+def test_retention_ragged_steps_and_narrow_heads_in_the_kernel(dev, B, H, T, d):
+    # a T off the 64-step chunk and head dims below 128 (multiples of 8) run
+    # in place: the kernel's buffer ranges load zeros past T and past d and
+    # drop the stores there (no padded copies); (1, 5, 4100, 128) spans
+    # several segments, the last one ragged
+    q = _rand((B, H, T, d), torch.bfloat16, 130, 1 / math.sqrt(d))
+    k = _rand((B, H, T, d), torch.bfloat16, 131, 1 / math.sqrt(d))
+    v = _rand((B, H, T, d), torch.bfloat16, 132, 1 / math.sqrt(d))
+    gam = _gammas(H)
+    o = K.retention(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(gam).to(dev), 0.9)
+    assert o.shape == (B, H, T, d)
+    ref = oracle.retention_quadratic(_np(q), _np(k), _np(v), gam.astype(np.float64), 0.9)
+    _gate(ref, o, TOL_BF16)
+
+
 def test_retention_long_many_segments(dev):
     # 64 chunks over one (b,h): exercises the segment carry pass.
     B, H, T = 1, 2, 4096
