@@ -23,10 +23,13 @@ Per form:
   * ``roofline``     — the form's dominant kernel timed alone the same way:
     algorithmic flops (MFMA-bound) or bytes (HBM-bound) per launch divided by
     its average launch duration, against MI355X's published peak;
-  * ``cpu_baseline`` — the numpy oracle (``oracle/``, the CPU restatement of
-    the reference's delivered-module arithmetic) timed on a bounded sample of
-    the same inputs on this host; its outputs double as a parity check of
-    the GPU outputs on that sample (``parity_max_rel``).
+  * ``cpu_baseline`` — the delivered form's op sequence as eager torch ops on
+    the host CPU (``oracle/torch_cpu.py``, the reference's own execution
+    style, pinned against the numpy oracle), with torch's pool set to every
+    CPU this process may use, timed on a bounded sample of the same inputs:
+    median and IQR per the reference's timing contract (``timing.py:54-80``);
+    its outputs double as a parity check of the GPU outputs on that sample
+    (``parity_max_rel``).
 
 Only rank 0 of one process prints, one JSON line on stdout.  ``--gpus`` above
 1 exits with a message: this build measures one GPU.
@@ -38,6 +41,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -175,12 +179,6 @@ def _blas_threads() -> int:
         return 1
 
 
-def cpu_threads() -> int:
-    """Threads a BLAS-backed numpy baseline can use: the BLAS pool, capped by
-    the CPUs this process may run on."""
-    return max(1, min(_blas_threads(), len(os.sched_getaffinity(0))))
-
-
 def host_provenance() -> dict:
     """What the CPU baseline ran on: CPU model, the CPUs this process may
     use, the BLAS pool, and the library versions."""
@@ -197,12 +195,16 @@ def host_provenance() -> dict:
     except OSError:  # pragma: no cover
         pass
     return {"cpu_model": model, "affinity_cpus": len(os.sched_getaffinity(0)), "os_cpu_count": os.cpu_count(),
-            "blas_threads": _blas_threads(), "torch": torch.__version__, "numpy": numpy.__version__,
+            "blas_threads": _blas_threads(), "torch_threads": len(os.sched_getaffinity(0)),
+            "torch": torch.__version__, "numpy": numpy.__version__,
             "python": sys.version.split()[0]}
 
 
-def time_cpu(fn, budget_s: float, min_reps: int = 2) -> tuple[float, int, object]:
-    """Median seconds per call of ``fn`` (≥ ``min_reps`` calls, ~``budget_s`` total)."""
+def time_cpu(fn, budget_s: float, min_reps: int = 4) -> tuple[float, float, int, object]:
+    """Median and IQR of seconds per call of ``fn`` (≥ ``min_reps`` calls,
+    about ``budget_s`` in all, at most 50), the reference's timing contract
+    (``timing.py:54-80``: median, and the IQR from quartiles at n = 4, 0.0
+    below 4 samples)."""
     times, out = [], None
     t_start = time.perf_counter()
     while len(times) < min_reps or time.perf_counter() - t_start < budget_s:
@@ -211,8 +213,37 @@ def time_cpu(fn, budget_s: float, min_reps: int = 2) -> tuple[float, int, object
         times.append(time.perf_counter() - t0)
         if len(times) >= 50:
             break
-    times.sort()
-    return times[len(times) // 2], len(times), out
+    med = statistics.median(times)
+    iqr = 0.0
+    if len(times) >= 4:
+        q1, _, q3 = statistics.quantiles(times, n=4)
+        iqr = q3 - q1
+    return med, iqr, len(times), out
+
+
+class host_threads:
+    """torch's intra-op pool set to every CPU this process may run on, for
+    the CPU baseline (restored afterwards)."""
+
+    def __enter__(self):
+        import torch
+
+        self.prev = torch.get_num_threads()
+        self.n = len(os.sched_getaffinity(0))
+        torch.set_num_threads(self.n)
+        return self
+
+    def __exit__(self, *exc):
+        import torch
+
+        torch.set_num_threads(self.prev)
+
+
+def cpu_record(value: float, iqr_value: float, unit: str, cores: int, sample: str, reps: int,
+               rel: float) -> dict:
+    return {"value": value, "iqr": iqr_value, "unit": unit, "cores": cores, "kind": "port",
+            "impl": "torch (the delivered form's eager ops on the host CPU, oracle/torch_cpu.py)",
+            "sample": f"{sample}, median of {reps} reps", "parity_max_rel": rel}
 
 
 # --------------------------------------------------------------------- traffic
@@ -223,10 +254,14 @@ FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
 TRAFFIC_TABLE = ROOT / "profiles" / "pmc_traffic_all_forms.md"
 
 
-def traffic_bytes(kernel_key: str) -> float | None:
+def traffic_bytes(kernel_key) -> float | None:
     """HBM bytes per launch of a kernel from the committed counter summary:
     (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0) KiB per dispatch, averaged over
-    its dispatches (rows ``| key | fetch KiB | write KiB | ... |``)."""
+    its dispatches (rows ``| key | fetch KiB | write KiB | ... |``).  A tuple
+    of keys (a dominant unit of several launches) sums its rows."""
+    if isinstance(kernel_key, tuple):
+        parts = [traffic_bytes(k) for k in kernel_key]
+        return None if any(p is None for p in parts) else sum(parts)
     if not kernel_key or not TRAFFIC_TABLE.exists():
         return None
     for line in TRAFFIC_TABLE.read_text().splitlines():
@@ -347,21 +382,15 @@ class C1WeightChain(Form):
     dominant_in_graph = True
 
     def cpu(self, budget):
-        import numpy as np
-
         import oracle
 
-        x = self.x_cpu.numpy()
-        W, adds = oracle.fold_linear_chain(self.Ws_cpu, self.bs_cpu)
-        sec, reps, out = time_cpu(lambda: oracle.folded_chain_forward(x, W, adds), budget, 20)
-        ref = oracle.linear_chain(x.astype(np.float64), [w.astype(np.float64) for w in self.Ws_cpu],
-                                  [b.astype(np.float64) for b in self.bs_cpu])
+        x, W, c = (t.detach().float().cpu() for t in (self.x, self.W_eff, self.c))
+        with host_threads() as ht:
+            sec, iqr, reps, out = time_cpu(lambda: oracle.torch_cpu.weight_chain(x, W, c), budget)
         self.step()
-        rel = oracle.verify_equiv(ref, self.y.cpu().double().numpy())["max_rel"]
-        return {"value": self.work / sec / 1e12, "unit": "TFLOP/s", "cores": cpu_threads(),
-                "kind": "port", "sample": f"full C1 forward (folded form, numpy fp32), {reps} reps",
-                "parity_max_rel": rel}
-
+        rel = oracle.verify_equiv(out.double().numpy(), self.y.cpu().double().numpy())["max_rel"]
+        return cpu_record(self.work / sec / 1e12, self.work * iqr / sec ** 2 / 1e12, "TFLOP/s", ht.n,
+                          "full C1 forward (the folded linear, fp32)", reps, rel)
 
 class C2SwiGLU(Form):
     name, dtype, unit, bound = "c2", "bf16", "TFLOP/s", "mfma"
@@ -416,30 +445,20 @@ class C2SwiGLU(Form):
         self.K.linear(self.h, self.w_cat, epilogue=self.L.EPI_SILU_MUL)
 
     def cpu(self, budget):
-        import numpy as np
-
         import oracle
 
-        rows = 256
-        x = self.x.reshape(-1, self.D)[:rows].float().cpu().numpy()
-        gam = self.gamma.float().cpu().numpy()
-        wcat = self.w_cat.float().cpu().numpy()
+        rows = 2048
+        x = self.x.reshape(-1, self.D)[:rows].cpu()
+        gam, wcat, wd = (t.cpu() for t in (self.gamma, self.w_cat, self.w_down))
         wg, wu = wcat[: self.F], wcat[self.F:]
-        wd = self.w_down.float().cpu().numpy()
-
-        def run():
-            return oracle.swiglu_fused(oracle.rms_norm(x, gam, 1e-6), wg, wu, wd)
-
-        sec, reps, out = time_cpu(run, budget)
+        with host_threads() as ht:
+            sec, iqr, reps, out = time_cpu(lambda: oracle.torch_cpu.swiglu_block(x, gam, wg, wu, wd, 1e-6), budget)
         self.step()
-        y = self.y.reshape(-1, self.D)[:rows].float().cpu().numpy()
-        rel = oracle.verify_equiv(out, y)["max_rel"]
+        rel = oracle.verify_equiv(out.double().numpy(), self.y.reshape(-1, self.D)[:rows].cpu().double().numpy())["max_rel"]
         flops = self.work * rows / self.M
-        return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": cpu_threads(),
-                "kind": "port",
-                "sample": f"first {rows} of {self.M} rows through rms_norm+swiglu (numpy fp32), {reps} reps",
-                "parity_max_rel": rel}
-
+        return cpu_record(flops / sec / 1e12, flops * iqr / sec ** 2 / 1e12, "TFLOP/s", ht.n,
+                          f"first {rows} of {self.M} rows: rms_norm, fused gate/up linear, silu*mul, down linear (bf16)",
+                          reps, rel)
 
 class C3Attention(Form):
     name, dtype, unit, bound = "c3", "bf16", "TFLOP/s", "mfma"
@@ -483,16 +502,16 @@ class C3Attention(Form):
     def cpu(self, budget):
         import oracle
 
-        q, k, v = (t[0, 0].float().cpu().numpy() for t in (self.q, self.k, self.v))
-        sec, reps, out = time_cpu(lambda: oracle.attention_om(q, k, v, self.scale, causal=True), budget)
+        nh = 4  # heads (b = 0, h = 0..3) of the 128; heads are independent
+        q, k, v = (t[0, :nh].cpu() for t in (self.q, self.k, self.v))
+        with host_threads() as ht:
+            sec, iqr, reps, out = time_cpu(lambda: oracle.torch_cpu.causal_attention(q, k, v, self.scale), budget)
         self.step()
-        rel = oracle.verify_equiv(out, self.o[0, 0].float().cpu().numpy())["max_rel"]
-        flops = self.work / (self.B * self.H)
-        return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": cpu_threads(),
-                "kind": "port",
-                "sample": f"one (b,h) of {self.B * self.H}: T=4096 single-leaf om form (numpy fp32), {reps} reps",
-                "parity_max_rel": rel}
-
+        rel = oracle.verify_equiv(out.double().numpy(), self.o[0, :nh].cpu().double().numpy())["max_rel"]
+        flops = self.work * nh / (self.B * self.H)
+        return cpu_record(flops / sec / 1e12, flops * iqr / sec ** 2 / 1e12, "TFLOP/s", ht.n,
+                          f"{nh} of {self.B * self.H} heads, T={self.T}: matmul, masked_fill, softmax, matmul (bf16; "
+                          "work counted as the causal half)", reps, rel)
 
 class C4Retention(Form):
     name, dtype, unit, bound = "c4", "bf16", "GB/s", "hbm"
@@ -502,8 +521,10 @@ class C4Retention(Form):
     peak = PEAK["hbm_gbs"]
     work = dom_work = 4.0 * B * H * T * Dh * 2  # q, k, v read + o written, bf16
     flops = B * H * (T / C) * (4 * C * C * Dh + 4 * C * Dh * Dh)
-    dom_name = "retention_scan"
-    dom_key = "retention_scan"
+    # the dominant unit is one retention call: the state pass (the start
+    # states of the T-segments) and the output pass, back to back
+    dom_name = "retention_state + retention_out"
+    dom_key = ("retention_state", "retention_out")
 
     def setup(self, dev):
         import torch
@@ -537,21 +558,19 @@ class C4Retention(Form):
         self.K.retention(self.q, self.k, self.v, self.gamma, 1.0)
 
     def cpu(self, budget):
-        import numpy as np
-
         import oracle
 
-        Ts = 1024  # the first 1024 steps of one (b,h): causal, so a prefix is exact
-        q, k, v = (t[0, :1, :Ts].float().cpu().numpy() for t in (self.q, self.k, self.v))
-        g = self.gamma[:1].cpu().numpy().astype(np.float32)
-        sec, reps, out = time_cpu(lambda: oracle.retention_kway(q, k, v, g, Ts // self.C, 1.0), budget)
+        Ts = 2048  # every head of batch 0, the first 2048 steps (causal: a prefix is exact)
+        q, k, v = (t[:1, :, :Ts].cpu() for t in (self.q, self.k, self.v))
+        g = self.gamma.cpu()
+        with host_threads() as ht:
+            sec, iqr, reps, out = time_cpu(lambda: oracle.torch_cpu.retention_chunked(q, k, v, g, self.C, 1.0), budget)
         self.step()
-        rel = oracle.verify_equiv(out, self.o[0, :1, :Ts].float().cpu().numpy())["max_rel"]
-        nbytes = 4.0 * Ts * self.Dh * 2
-        return {"value": nbytes / sec / 1e9, "unit": "GB/s", "cores": cpu_threads(), "kind": "port",
-                "sample": f"(b=0,h=0), first {Ts} of {self.T} steps, K-way form C=64 (numpy fp32), {reps} reps",
-                "parity_max_rel": rel}
-
+        rel = oracle.verify_equiv(out.double().numpy(), self.o[:1, :, :Ts].cpu().double().numpy())["max_rel"]
+        nbytes = 4.0 * self.H * Ts * self.Dh * 2
+        return cpu_record(nbytes / sec / 1e9, nbytes * iqr / sec ** 2 / 1e9, "GB/s", ht.n,
+                          f"b=0, all {self.H} heads, first {Ts} of {self.T} steps: the chunked decayed form, C={self.C} "
+                          "(bf16 operands, fp32 arithmetic)", reps, rel)
 
 class C5SSM(Form):
     name, dtype, unit, bound = "c5", "f32", "GB/s", "hbm"
@@ -592,23 +611,21 @@ class C5SSM(Form):
     dominant = step
 
     def cpu(self, budget):
-        import numpy as np
-
         import oracle
 
-        Dn, Ts = 32, 4096  # 32 channels of batch 0, first 4096 steps (causal: a prefix is exact)
-        a = self.a[:1, :Ts, :Dn].cpu().numpy()
-        bx = self.bx[:1, :Ts].cpu().numpy()
-        c = self.c[:1, :Ts].cpu().numpy()
-        x = self.x[:1, :Ts, :Dn].cpu().numpy()
-        sec, reps, (yr, _) = time_cpu(lambda: oracle.ssm_serial(a, bx, c, x), budget)
+        Ts = 512  # every lane (all batches, channels, states), the first 512 steps (a prefix is exact)
+        a = self.a[:, :Ts].cpu()
+        bx, c, x = (t[:, :Ts].cpu() for t in (self.bx, self.c, self.x))
+        h0 = self.h.cpu()
+        with host_threads() as ht:
+            sec, iqr, reps, out = time_cpu(lambda: oracle.torch_cpu.ssm_scan(a, bx, c, x, h0), budget)
+        del a
         self.step()
-        rel = oracle.verify_equiv(yr, self.y[:1, :Ts, :Dn].cpu().numpy())["max_rel"]
-        nbytes = 4.0 * (Ts * Dn * self.N + 2 * Ts * self.N + 2 * Ts * Dn)
-        return {"value": nbytes / sec / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-                "sample": f"b=0, {Dn} of {self.D} channels, first {Ts} of {self.T} steps, serial recurrence (numpy fp32), {reps} reps",
-                "parity_max_rel": rel}
-
+        rel = oracle.verify_equiv(out.double().numpy(), self.y[:, :Ts].cpu().double().numpy())["max_rel"]
+        nbytes = self.work * Ts / self.T
+        return cpu_record(nbytes / sec / 1e9, nbytes * iqr / sec ** 2 / 1e9, "GB/s", ht.n,
+                          f"all {self.B}x{self.D}x{self.N} lanes, first {Ts} of {self.T} steps: the serial recurrence "
+                          "and read-out, each step over every lane (fp32)", reps, rel)
 
 class DenseScan(Form):
     """The dense affine monoid (not one of C1-C5): a batched LTI
@@ -649,18 +666,18 @@ class DenseScan(Form):
     def cpu(self, budget):
         import oracle
 
-        Bs = 256  # 256 of the 16384 sequences (independent: a subset is exact)
-        A = self.A.cpu().numpy()
-        b = self.b[:, :Bs, :, 0].cpu().numpy()
-        h = self.h[:Bs].cpu().numpy()
-        sec, reps, states = time_cpu(lambda: oracle.serial_aff_scan(A, b, h), budget)
+        Bs = 2048  # 2048 of the 16384 sequences (independent: a subset is exact), all steps
+        A = self.A.cpu()
+        b = self.b[:, :Bs, :, 0].cpu()
+        h = self.h[:Bs, :, 0].cpu()
+        with host_threads() as ht:
+            sec, iqr, reps, out = time_cpu(lambda: oracle.torch_cpu.dense_scan(A, b, h), budget)
         self.step()
-        rel = oracle.verify_equiv(states[-1], self.out[:Bs].cpu().numpy())["max_rel"]
+        rel = oracle.verify_equiv(out.double().numpy(), self.out[:Bs, :, 0].cpu().double().numpy())["max_rel"]
         flops = 2.0 * self.T * Bs * self.d * self.d
-        return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": cpu_threads(), "kind": "port",
-                "sample": f"{Bs} of {self.B} sequences, all {self.T} steps, serial recurrence (numpy fp32), {reps} reps",
-                "parity_max_rel": rel}
-
+        return cpu_record(flops / sec / 1e12, flops * iqr / sec ** 2 / 1e12, "TFLOP/s", ht.n,
+                          f"{Bs} of {self.B} sequences, all {self.T} steps: one batched matmul + add per step (fp32)",
+                          reps, rel)
 
 class OmdScanAttention(Form):
     """Deferred-affine attention (not one of C1-C5): softmax attention of
@@ -708,28 +725,17 @@ class OmdScanAttention(Form):
         self.K.attn_carrier_f32(self.q, self.kb, self.V, 1.0)
 
     def cpu(self, budget):
-        import numpy as np
-
         import oracle
 
-        Tq = 256  # 256 of the 4096 queries (rows are independent), all T keys
-        q, k, a, x, h = (t.cpu().double().numpy() for t in self.ins)
-        q = q[:Tq]
-
-        def run():
-            states = oracle.serial_affd_scan(a, x, h)
-            sc = q @ k.T
-            w = np.exp(sc - sc.max(-1, keepdims=True))
-            return (w / w.sum(-1, keepdims=True)) @ states
-
-        sec, reps, ref = time_cpu(run, budget)
+        q, k, a, x, h = (t.cpu() for t in self.ins)
+        with host_threads() as ht:
+            sec, iqr, reps, out = time_cpu(lambda: oracle.torch_cpu.omd_attention(q, k, a, x, h), budget)
         self.step()
-        rel = oracle.verify_equiv(ref, self.out[:Tq].double().cpu().numpy())["max_rel"]
-        flops = 2.0 * Tq * self.T * (self.dk + self.d)
-        return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": cpu_threads(), "kind": "port",
-                "sample": f"{Tq} of {self.Tq} queries over all {self.T} scan states (numpy fp64: serial scan, "
-                          f"dense softmax), {reps} reps", "parity_max_rel": rel}
-
+        rel = oracle.verify_equiv(out.double().numpy(), self.out.double().cpu().numpy())["max_rel"]
+        flops = 2.0 * self.Tq * self.T * (self.dk + self.d)
+        return cpu_record(flops / sec / 1e12, flops * iqr / sec ** 2 / 1e12, "TFLOP/s", ht.n,
+                          f"the full form: {self.Tq} queries over all {self.T} scan states (serial scan, dense "
+                          "softmax, fp32)", reps, rel)
 
 class CopyStream(Form):
     """STREAM-style device copy of 2 GiB fp32: the measured-achievable HBM

@@ -518,3 +518,73 @@ def test_omd_compose_masked_block_and_dense_fibre():
         z = oracle.omd_compose(g, g)
         out = oracle.omd_applym(z, rng.standard_normal(i))
     assert np.isneginf(z[0][1]).all() and z[1][1] == 0 and np.isnan(out[1]).all()
+
+
+# ------------------------------------------- the torch CPU restatement
+# oracle.torch_cpu (the CPU baseline bench.py times) against the numpy
+# functions above, in float64 where the form allows it (fp32 for the
+# chunked retention's promoted arithmetic)
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a))
+
+
+def test_torch_cpu_weight_chain_and_swiglu():
+    rng = np.random.default_rng(3)
+    Ws = [rng.standard_normal((16, 16)) / 4 for _ in range(3)]
+    bs = [rng.standard_normal(16) for _ in range(3)]
+    x = rng.standard_normal((5, 16))
+    W, adds = oracle.fold_linear_chain(Ws, bs)
+    c = sum(adds[1:], adds[0]) if len(adds) > 1 else adds[0]
+    got = oracle.torch_cpu.weight_chain(_t(x), _t(W), _t(np.asarray(c)))
+    _close(oracle.linear_chain(x, Ws, bs), got.numpy(), 1e-12)
+    g = 1 + 0.1 * rng.standard_normal(16)
+    wg, wu, wd = rng.standard_normal((24, 16)), rng.standard_normal((24, 16)), rng.standard_normal((16, 24))
+    got = oracle.torch_cpu.swiglu_block(_t(x), _t(g), _t(wg), _t(wu), _t(wd), 1e-6)
+    _close(oracle.swiglu_fused(oracle.rms_norm(x, g, 1e-6), wg, wu, wd), got.numpy(), 1e-12)
+
+
+def test_torch_cpu_causal_attention():
+    rng = np.random.default_rng(4)
+    q, k, v = (rng.standard_normal((2, 3, 40, 8)) for _ in range(3))
+    got = oracle.torch_cpu.causal_attention(_t(q), _t(k), _t(v), 0.3)
+    _close(oracle.attention_om(q, k, v, 0.3, causal=True), got.numpy(), 1e-12)
+
+
+def test_torch_cpu_retention_chunked_equals_quadratic():
+    rng = np.random.default_rng(5)
+    q, k, v = (rng.standard_normal((2, 3, 256, 16)).astype(np.float32) / 4 for _ in range(3))
+    g = np.array([0.9, 0.97, 0.995], dtype=np.float32)
+    got = oracle.torch_cpu.retention_chunked(_t(q), _t(k), _t(v), _t(g), 64, 0.5)
+    ref = oracle.retention_quadratic(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64),
+                                     g.astype(np.float64), 0.5)
+    _close(ref, got.double().numpy(), 1e-5)
+
+
+def test_torch_cpu_scans():
+    rng = np.random.default_rng(6)
+    B, T, D, N = 2, 50, 6, 4
+    a = rng.random((B, T, D, N)) * 0.9
+    bx, c = rng.standard_normal((B, T, N)), rng.standard_normal((B, T, N))
+    x = rng.standard_normal((B, T, D))
+    ys, _ = oracle.ssm_serial(a, bx, c, x)
+    got = oracle.torch_cpu.ssm_scan(_t(a), _t(bx), _t(c), _t(x), torch.zeros(B, D, N, dtype=torch.float64))
+    _close(ys, got.numpy(), 1e-12)
+    A = rng.standard_normal((5, 5)) * 0.3
+    b = rng.standard_normal((30, 7, 5))
+    h = rng.standard_normal((7, 5))
+    ref = oracle.serial_aff_scan(A, b, h[..., None])[-1][..., 0]
+    _close(ref, oracle.torch_cpu.dense_scan(_t(A), _t(b), _t(h)).numpy(), 1e-12)
+
+
+def test_torch_cpu_omd_attention():
+    rng = np.random.default_rng(7)
+    T, d, Tq, dk = 40, 6, 9, 5
+    q, k = rng.standard_normal((Tq, dk)), rng.standard_normal((T, dk))
+    a, x, h = rng.random((T, d)) * 0.5 + 0.5, rng.standard_normal((T, d)), rng.standard_normal(d)
+    states = oracle.serial_affd_scan(a, x, h)
+    s = q @ k.T
+    w = np.exp(s - s.max(-1, keepdims=True))
+    ref = (w / w.sum(-1, keepdims=True)) @ states
+    _close(ref, oracle.torch_cpu.omd_attention(_t(q), _t(k), _t(a), _t(x), _t(h)).numpy(), 1e-12)
