@@ -75,6 +75,11 @@ SIGNATURES: dict[str, tuple] = {
         [_i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _f32, _p, _p, _p, _i64,
          _i64, _p],
     ),
+    "catopt_hip_attn_carrier_f32_masked": (
+        _i32,
+        [_i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _f32, _i32, _i64, _p,
+         _i64, _p, _p, _p, _i64, _i64, _p],
+    ),
     "catopt_hip_aff_scan_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32, _i64]),
     "catopt_hip_aff_scan": (
         _i32,

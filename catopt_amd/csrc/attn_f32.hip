@@ -23,6 +23,12 @@
 // The max is moved eagerly (every tile that raises it rescales Oᵀ and l), so
 // the emitted m is the true row max; a row with no finite score keeps m = −∞
 // and l = 0, a = 0 (the empty carrier).
+//
+// Mask modes (as the bf16 kernel's): causal (keep key j for query i iff
+// j <= i + causal_off; tiles past a workgroup's last key are skipped), a
+// uint8 keep-plane, or an fp32 additive bias plane added to the scaled score
+// (scale·q·k + bias, as torch forms it); the planes are (Tq, Tk) with row
+// stride mask_ld, shared over the batch.
 #include "common.hpp"
 
 namespace catopt {
@@ -41,12 +47,12 @@ struct CarrierLds {
   static constexpr int BYTES = (kKT * KST + kKT * VST) * 4;
 };
 
-template <int DK, int DVB>
+template <int DK, int DVB, int MASK>
 __global__ __launch_bounds__(kNT) void attn_carrier_f32(
     const float* __restrict__ q, int64_t q_sb, int64_t ldq, const float* __restrict__ k, int64_t k_sb,
     int64_t ldk, const float* __restrict__ v, int64_t v_sb, int64_t ldv, float* __restrict__ m_out,
     float* __restrict__ l_out, float* __restrict__ num, int64_t n_sb, int64_t ldn, int Tq, int Tk, int dk,
-    int dv, float scale) {
+    int dv, float scale, int64_t causal_off, const void* __restrict__ mask, int64_t mask_ld) {
   using L = CarrierLds<DK, DVB>;
   extern __shared__ __attribute__((aligned(16))) float smem[];
   float* Ks = smem;
@@ -122,7 +128,12 @@ __global__ __launch_bounds__(kNT) void attn_carrier_f32(
     }
   };
 
-  const int ntiles = (Tk + kKT - 1) / kKT;
+  int ntiles = (Tk + kKT - 1) / kKT;
+  if (MASK == CATOPT_MASK_CAUSAL) {  // keys past the workgroup's last query + causal_off are masked
+    const int64_t lim = (int64_t)blockIdx.x * kQT + kQT + causal_off;
+    const int64_t nt = lim <= 0 ? 0 : (lim + kKT - 1) / kKT;
+    if (nt < ntiles) ntiles = (int)nt;
+  }
   if (ntiles > 0) {
     if (PF) {
       load_tile(0);
@@ -149,7 +160,17 @@ __global__ __launch_bounds__(kNT) void attn_carrier_f32(
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int key = kv0 + 8 * (r >> 2) + 4 * g + (r & 3);
-      sacc[r] = key < Tk ? sacc[r] * scale : -__builtin_inff();
+      bool keep = key < Tk;
+      float add = 0.f;
+      if (MASK == CATOPT_MASK_CAUSAL) keep = keep && (int64_t)key <= (int64_t)qrow + causal_off;
+      if (MASK == CATOPT_MASK_BOOL || MASK == CATOPT_MASK_BIAS) {
+        // the plane is read at a clamped, always-valid index; rows past Tq
+        // are never stored
+        const int64_t mi = (int64_t)(qok ? qrow : Tq - 1) * mask_ld + (key < Tk ? key : Tk - 1);
+        if (MASK == CATOPT_MASK_BOOL) keep = keep && static_cast<const uint8_t*>(mask)[mi] != 0;
+        if (MASK == CATOPT_MASK_BIAS) add = static_cast<const float*>(mask)[mi];
+      }
+      sacc[r] = keep ? __builtin_fmaf(sacc[r], scale, add) : -__builtin_inff();
       tmax = fmaxf(tmax, sacc[r]);
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
@@ -170,7 +191,10 @@ __global__ __launch_bounds__(kNT) void attn_carrier_f32(
       const float mc = m_new * c;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], c, -mc));  // exp2(-inf) = 0
+        // a bias can put scores near -FLT_MAX, where m·c overflows: the
+        // difference s - m is exact there
+        p[r] = MASK == CATOPT_MASK_BIAS ? __builtin_amdgcn_exp2f((sacc[r] - m_new) * c)
+                                        : __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], c, -mc));  // exp2(-inf) = 0
         l_run += p[r];
       }
     }
@@ -213,15 +237,29 @@ __global__ __launch_bounds__(kNT) void attn_carrier_f32(
   }
 }
 
+struct MaskArgs {
+  int32_t mode;
+  int64_t causal_off;
+  const void* mask;
+  int64_t ld;
+};
+
 template <int DK, int DVB>
 int32_t carrier_launch(int64_t batch, int Tq, int Tk, int dk, int dv, const float* q, int64_t q_sb,
                        int64_t ldq, const float* k, int64_t k_sb, int64_t ldk, const float* v, int64_t v_sb,
                        int64_t ldv, float scale, float* m_out, float* l_out, float* num, int64_t n_sb,
-                       int64_t ldn, hipStream_t s) {
+                       int64_t ldn, const MaskArgs& ma, hipStream_t s) {
   using L = CarrierLds<DK, DVB>;
   const dim3 grid((uint32_t)((Tq + kQT - 1) / kQT), (uint32_t)batch);
-  attn_carrier_f32<DK, DVB><<<grid, dim3(kNT), L::BYTES, s>>>(q, q_sb, ldq, k, k_sb, ldk, v, v_sb, ldv, m_out,
-                                                               l_out, num, n_sb, ldn, Tq, Tk, dk, dv, scale);
+#define CATOPT_CARRIER_MASK(M)                                                                                   attn_carrier_f32<DK, DVB, M><<<grid, dim3(kNT), L::BYTES, s>>>(q, q_sb, ldq, k, k_sb, ldk, v, v_sb, ldv,                                                                     m_out, l_out, num, n_sb, ldn, Tq, Tk, dk, dv,                                                                  scale, ma.causal_off, ma.mask, ma.ld)
+  switch (ma.mode) {
+    case CATOPT_MASK_NONE: CATOPT_CARRIER_MASK(CATOPT_MASK_NONE); break;
+    case CATOPT_MASK_CAUSAL: CATOPT_CARRIER_MASK(CATOPT_MASK_CAUSAL); break;
+    case CATOPT_MASK_BOOL: CATOPT_CARRIER_MASK(CATOPT_MASK_BOOL); break;
+    case CATOPT_MASK_BIAS: CATOPT_CARRIER_MASK(CATOPT_MASK_BIAS); break;
+    default: return CATOPT_E_INVAL;
+  }
+#undef CATOPT_CARRIER_MASK
   CATOPT_LAUNCH_CHECK();
   return CATOPT_OK;
 }
@@ -230,11 +268,11 @@ template <int DK>
 int32_t carrier_dv(int64_t batch, int Tq, int Tk, int dk, int dv, const float* q, int64_t q_sb, int64_t ldq,
                    const float* k, int64_t k_sb, int64_t ldk, const float* v, int64_t v_sb, int64_t ldv,
                    float scale, float* m_out, float* l_out, float* num, int64_t n_sb, int64_t ldn,
-                   hipStream_t s) {
+                   const MaskArgs& ma, hipStream_t s) {
   const int dvb = (dv + 31) / 32;
 #define CATOPT_CARRIER(NB)                                                                                    \
   return carrier_launch<DK, NB>(batch, Tq, Tk, dk, dv, q, q_sb, ldq, k, k_sb, ldk, v, v_sb, ldv, scale, m_out, \
-                                l_out, num, n_sb, ldn, s)
+                                l_out, num, n_sb, ldn, ma, s)
   if (dvb <= 1) CATOPT_CARRIER(1);
   if (dvb <= 2) CATOPT_CARRIER(2);
   if (dvb <= 4) CATOPT_CARRIER(4);
@@ -247,26 +285,41 @@ int32_t carrier_dv(int64_t batch, int Tq, int Tk, int dk, int dv, const float* q
 
 using namespace catopt;
 
-extern "C" int32_t catopt_hip_attn_carrier_f32(int64_t batch, int64_t Tq, int64_t Tk, int64_t dk, int64_t dv,
-                                               const float* q, int64_t q_sb, int64_t ldq, const float* k,
-                                               int64_t k_sb, int64_t ldk, const float* v, int64_t v_sb,
-                                               int64_t ldv, float scale, float* m_out, float* l_out, float* num,
-                                               int64_t num_sb, int64_t ldn, void* stream) {
+extern "C" int32_t catopt_hip_attn_carrier_f32_masked(
+    int64_t batch, int64_t Tq, int64_t Tk, int64_t dk, int64_t dv, const float* q, int64_t q_sb, int64_t ldq,
+    const float* k, int64_t k_sb, int64_t ldk, const float* v, int64_t v_sb, int64_t ldv, float scale,
+    int32_t mask_mode, int64_t causal_off, const void* mask, int64_t mask_ld, float* m_out, float* l_out,
+    float* num, int64_t num_sb, int64_t ldn, void* stream) {
   if (batch < 0 || Tq < 0 || Tk < 0 || dk < 1 || dv < 1) return CATOPT_E_INVAL;
+  if (mask_mode < CATOPT_MASK_NONE || mask_mode > CATOPT_MASK_BIAS) return CATOPT_E_INVAL;
   if (dk > 128 || dv > 256) return CATOPT_E_UNSUPPORTED;
   if (batch == 0 || Tq == 0) return CATOPT_OK;
   if (!q || !m_out || !l_out || !num || (Tk > 0 && (!k || !v))) return CATOPT_E_INVAL;
   if (ldq < dk || ldk < dk || ldv < dv || ldn < dv || q_sb < 0 || k_sb < 0 || v_sb < 0 || num_sb < 0)
     return CATOPT_E_INVAL;
+  if ((mask_mode == CATOPT_MASK_BOOL || mask_mode == CATOPT_MASK_BIAS) && Tk > 0 && (!mask || mask_ld < Tk))
+    return CATOPT_E_INVAL;
+  if (mask_mode == CATOPT_MASK_BIAS && (reinterpret_cast<uintptr_t>(mask) & 3)) return CATOPT_E_INVAL;
   if (batch > 65535 || Tq > 0x7fffffffLL - kQT || Tk > 0x7fffffffLL - kKT) return CATOPT_E_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int iTq = (int)Tq, iTk = (int)Tk, idk = (int)dk, idv = (int)dv;
+  const MaskArgs ma{mask_mode, causal_off, mask, mask_ld};
 #define CATOPT_CARRIER_DK(D)                                                                             \
   return carrier_dv<D>(batch, iTq, iTk, idk, idv, q, q_sb, ldq, k, k_sb, ldk, v, v_sb, ldv, scale, m_out, \
-                       l_out, num, num_sb, ldn, s)
+                       l_out, num, num_sb, ldn, ma, s)
   if (dk <= 16) CATOPT_CARRIER_DK(16);
   if (dk <= 32) CATOPT_CARRIER_DK(32);
   if (dk <= 64) CATOPT_CARRIER_DK(64);
   CATOPT_CARRIER_DK(128);
 #undef CATOPT_CARRIER_DK
+}
+
+extern "C" int32_t catopt_hip_attn_carrier_f32(int64_t batch, int64_t Tq, int64_t Tk, int64_t dk, int64_t dv,
+                                               const float* q, int64_t q_sb, int64_t ldq, const float* k,
+                                               int64_t k_sb, int64_t ldk, const float* v, int64_t v_sb,
+                                               int64_t ldv, float scale, float* m_out, float* l_out, float* num,
+                                               int64_t num_sb, int64_t ldn, void* stream) {
+  return catopt_hip_attn_carrier_f32_masked(batch, Tq, Tk, dk, dv, q, q_sb, ldq, k, k_sb, ldk, v, v_sb, ldv,
+                                            scale, CATOPT_MASK_NONE, 0, nullptr, 0, m_out, l_out, num, num_sb,
+                                            ldn, stream);
 }

@@ -646,12 +646,27 @@ extern "C" int64_t catopt_hip_retention_workspace_bytes(int64_t B, int64_t H, in
   return BH * 2 * P * WFLOATS * (int64_t)sizeof(float);  // two state pieces per range
 }
 
+namespace catopt {
+// fp32 operands (retention_f32.hip): d a multiple of 4 up to 128, any T.
+int32_t retention_f32_launch(int64_t B, int64_t H, int64_t T, int64_t d, const float* q, const float* k,
+                             const float* v, const float* gamma, float scale, float* o, hipStream_t s);
+}  // namespace catopt
+
 extern "C" int32_t catopt_hip_retention_fwd(int32_t dtype, int64_t B, int64_t H, int64_t T,
                                             int64_t d, int64_t chunk, const void* q, const void* k,
                                             const void* v, const float* gamma, float scale, void* o,
                                             void* workspace, int64_t workspace_bytes,
                                             void* stream) {
   if (B < 0 || H < 0 || T < 0 || workspace_bytes < 0) return CATOPT_E_INVAL;
+  if (dtype == CATOPT_F32) {  // no workspace: the state stays in registers
+    if (d < 1 || d > 128 || d % 4 || chunk != CH) return CATOPT_E_UNSUPPORTED;
+    if (B == 0 || H == 0 || T == 0) return CATOPT_OK;
+    if (!q || !k || !v || !gamma || !o) return CATOPT_E_INVAL;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return CATOPT_E_INVAL;
+    return retention_f32_launch(B, H, T, d, static_cast<const float*>(q), static_cast<const float*>(k),
+                                static_cast<const float*>(v), gamma, scale, static_cast<float*>(o),
+                                static_cast<hipStream_t>(stream));
+  }
   if (dtype != CATOPT_BF16 || !dims_ok(d, d) || chunk != CH) return CATOPT_E_UNSUPPORTED;
   if (B == 0 || H == 0 || T == 0) return CATOPT_OK;
   if (!q || !k || !v || !gamma || !o) return CATOPT_E_INVAL;

@@ -28,9 +28,10 @@ as in the reference, and each leaf is classified once, at construction:
   bf16 operands with head dims up to 128 (other widths than 64 / 128
   zero-padded) and a mask that is one ``(Tq, Tk)`` plane shared over the
   leading axes run one launch of the fused attention kernel (scores, mask, exponentials and ``e @ v`` stay on chip; a single
-  leaf is normalised in the kernel).  Unmasked fp32 operands run the fp32
-  carrier kernel.  Any other call — another head dim, a per-batch mask —
-  takes the score path below for that leaf.
+  leaf is normalised in the kernel).  fp32 operands (``dk <= 128``,
+  ``dv <= 256``) run the fp32 carrier kernel with the same mask modes.  Any
+  other call — another head dim, a per-batch mask — takes the score path
+  below for that leaf.
 * ``scores`` — any other score (the reference's ``slice`` / ``stack``
   modes): the score block is evaluated, its row statistics and
   ``exp(s - m)`` come from ``catopt_hip_om_rows`` and ``e @ v`` from the HIP
@@ -620,14 +621,18 @@ class HipOMModule(HipExecutorBase, nn.Module):
 
     def _attn(self, lf: dict, ev, normalize: bool):
         """An ``attn`` leaf on the attention kernels: the normalised output
-        when ``normalize`` (bf16 kernel only), else ``((m, l, a), dtype)``;
+        when ``normalize`` (bf16 kernel only; fp32 leaves return ``None`` and
+        are read out from their carrier), else ``((m, l, a), dtype)``;
         ``None`` outside the kernels' envelopes."""
         q, k, v = ev(lf["q"]), ev(lf["k"]), ev(lf["v"])
         if not _in_envelope(q, k, v):
-            if normalize or lf["mask_kind"] != "none" or not _f32_envelope(q, k, v):
+            if normalize or not _f32_envelope(q, k, v):
+                return None
+            mask_kw = mask_kwargs(lf, ev, q.shape[-2], k.shape[-2])
+            if mask_kw is None:
                 return None
             self.kernel_leaves += 1
-            return K.attn_carrier_f32(q, k, v, float(lf["scale"])), v.dtype
+            return K.attn_carrier_f32(q, k, v, float(lf["scale"]), **mask_kw), v.dtype
         mask_kw = mask_kwargs(lf, ev, q.shape[-2], k.shape[-2])
         if mask_kw is None:
             return None

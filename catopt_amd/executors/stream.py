@@ -17,7 +17,9 @@ Leaves:
   executor: ``masked_fill(…, M, -inf)``, ``add(…, attnbias(m))``, key-axis
   ``concat`` scores) with bf16 operands and head dims up to 128: one launch
   of the HIP attention kernel in carrier mode (scores, mask and
-  exponentials stay on chip; the carrier is fp32);
+  exponentials stay on chip; the carrier is fp32); fp32 operands with
+  ``dk <= 128``, ``dv <= 256``: one launch of the fp32 carrier kernel, with
+  the same mask modes;
 * any other ``om_elem(s, v)``: the score and value operands are evaluated and
   folded with ``om_elem`` (``torch_bridge.py:1974-1981``; on device fp32 /
   bf16 operands the ``catopt_hip_om_rows`` row kernel and the HIP GEMM);
@@ -48,7 +50,7 @@ from .. import kernels as K
 from ..bindings import _matmul, _om_compose, om_elem_dense
 from ..evaluator import HipIRModule
 from ..ir import IR, is_op
-from .om import _as_bhtd, _classify_mask, _in_envelope, mask_kwargs, parse_score
+from .om import _as_bhtd, _classify_mask, _f32_envelope, _in_envelope, mask_kwargs, parse_score
 
 __all__ = [
     "HipStreamingOMModule",
@@ -81,10 +83,12 @@ def om_step(state: tuple | None, s: torch.Tensor, v: torch.Tensor):
 
 
 def _carrier_qk(q, k, v, scale: float = 1.0, **mask_kw) -> tuple | None:
-    """``om_elem(scale · q kᵀ, v)`` by the attention kernel in carrier mode, or
-    ``None`` outside its envelope."""
+    """``om_elem(scale · q kᵀ, v)`` by the attention kernel in carrier mode
+    (bf16) or the fp32 carrier kernel, or ``None`` outside their envelopes."""
     if not _in_envelope(q, k, v):
-        return None
+        if not _f32_envelope(q, k, v):
+            return None
+        return K.attn_carrier_f32(q, k, v, float(scale), **mask_kw)
     q4, k4, v4, lead = _as_bhtd(q, k, v)
     if q4 is None or not K.attention_grid_ok(q4):
         return None
@@ -95,8 +99,9 @@ def _carrier_qk(q, k, v, scale: float = 1.0, **mask_kw) -> tuple | None:
 
 def om_step_qk(state: tuple | None, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
     """:func:`om_step` for the canonical score ``s = q @ kᵀ`` (no scale),
-    ``om_lower.py:910-917``.  bf16 operands with head dims up to 128 never
-    materialise ``s``: the attention kernel emits the block's carrier."""
+    ``om_lower.py:910-917``.  bf16 operands with head dims up to 128 (fp32:
+    ``dk <= 128``, ``dv <= 256``) never materialise ``s``: an attention
+    kernel emits the block's carrier."""
     e = _carrier_qk(q, k, v, 1.0)
     if e is None:
         return om_step(state, _matmul(q, k.transpose(-2, -1)), v)

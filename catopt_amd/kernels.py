@@ -385,16 +385,17 @@ RETENTION_HEAD_DIM = 128
 def retention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma: torch.Tensor,
               scale: float = 1.0) -> torch.Tensor:
     """``scale * Σ_{s<=t} γ_h^(t-s) (q_t·k_s) v_s`` for ``q, k (B,H,T,dk)``,
-    ``v (B,H,T,dv)`` bf16, ``dk, dv <= 128``.  The kernel reads a head dim
-    ``d`` (a multiple of 8) and any ``T`` in place: columns past ``d`` and
-    rows past ``T`` of its 64-step chunks load as zeros and are never stored.
-    When ``dk`` and ``dv`` differ, or are not multiples of 8, the narrower
-    operands run zero-padded to the common width (zero columns leave q·k
-    unchanged and add zero output columns, dropped)."""
+    ``v (B,H,T,dv)``, all bf16 or all fp32, ``dk, dv <= 128``.  The kernels
+    read a head dim ``d`` (a multiple of 8 for bf16, of 4 for fp32) and any
+    ``T`` in place: columns past ``d`` and rows past ``T`` of the 64-step
+    chunks load as zeros and are never stored.  When ``dk`` and ``dv``
+    differ, or are not such multiples, the narrower operands run zero-padded
+    to the common width (zero columns leave q·k unchanged and add zero output
+    columns, dropped).  fp32 operands compute in fp32 throughout."""
     _need_device(q, k, v, gamma)
     lib = L.load()
-    if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
-        raise NotImplementedError("HIP retention runs on bf16 operands")
+    if q.dtype not in (torch.bfloat16, torch.float32) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise NotImplementedError("HIP retention runs on bf16 or fp32 operands")
     if q.dim() != 4 or q.shape != k.shape or v.dim() != 4 or v.shape[:3] != q.shape[:3]:
         raise ValueError("retention operands must be q, k (B, H, T, dk) and v (B, H, T, dv)")
     B, H, T, dk = q.shape
@@ -403,7 +404,8 @@ def retention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma: torch.Te
         raise NotImplementedError(f"HIP retention needs dk, dv <= {RETENTION_HEAD_DIM}")
     if T == 0 or B * H == 0:
         return torch.zeros_like(v)
-    d = -(-max(dk, dv, 8) // 8) * 8
+    step = 4 if q.dtype == torch.float32 else 8
+    d = -(-max(dk, dv, step) // step) * step
     if dk != d or dv != d:
         pad = torch.nn.functional.pad
         q, k = (pad(t, (0, d - dk)) for t in (q, k))
@@ -414,11 +416,14 @@ def retention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma: torch.Te
         raise ValueError("gamma must hold one rate per head")
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     o = torch.empty_like(v)
-    wsb = lib.catopt_hip_retention_workspace_bytes(B, H, T, d, RETENTION_CHUNK)
-    if wsb < 0:
-        raise ValueError("retention workspace query rejected the shape")
+    dt = L.F32 if q.dtype == torch.float32 else L.BF16
+    wsb = 0  # the fp32 kernel keeps its state in registers and takes no workspace
+    if dt == L.BF16:
+        wsb = lib.catopt_hip_retention_workspace_bytes(B, H, T, d, RETENTION_CHUNK)
+        if wsb < 0:
+            raise ValueError("retention workspace query rejected the shape")
     ws = _workspace(wsb, q.device)
-    st = lib.catopt_hip_retention_fwd(L.BF16, B, H, T, d, RETENTION_CHUNK, _ptr(q), _ptr(k),
+    st = lib.catopt_hip_retention_fwd(dt, B, H, T, d, RETENTION_CHUNK, _ptr(q), _ptr(k),
                                       _ptr(v), _ptr(g), float(scale), _ptr(o), _ptr(ws), wsb,
                                       _stream(q))
     L.check("catopt_hip_retention_fwd", st)
@@ -553,12 +558,37 @@ def affd_scan(a: torch.Tensor, u: torch.Tensor, h0: torch.Tensor | None,
     return (out.reshape(T, *sshape) if out is not None else None), hf.reshape(sshape)
 
 
-def attn_carrier_f32(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float = 1.0) -> tuple:
+def _rows3(t: torch.Tensor, nb: int, rows: int, cols: int) -> tuple:
+    """``t`` as fp32 ``(nb, rows, cols)`` with unit column stride — a view
+    when the leading axes collapse to one stride, else a contiguous copy —
+    and its batch and row strides (elements, both non-negative, the row
+    stride at least ``cols``)."""
+    t3 = t.to(torch.float32).reshape(nb, rows, cols)
+    sb, ld = t3.stride(0), t3.stride(1)
+    if rows <= 1:
+        ld = cols  # the row stride is never applied
+    if nb <= 1:
+        sb = 0
+    if t3.stride(2) != 1 or sb < 0 or ld < cols:
+        t3 = t3.contiguous()
+        sb, ld = (rows * cols if nb > 1 else 0), cols
+    return t3, sb, ld
+
+
+def attn_carrier_f32(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float = 1.0, *,
+                     causal: bool = False, causal_off: int = 0, mask: torch.Tensor | None = None,
+                     bias: torch.Tensor | None = None) -> tuple:
     """The om element of ``s = scale · q kᵀ`` over values ``v`` in fp32:
     ``(m (…,Tq,1), l (…,Tq,1), a (…,Tq,dv))``, ``dk ≤ 128``, ``dv ≤ 256``.
     ``k (…,Tk,dk)``; ``q (…,Tq,dk)`` or ``(Tq,dk)`` and ``v (…,Tk,dv)`` or
-    ``(Tk,dv)``, a 2-D operand shared over the leading axes."""
-    _need_device(q, k, v)
+    ``(Tk,dv)``, a 2-D operand shared over the leading axes.
+
+    The mask keywords are :func:`attention`'s: ``causal`` keeps key ``j``
+    for query ``i`` iff ``j <= i + causal_off``; ``mask`` is a bool keep
+    plane and ``bias`` an additive float plane (added to the scaled score),
+    each ``(Tq, Tk)`` and shared over the leading axes.  Rows with every key
+    masked get the empty carrier ``(-inf, 0, 0)``."""
+    _need_device(q, k, v, mask, bias)
     lib = L.load()
     lead = tuple(k.shape[:-2])
     Tq, dk = q.shape[-2], q.shape[-1]
@@ -567,23 +597,38 @@ def attn_carrier_f32(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: f
             (v.dim() > 2 and tuple(v.shape[:-2]) != lead):
         raise ValueError(f"attn_carrier_f32: q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)} do not fit")
     nb = math.prod(lead) if lead else 1
+    # operands are read in place through (batch, row) strides: a key block cut
+    # from a longer sequence is not copied
+    q3, q_sb, ldq = _rows3(q, 1 if q.dim() == 2 else nb, Tq, dk)
+    k3, k_sb, ldk = _rows3(k, nb, Tk, dk)
+    v3, v_sb, ldv = _rows3(v, 1 if v.dim() == 2 else nb, Tk, dv)
     if q.dim() == 2:  # one query block shared by every key block
-        q3, q_sb = q.to(torch.float32).contiguous(), 0
-    else:
-        q3, q_sb = q.to(torch.float32).reshape(nb, Tq, dk).contiguous(), Tq * dk
-    k3 = k.to(torch.float32).reshape(nb, Tk, dk).contiguous()
+        q_sb = 0
     if v.dim() == 2:
-        v3, v_sb = v.to(torch.float32).contiguous(), 0
-    else:
-        v3 = v.to(torch.float32).reshape(nb, Tk, dv).contiguous()
-        v_sb = Tk * dv
+        v_sb = 0
+    if (mask is not None) + (bias is not None) + bool(causal) > 1:
+        raise ValueError("pass at most one of causal=True, mask, bias")
+    mode, plane, mask_ld = L.MASK_NONE, None, 0
+    if mask is not None or bias is not None:
+        t = mask if mask is not None else bias
+        if t.shape[-2:] != (Tq, Tk) or t.numel() != Tq * Tk:
+            raise NotImplementedError(f"the mask plane must be ({Tq}, {Tk}) shared over the leading axes, "
+                                      f"got {tuple(t.shape)}")
+        if mask is not None:
+            plane, mode = mask.reshape(Tq, Tk).to(torch.uint8).contiguous(), L.MASK_BOOL
+        else:
+            plane, mode = bias.reshape(Tq, Tk).to(torch.float32).contiguous(), L.MASK_BIAS
+        mask_ld = Tk
+    elif causal:
+        mode = L.MASK_CAUSAL
     m = torch.empty((nb, Tq), dtype=torch.float32, device=q.device)
     lv = torch.empty((nb, Tq), dtype=torch.float32, device=q.device)
     a = torch.empty((nb, Tq, dv), dtype=torch.float32, device=q.device)
-    st = lib.catopt_hip_attn_carrier_f32(nb, Tq, Tk, dk, dv, _ptr(q3), q_sb, dk, _ptr(k3), Tk * dk, dk,
-                                         _ptr(v3), v_sb, dv, float(scale), _ptr(m), _ptr(lv), _ptr(a), Tq * dv, dv,
-                                         _stream(q))
-    L.check("catopt_hip_attn_carrier_f32", st)
+    st = lib.catopt_hip_attn_carrier_f32_masked(nb, Tq, Tk, dk, dv, _ptr(q3), q_sb, ldq, _ptr(k3), k_sb, ldk,
+                                                _ptr(v3), v_sb, ldv, float(scale), mode, int(causal_off),
+                                                _ptr(plane), mask_ld, _ptr(m), _ptr(lv), _ptr(a), Tq * dv, dv,
+                                                _stream(q))
+    L.check("catopt_hip_attn_carrier_f32_masked", st)
     return m.reshape(*lead, Tq, 1), lv.reshape(*lead, Tq, 1), a.reshape(*lead, Tq, dv)
 
 

@@ -362,6 +362,29 @@ int32_t catopt_hip_attn_carrier_f32(int64_t batch, int64_t Tq, int64_t Tk,
                                     int64_t num_sb, int64_t ldn, void* stream);
 
 /*
+ * catopt_hip_attn_carrier_f32 with a mask on the score block, in the modes
+ * of catopt_hip_attn_fwd: CATOPT_MASK_CAUSAL keeps key j for query i iff
+ * j <= i + causal_off (key tiles wholly past a query block are not read);
+ * CATOPT_MASK_BOOL keeps where the uint8 plane mask[i, j] != 0;
+ * CATOPT_MASK_BIAS adds the fp32 plane mask[i, j] (4-byte aligned) to the
+ * scaled score, s = scale·q kᵀ + bias, as torch forms it (−inf masks; a row
+ * biased by −FLT_MAX throughout keeps finite scores and weighs its keys as
+ * torch does).  The plane is [Tq, Tk] with row stride mask_ld >= Tk, shared
+ * over the batch.  A row whose keys are all masked gets the empty carrier.
+ * Replaces, for fp32 operands, a masked score leaf of BatchedOMModule: the
+ * score block with its cmask / masked_fill or attnbias term (om.py:1023-1050,
+ * evaluated by _stacked_scores, om_lower.py:672-719) and _batched_elem
+ * (om_lower.py:462-472) over it.
+ */
+int32_t catopt_hip_attn_carrier_f32_masked(
+    int64_t batch, int64_t Tq, int64_t Tk, int64_t dk, int64_t dv,
+    const float* q, int64_t q_sb, int64_t ldq, const float* k, int64_t k_sb,
+    int64_t ldk, const float* v, int64_t v_sb, int64_t ldv, float scale,
+    int32_t mask_mode, int64_t causal_off, const void* mask, int64_t mask_ld,
+    float* m_out, float* l_out, float* num, int64_t num_sb, int64_t ldn,
+    void* stream);
+
+/*
  * The om combine of L carriers of one query block followed by the diagonal
  * deferred-affine readout, in one pass (fp32):
  *   M = max_i m_i (NaN-propagating, as amax), w_i = isfinite(m_i) ?

@@ -133,3 +133,18 @@ def test_host_argument_checks(lib):
                                            None, None, None, 0, 300, None) == L.E_UNSUPPORTED
     assert lib.catopt_hip_attn_carrier_f32(1, 4, 4, 16, 8, None, 0, 8, None, 0, 16, None, 0, 8, 1.0,
                                            None, None, None, 0, 8, None) == L.E_INVAL
+    # masked fp32 carrier: unknown mode, a plane mode without a plane, a row
+    # stride below Tk, a misaligned bias (all rejected before any launch;
+    # the operand addresses are never read)
+    fake = 4096
+
+    def masked(mode, mask, ld, dk=16):
+        return lib.catopt_hip_attn_carrier_f32_masked(1, 4, 4, dk, 8, fake, 0, dk, fake, 0, dk, fake, 0, 8, 1.0,
+                                                      mode, 0, mask, ld, fake, fake, fake, 0, 8, None)
+
+    assert masked(7, None, 0) == L.E_INVAL
+    assert masked(-1, None, 0) == L.E_INVAL
+    assert masked(L.MASK_BOOL, None, 4) == L.E_INVAL
+    assert masked(L.MASK_BIAS, fake, 3) == L.E_INVAL
+    assert masked(L.MASK_BIAS, fake + 2, 4) == L.E_INVAL
+    assert masked(L.MASK_CAUSAL, None, 0, dk=129) == L.E_UNSUPPORTED
