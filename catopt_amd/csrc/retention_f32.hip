@@ -47,22 +47,31 @@ __device__ __forceinline__ f32x16 mfma_f32(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float4 ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+__device__ __forceinline__ float4 ld4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
 }
 
-__device__ __forceinline__ float ld1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+__device__ __forceinline__ float ld1(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
 }
 
-// Row-tile operand of q or k: reg[4u + e] = X[t0 + 32·tile + l32][dd0 + 8u + 4g + e].
-__device__ __forceinline__ void load_rows(__amdgpu_buffer_rsrc_t r, int t0, int tile, int l32, int g, int dd0,
-                                          int d, float (&reg)[16]) {
-  const int row = t0 + 32 * tile + l32;
+// Byte offset of column `col` in a row, or kOOB past the row's width d.  It
+// is added to row offsets below 2^31, so a past-the-width column stays out of
+// range; computed once per lane (and kept opaque) so that no load carries a
+// select the compiler could split into branches around the load.
+__device__ __forceinline__ uint32_t col_bytes(int col, int d) {
+  uint32_t c = col < d ? (uint32_t)col * 4u : kOOB;
+  asm volatile("" : "+v"(c));
+  return c;
+}
+
+// Row-tile operand of q or k: reg[4u + e] = X[row0 + l32][dd0 + 8u + 4g + e]
+// with vrow[u] = l32·d·4 + col_bytes(dd0 + 8u + 4g) and soff = row0·d·4.
+__device__ __forceinline__ void load_rows(__amdgpu_buffer_rsrc_t r, const uint32_t (&vrow)[4], uint32_t soff,
+                                          float (&reg)[16]) {
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    const int col = dd0 + 8 * u + 4 * g;
-    const float4 x = ld4(r, col < d ? (uint32_t)(row * d + col) * 4u : kOOB);
+    const float4 x = ld4(r, vrow[u], soff);
     reg[4 * u + 0] = x.x;
     reg[4 * u + 1] = x.y;
     reg[4 * u + 2] = x.z;
@@ -70,14 +79,13 @@ __device__ __forceinline__ void load_rows(__amdgpu_buffer_rsrc_t r, int t0, int 
   }
 }
 
-// Column operand: reg[t] = X[t0 + 32·tile + acc_row(t, g)][col] (zeros when col >= d).
-__device__ __forceinline__ void load_cols(__amdgpu_buffer_rsrc_t r, int t0, int tile, int g, int col, int d,
+// Column operand: reg[t] = X[row0 + acc_row(t, g)][col] with
+// vcol = 4g·d·4 + col_bytes(col) and soff = row0·d·4; the rest of the row
+// index, 8(t/4) + t%4, goes into the scalar offset.
+__device__ __forceinline__ void load_cols(__amdgpu_buffer_rsrc_t r, uint32_t vcol, uint32_t soff, int d,
                                           float (&reg)[16]) {
 #pragma unroll
-  for (int t = 0; t < 16; ++t) {
-    const int row = t0 + 32 * tile + acc_row(t, g);
-    reg[t] = ld1(r, col < d ? (uint32_t)(row * d + col) * 4u : kOOB);
-  }
+  for (int t = 0; t < 16; ++t) reg[t] = ld1(r, vcol, soff + (uint32_t)((8 * (t >> 2) + (t & 3)) * d * 4));
 }
 
 __global__ __launch_bounds__(kNT) void retention_f32(const float* __restrict__ q, const float* __restrict__ k,
@@ -121,24 +129,33 @@ __global__ __launch_bounds__(kNT) void retention_f32(const float* __restrict__ q
   }
   const float gC = __builtin_amdgcn_exp2f((float)kC * lg);
 
+  // per-lane parts of the load offsets (bytes); row bases go to soffset
+  uint32_t vrow[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) vrow[u] = (uint32_t)(l32 * d * 4) + col_bytes(dd0 + 8 * u + 4 * g, d);
+  const uint32_t vcol_v = (uint32_t)(4 * g * d * 4) + col_bytes(c0 + l32, d);
+  const uint32_t vcol_k = (uint32_t)(4 * g * d * 4) + col_bytes(dd0 + l32, d);
+  const uint32_t tile_b = 32u * (uint32_t)d * 4u;  // bytes of 32 rows
+
   f32x16 sacc = {};  // S[dd0 + acc_row(r, g)][c0 + l32]
   const int nch = (T + kC - 1) / kC;
   float qr[2][16], kr[2][16];
   if (active) {
-    load_rows(rq, 0, 0, l32, g, dd0, d, qr[0]);
-    load_rows(rq, 0, 1, l32, g, dd0, d, qr[1]);
-    load_rows(rk, 0, 0, l32, g, dd0, d, kr[0]);
-    load_rows(rk, 0, 1, l32, g, dd0, d, kr[1]);
+    load_rows(rq, vrow, 0, qr[0]);
+    load_rows(rq, vrow, tile_b, qr[1]);
+    load_rows(rk, vrow, 0, kr[0]);
+    load_rows(rk, vrow, tile_b, kr[1]);
   }
   for (int n = 0; n < nch; ++n) {
     const int t0 = n * kC;
+    const uint32_t sb = (uint32_t)t0 * (uint32_t)d * 4u;  // the chunk's first row
     float* buf = red + (n & 1) * (4 * kC * kSlice);
     if (active) {
       float vr[2][16], kc[2][16];
-      load_cols(rv, t0, 0, g, c0 + l32, d, vr[0]);
-      load_cols(rv, t0, 1, g, c0 + l32, d, vr[1]);
-      load_cols(rk, t0, 0, g, dd0 + l32, d, kc[0]);
-      load_cols(rk, t0, 1, g, dd0 + l32, d, kc[1]);
+      load_cols(rv, vcol_v, sb, d, vr[0]);
+      load_cols(rv, vcol_v, sb + tile_b, d, vr[1]);
+      load_cols(rk, vcol_k, sb, d, kc[0]);
+      load_cols(rk, vcol_k, sb + tile_b, d, kc[1]);
 
       // inter-chunk term, then the per-row decay γ^a
       f32x16 oacc[2] = {{}, {}};
@@ -162,10 +179,11 @@ __global__ __launch_bounds__(kNT) void retention_f32(const float* __restrict__ q
       }
       // the next chunk's q and k rows (their registers are free from here)
       if (n + 1 < nch) {
-        load_rows(rq, t0 + kC, 0, l32, g, dd0, d, qr[0]);
-        load_rows(rq, t0 + kC, 1, l32, g, dd0, d, qr[1]);
-        load_rows(rk, t0 + kC, 0, l32, g, dd0, d, kr[0]);
-        load_rows(rk, t0 + kC, 1, l32, g, dd0, d, kr[1]);
+        const uint32_t nb = sb + 2u * tile_b;
+        load_rows(rq, vrow, nb, qr[0]);
+        load_rows(rq, vrow, nb + tile_b, qr[1]);
+        load_rows(rk, vrow, nb, kr[0]);
+        load_rows(rk, vrow, nb + tile_b, kr[1]);
       }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -204,7 +222,11 @@ __global__ __launch_bounds__(kNT) void retention_f32(const float* __restrict__ q
       for (int it = 0; it < 2; ++it) {
         const int i = 32 * it + 8 * w + 4 * g + e;
         float s = 0.f;
-        for (int x = 0; x < nact; ++x) s += buf[x * (kC * kSlice) + i * kSlice + l32];
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {  // partials of waves past nact were not written: selected out
+          const float px = buf[x * (kC * kSlice) + i * kSlice + l32];
+          s += x < nact ? px : 0.f;
+        }
         const int row = t0 + i;
         if (row < T && col < d) oh[(int64_t)row * d + col] = scale * s;
       }

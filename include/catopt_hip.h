@@ -204,11 +204,17 @@ int32_t catopt_hip_om_compose(int64_t rows, int64_t dv, const float* m1,
  * evaluated chunk-wise: intra-chunk (q_i k_iᵀ ⊙ decay(γ, C)) v_i on MFMA,
  * inter-chunk through the state S_{i+1} = γ^C S_i + Σ_c γ^{C-c} k_ic ⊗ v_ic
  * carried across chunks (the rank-1 decay_vec factors of the cross blocks,
- * om.py:1075-1089).  q, k, v, o: [B, H, T, d] contiguous, bf16; gamma: [H]
- * fp32; chunk ∈ {64}; d = 128; T a multiple of chunk.
- * Workspace: catopt_hip_retention_workspace_bytes(...) bytes, any contents
- * (0 here: one pass whose carried state stays in registers; the query keeps
- * callers independent of that).  -1 for an unsupported d / chunk.
+ * om.py:1075-1089).  q, k, v, o: [B, H, T, d] contiguous, 16-byte aligned,
+ * all of dtype: CATOPT_BF16 (MFMA in bf16, state and accumulation in fp32;
+ * d a multiple of 8 up to 128) or CATOPT_F32 (operands, products and state
+ * in fp32; d a multiple of 4 up to 128); gamma: [H] fp32; chunk ∈ {64}; any
+ * T (rows past T of the last chunk read as zeros and are not stored).
+ * Workspace (bf16 only; the fp32 kernel takes none and ignores it):
+ * catopt_hip_retention_workspace_bytes(...) bytes, any contents — the
+ * per-segment start-state pieces when T is split into segments over the
+ * current device's CUs, 0 when one segment per head fills the device
+ * (without a device, the bound for the most segments any device takes).
+ * -1 for an unsupported d / chunk.
  */
 int64_t catopt_hip_retention_workspace_bytes(int64_t B, int64_t H, int64_t T,
                                              int64_t d, int64_t chunk);

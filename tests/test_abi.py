@@ -112,6 +112,14 @@ def test_host_argument_checks(lib):
                                         None, None, 0, None) == L.E_UNSUPPORTED
     assert lib.catopt_hip_retention_fwd(L.BF16, 1, 1, 100, 128, 64, None, None, None, None, 1.0,
                                         None, None, 0, None) == L.E_INVAL
+    # fp32: head dims are multiples of 4 (100 is one), up to 128; chunk 64 only
+    assert lib.catopt_hip_retention_fwd(L.F32, 1, 1, 100, 100, 64, None, None, None, None, 1.0,
+                                        None, None, 0, None) == L.E_INVAL
+    for d, chunk in ((102, 64), (132, 64), (128, 128)):
+        assert lib.catopt_hip_retention_fwd(L.F32, 1, 1, 100, d, chunk, None, None, None, None, 1.0,
+                                            None, None, 0, None) == L.E_UNSUPPORTED
+    assert lib.catopt_hip_retention_fwd(L.F32, 1, 1, 0, 128, 64, None, None, None, None, 1.0,
+                                        None, None, 0, None) == L.OK
     zeros = (C.c_int64 * 3)(0, 0, 0)
     assert lib.catopt_hip_attn_fwd(L.BF16, 1, 1, 8, 8, 96, 96, None, zeros, None, zeros, None, zeros,
                                    1.0, L.MASK_CAUSAL, 0, None, 0, 1, None, zeros, None, None,
