@@ -88,11 +88,13 @@ def test_the_extracted_form_verifies_against_the_term_as_written(sink, dev):
     b = DecayedTerms(B=2, K=4, C=64, D=64)
     vals, x = b.values(dtype=torch.float32, seed=5)
     vd, xd = _dev(vals, x, dev)
-    # fp32 operands: the kernel is bf16-only, so the planned module runs the
-    # generic path for them (counted) and still equals the written term
-    mod = deliver(b.ir(b.root()), vd, sink).module
+    # fp32 operands run the fp32 retention kernel (no fallback) and equal
+    # the written term evaluated op by op on the device
+    res32 = deliver(b.ir(b.root()), vd, sink, (xd,), verify_ir=b.ir(b.root()), rtol=TOL_F32)
+    assert res32.verified.passed, res32.verified
+    mod = res32.module
     out = mod(xd)
-    assert mod.is_batched and mod.fallbacks == 1
+    assert mod.is_batched and mod.fallbacks == 0
     _gate(_retention_ref(b, vals, x), out, TOL_F32)
     # bf16 operands: the kernel runs and agrees with the bf16 generic module
     vals16, x16 = b.values(dtype=torch.bfloat16, seed=5)
