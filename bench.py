@@ -691,7 +691,7 @@ class OmdScanAttention(Form):
                 "16 key blocks, diagonal scan a_t,x_t (T,64), fp32")
     peak = PEAK["fp32_tflops"]
     work = 2.0 * Tq * T * (dk + 2 * d)  # scores + the two numerator parts
-    dom_name = dom_key = "attn_carrier_f32<64, 4>"
+    dom_name = dom_key = "attn_carrier_f32<64, 4, 0>"
     dom_work = work  # one launch computes every leaf's carrier
 
     def setup(self, dev):

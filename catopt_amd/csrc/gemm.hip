@@ -116,9 +116,10 @@ __global__ __launch_bounds__(NTH) void gemm_generic(
 // chain: one 64 x 512 x 512 GEMM that the 64x64 tiles above spread over only
 // 8 workgroups).  One workgroup per 16x16 output tile; its 4 waves split K
 // into quarters and reduce the four 16x16 partials through LDS in a fixed
-// order (deterministic).  The partials are stored transposed, one 16-byte
-// write per lane, and read back with consecutive lanes on consecutive
-// words, so neither side has bank conflicts.  16x16x4 fp32 MFMA: lane l
+// order (deterministic).  Each lane stores its 4 accumulators with one
+// 16-byte write at 16 l (consecutive lanes on consecutive chunks) and the
+// reduction reads them back with consecutive lanes on consecutive words, so
+// neither side has bank conflicts.  16x16x4 fp32 MFMA: lane l
 // supplies A row l%16 and W row l%16 at k-group l/16; accumulator register
 // r of lane l is output (4*(l/16) + r, l%16).  The k index of the MFMA is
 // only a summation order, so each lane loads 4 consecutive k with one
@@ -139,7 +140,7 @@ __global__ __launch_bounds__(256) void gemm_f32_skinny(
     const float* __restrict__ A, int64_t lda, const float* __restrict__ W, int64_t ldw,
     const float* __restrict__ bias, const float* __restrict__ bias2, float* __restrict__ C,
     int64_t ldc, int M, int N, int K) {
-  __shared__ __attribute__((aligned(16))) float part[4][16][16];  // [wave][column][row]
+  __shared__ __attribute__((aligned(16))) float part[4][64][4];  // [wave][lane][accumulator]
   const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 16;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, kq = lane >> 4;
@@ -163,13 +164,16 @@ __global__ __launch_bounds__(256) void gemm_f32_skinny(
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc = mfma16x16x4f32(av[s][e], bv[s][e], acc);
   }
-  // lane (kq, r16) holds rows 4 kq .. 4 kq + 3 of column r16: one 16-byte write
-  *reinterpret_cast<f32x4*>(&part[wave][r16][4 * kq]) = acc;
+  // lane l = 16 kq + r16 holds rows 4 kq .. 4 kq + 3 of column r16
+  *reinterpret_cast<f32x4*>(&part[wave][lane][0]) = acc;
   __syncthreads();
-  const int i = tid & 15, j = tid >> 4;  // 256 threads: one output each, rows fastest
+  // lane t of wave w sums output (4 w + t % 4, t / 4), which every wave's
+  // lane 16 w + t / 4 holds in accumulator t % 4: word 64 w + t of each block
+  const int i = 4 * wave + (lane & 3), j = lane >> 2;
+  const int src = 16 * wave + j;
   const int m = m0 + i, n = n0 + j;
   if (m >= M || n >= N) return;
-  float o = ((part[0][j][i] + part[1][j][i]) + part[2][j][i]) + part[3][j][i];
+  float o = ((part[0][src][i & 3] + part[1][src][i & 3]) + part[2][src][i & 3]) + part[3][src][i & 3];
   if (EPI == CATOPT_EPI_BIAS || EPI == CATOPT_EPI_BIAS_ADD2) o += bias[n];
   if (EPI == CATOPT_EPI_BIAS_ADD2) o += bias2[n];
   C[(int64_t)m * ldc + n] = o;
