@@ -35,7 +35,13 @@
 // MI355X that and reading all of a tile's K fragments before its first MFMA
 // each measured 1-2%; copies of the kernel with one part taken out put the
 // rest of the time in no single place (tile loads 12%, K or V fragment reads
-// 5-6% each, exponentials 4%, half the MFMAs 23%).
+// 5-6% each, exponentials 4%, half the MFMAs 23%).  Two alternatives measured
+// slower: 8-wave workgroups whose two wave groups alternate MFMA and softmax
+// phases between barriers, as the GEMM's ping-pong does (5%: with one
+// MFMA-issuing wave per SIMD the fragment reads, 1 KB per MFMA and half of it
+// through the half-rate transposing read, no longer keep the MFMAs fed;
+// with the softmax taken out that variant still ran 574 us at C3), and
+// raising the wave priority around the MFMA blocks (1.5%).
 //
 // Softmax runs in the exp2 domain: p = exp2((s - m) * c), c = scale·log2(e).
 // The running max is only moved (and Oᵀ, l rescaled) when a tile raises it
@@ -355,9 +361,7 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
       bf16x8 p0[2], p1[2];
       read_k(0);
       read_k(1);
-      __builtin_amdgcn_s_setprio(1);
       qk(0, s0);
-      __builtin_amdgcn_s_setprio(0);
       if (need_mask) apply_mask(0, s0);
       const float a0 = half_max(s0);
       if (a0 != 1.f) rescale(a0);
@@ -394,11 +398,9 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
       pin(l_run[0]);
       __builtin_amdgcn_sched_barrier(0);
       if (a1 != 1.f) rescale(a1);
-      __builtin_amdgcn_s_setprio(1);
       pv(1, p1);
     }
 
-    __builtin_amdgcn_s_setprio(0);
     if (kvt + 1 < nkv) {
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
