@@ -38,7 +38,8 @@ reference's O(K²) pair products (``decayed_lower.py:671-700``).  γ is held in
 fp32 and every decay factor is formed in fp32 inside the kernel.  bf16
 operands run the bf16 kernel (MFMA in bf16, state and accumulation in fp32);
 fp32 operands run the fp32 kernel, whose operands, products and state all
-stay fp32.  Other dtypes take the generic module (counted in ``fallbacks``).
+stay fp32; fp16 operands run it widened to fp32, the output rounded to fp16.
+Other dtypes take the generic module (counted in ``fallbacks``).
 """
 
 from __future__ import annotations
@@ -343,7 +344,7 @@ def _kernel_args(q, k, v, g, p):
     ts = (q, k, v)
     if not all(isinstance(t, torch.Tensor) and t.device.type == "cuda" for t in ts):
         return None
-    if q.dtype not in (torch.bfloat16, torch.float32) or k.dtype != q.dtype or v.dtype != q.dtype:
+    if q.dtype not in (torch.bfloat16, torch.float32, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
         return None
     if q.shape != k.shape or v.shape[:-1] != q.shape[:-1] or not 2 <= q.dim() <= 4:
         return None

@@ -29,7 +29,8 @@ as in the reference, and each leaf is classified once, at construction:
   zero-padded) and a mask that is one ``(Tq, Tk)`` plane shared over the
   leading axes run one launch of the fused attention kernel (scores, mask, exponentials and ``e @ v`` stay on chip; a single
   leaf is normalised in the kernel).  fp32 operands (``dk <= 128``,
-  ``dv <= 256``) run the fp32 carrier kernel with the same mask modes.  Any
+  ``dv <= 256``) run the fp32 carrier kernel with the same mask modes; fp16
+  operands run it widened to fp32 (the output is rounded to fp16).  Any
   other call — another head dim, a per-batch mask — takes the score path
   below for that leaf.
 * ``scores`` — any other score (the reference's ``slice`` / ``stack``
@@ -510,10 +511,12 @@ def _in_envelope(q, k, v) -> bool:
 
 def _f32_envelope(q, k, v) -> bool:
     """Operands of the fp32 carrier kernel: ``dk <= 128``, ``dv <= 256``, one
-    leading shape (or a 2-D ``q`` / ``v`` shared over it)."""
+    leading shape (or a 2-D ``q`` / ``v`` shared over it); all fp32, or all
+    fp16 (widened to fp32 on the device; the result is rounded back)."""
     ts = (q, k, v)
-    if not all(isinstance(t, torch.Tensor) and t.device.type == "cuda" and t.dtype == torch.float32
-               for t in ts):
+    if not all(isinstance(t, torch.Tensor) and t.device.type == "cuda" for t in ts):
+        return False
+    if q.dtype not in (torch.float32, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
         return False
     if q.dim() < 2 or k.dim() < 2 or v.dim() < 2:
         return False

@@ -19,7 +19,7 @@ Leaves:
   of the HIP attention kernel in carrier mode (scores, mask and
   exponentials stay on chip; the carrier is fp32); fp32 operands with
   ``dk <= 128``, ``dv <= 256``: one launch of the fp32 carrier kernel, with
-  the same mask modes;
+  the same mask modes (fp16 operands widened to fp32 for it);
 * any other ``om_elem(s, v)``: the score and value operands are evaluated and
   folded with ``om_elem`` (``torch_bridge.py:1974-1981``; on device fp32 /
   bf16 operands the ``catopt_hip_om_rows`` row kernel and the HIP GEMM);
@@ -84,7 +84,8 @@ def om_step(state: tuple | None, s: torch.Tensor, v: torch.Tensor):
 
 def _carrier_qk(q, k, v, scale: float = 1.0, **mask_kw) -> tuple | None:
     """``om_elem(scale · q kᵀ, v)`` by the attention kernel in carrier mode
-    (bf16) or the fp32 carrier kernel, or ``None`` outside their envelopes."""
+    (bf16) or the fp32 carrier kernel (fp32, or fp16 widened), or ``None``
+    outside their envelopes."""
     if not _in_envelope(q, k, v):
         if not _f32_envelope(q, k, v):
             return None

@@ -385,7 +385,8 @@ RETENTION_HEAD_DIM = 128
 def retention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma: torch.Tensor,
               scale: float = 1.0) -> torch.Tensor:
     """``scale * Σ_{s<=t} γ_h^(t-s) (q_t·k_s) v_s`` for ``q, k (B,H,T,dk)``,
-    ``v (B,H,T,dv)``, all bf16 or all fp32, ``dk, dv <= 128``.  The kernels
+    ``v (B,H,T,dv)``, all bf16, fp32 or fp16 (widened to fp32), ``dk, dv <=
+    128``.  The kernels
     read a head dim ``d`` (a multiple of 8 for bf16, of 4 for fp32) and any
     ``T`` in place: columns past ``d`` and rows past ``T`` of the 64-step
     chunks load as zeros and are never stored.  When ``dk`` and ``dv``
@@ -394,8 +395,11 @@ def retention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma: torch.Te
     columns, dropped).  fp32 operands compute in fp32 throughout."""
     _need_device(q, k, v, gamma)
     lib = L.load()
+    if q.dtype == torch.float16 and k.dtype == q.dtype and v.dtype == q.dtype:
+        # fp16: the fp32 kernel on widened operands, the output rounded back
+        return retention(q.float(), k.float(), v.float(), gamma, scale).to(torch.float16)
     if q.dtype not in (torch.bfloat16, torch.float32) or k.dtype != q.dtype or v.dtype != q.dtype:
-        raise NotImplementedError("HIP retention runs on bf16 or fp32 operands")
+        raise NotImplementedError("HIP retention runs on bf16, fp32 or fp16 operands")
     if q.dim() != 4 or q.shape != k.shape or v.dim() != 4 or v.shape[:3] != q.shape[:3]:
         raise ValueError("retention operands must be q, k (B, H, T, dk) and v (B, H, T, dv)")
     B, H, T, dk = q.shape

@@ -17,10 +17,15 @@
   and 64, ``fallbacks == 0``) and the kernel directly on a ragged ``T`` with
   ``dk != dv``.
 
-References: float64 numpy over the same fp32 inputs (``oracle.om_elem`` /
-``om_apply`` / ``fused_om_levels``, ``oracle.retention_quadratic`` /
-``retention_kway``).  Gate: 1e-5, global relative error (the verify
-metric), NaN positions exact.
+* fp16 operands run the same fp32 kernels widened on the device, the output
+  rounded to fp16: a masked om leaf, a streaming fold and the K-way
+  retention form, with no fallback.
+
+References: float64 numpy over the same fp32 (or fp16-rounded) inputs
+(``oracle.om_elem`` / ``om_apply`` / ``fused_om_levels``,
+``oracle.retention_quadratic`` / ``retention_kway``).  Gates: 1e-5 for fp32,
+2e-3 for fp16 (its output rounding is 2^-11), global relative error (the
+verify metric), NaN positions exact.
 """
 
 from __future__ import annotations
@@ -41,6 +46,7 @@ from catopt_amd.sink import HipSink, deliver
 pytestmark = pytest.mark.gpu
 mk = Op.make
 TOL = 1e-5
+TOL_F16 = 2e-3
 NEG_INF = Const(float("-inf"))
 F32_MIN = float(np.finfo(np.float32).min)
 
@@ -293,4 +299,55 @@ def test_f32_retention_kernel_ragged_steps_and_widths(dev, T, dk, dv):
     assert out.shape == (B, H, T, dv) and out.dtype == torch.float32
     ref = oracle.retention_quadratic(_np(q), _np(k), _np(v), gam.double().numpy(), 0.75)
     rep = oracle.verify_equiv(ref, _np(out), rtol=TOL)
+    assert rep["passed"], rep
+
+
+# --------------------------------------------------------------------- fp16
+
+
+@pytest.mark.parametrize("kind", ["cmask", "bias_param"])
+def test_f16_masked_leaf_runs_the_fp32_kernel(sink, dev, kind):
+    B, H, Tq, Tk, d = 1, 2, 130, 170, 64
+    rng = np.random.default_rng(40 + len(kind))
+    ir = _masked_ir(B, H, Tq, Tk, d, kind)
+    plane = _plane(kind, Tq, Tk, rng)
+    params = {} if kind == "cmask" else {"m": torch.from_numpy(plane)}
+    q, k, v = (t.half() for t in (_rand((B, H, Tq, d), 41), _rand((B, H, Tk, d), 42), _rand((B, H, Tk, d), 43)))
+    ins = [q.to(dev), k.to(dev), v.to(dev)]
+    res = deliver(ir, params, sink, tuple(ins))
+    mod = res.module
+    out = mod(*ins)
+    assert isinstance(mod, HipOMModule) and mod.fallbacks == 0 and mod.kernel_leaves == 1
+    assert out.dtype == torch.float16
+    s = d ** -0.5 * (_np(q) @ np.swapaxes(_np(k), -1, -2))
+    s = s + plane.astype(np.float64) if kind == "bias_param" else np.where(plane, s, -np.inf)
+    _gate_nan(_softmax_ref(s, _np(v)), out, TOL_F16)
+
+
+def test_f16_streaming_blocks_fold_on_the_kernel(dev):
+    B, H, Tq, cuts, d = 1, 2, 96, (64, 32), 32
+    mod = to_streaming_om_module(_split_causal_ir(B, H, Tq, cuts, d))
+    ins, ref = _split_inputs(B, H, Tq, cuts, d, dev)
+    ins = [t.half() for t in ins]
+    # the reference over the fp16-rounded inputs
+    q, ks, vs = ins[0], ins[1:1 + len(cuts)], ins[1 + len(cuts):]
+    s = _np(q) @ np.swapaxes(np.concatenate([_np(x) for x in ks], -2), -1, -2)
+    s = np.where(oracle.cmask_keep(Tq, sum(cuts)), s, -np.inf)
+    ref = _softmax_ref(s, np.concatenate([_np(x) for x in vs], -2))
+    out = mod(*ins)
+    assert mod.kernel_leaves == len(cuts) and out.dtype == torch.float16
+    _gate_nan(ref, out, TOL_F16)
+
+
+def test_f16_retention_kway_executor(sink, dev):
+    B, H, T, d, C = 1, 2, 256, 64, 64
+    ir, _ = forms.retention_kway_form(B, H, T, d, C, scale=0.5)
+    gam = _gammas(H)
+    q, k, v = (_rand((B, H, T, d), 80 + i, 1 / math.sqrt(d)).half() for i in range(3))
+    ins = tuple(t.to(dev) for t in (q, k, v))
+    res = deliver(ir, {"gamma": gam}, sink, ins)
+    out = res.module(*ins)
+    assert res.module.fallbacks == 0 and out.dtype == torch.float16
+    ref = oracle.retention_quadratic(_np(q), _np(k), _np(v), gam.double().numpy(), 0.5)
+    rep = oracle.verify_equiv(ref, _np(out), rtol=TOL_F16)
     assert rep["passed"], rep
