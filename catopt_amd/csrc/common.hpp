@@ -81,6 +81,15 @@ __device__ __forceinline__ constexpr int acc_row(int r, int g) {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// γ^k for an integer k >= 0 from lg = log2|γ| and neg = (γ < 0), as pow
+// gives it for an integer exponent: 1 at k = 0 (0^0 included, where
+// exp2(0 · log2 0) would be NaN) and, for a negative γ, the sign of k's
+// parity.
+__device__ __forceinline__ float pow_k(float lg, bool neg, int k) {
+  const float r = k == 0 ? 1.f : __builtin_amdgcn_exp2f((float)k * lg);
+  return (neg && (k & 1)) ? -r : r;
+}
+
 // LDS byte address of a pointer into dynamic shared memory.
 __device__ __forceinline__ uint32_t lds_u32(const void* p) {
   return static_cast<uint32_t>(

@@ -189,11 +189,11 @@ __device__ __forceinline__ void dma_tile(const uint16_t* base, int64_t rows, int
 // Decay factors of a lane's transposed-v elements: element e of the key-step
 // u fragment is key 16u + 4g + (e < 4 ? e : e + 4); vf3[e] = γ^(C - key) at
 // u = 3, and step u - 1's factors are step u's times γ^16.
-__device__ __forceinline__ void v_decay3(const Lanes& L, float lg, float vf3[8]) {
+__device__ __forceinline__ void v_decay3(const Lanes& L, float lg, bool neg, float vf3[8]) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int key = 48 + 4 * (L.G >> 1) + (e < 4 ? e : e + 4);
-    vf3[e] = __builtin_amdgcn_exp2f((float)(CH - key) * lg);
+    vf3[e] = pow_k(lg, neg, CH - key);
   }
 }
 
@@ -246,11 +246,13 @@ __global__ __launch_bounds__(NT, 1) void retention_state(
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const Lanes L(tid);
-  const float lg = __log2f(gamma[bh % H]);
-  const float gC = __builtin_amdgcn_exp2f((float)CH * lg);
-  const float g16 = __builtin_amdgcn_exp2f(16.f * lg);
+  const float gam = gamma[bh % H];
+  const float lg = __log2f(fabsf(gam));
+  const bool neg = gam < 0.f;
+  const float gC = pow_k(lg, neg, CH);
+  const float g16 = pow_k(lg, neg, 16);
   float vf3[8];
-  v_decay3(L, lg, vf3);
+  v_decay3(L, lg, neg, vf3);
   uint32_t koff[4], voff[4];
   tile_offsets(tid, dk, koff);
   tile_offsets(tid, dv, voff);
@@ -320,22 +322,22 @@ __global__ __launch_bounds__(NT, 1) void retention_state(
 template <int ROLE>  // 0..2: the score tile (kb, qb) = (0,0), (0,1), (1,1); 3: none
 __device__ __forceinline__ void out_segment(
     char* lds, const uint16_t* qh, const uint16_t* kh, const uint16_t* vh, uint16_t* oh, int64_t T,
-    int dk, int dv, float scale, float lg, int c0, int c1, f32x16 S[4], const Lanes& L, int w, int tid) {
+    int dk, int dv, float scale, float lg, bool neg, int c0, int c1, f32x16 S[4], const Lanes& L, int w, int tid) {
   constexpr bool SCORE = ROLE < 3;
   constexpr int KB = ROLE == 2 ? 1 : 0;
   constexpr int QB = ROLE == 0 ? 0 : 1;
-  const float gC = __builtin_amdgcn_exp2f((float)CH * lg);
-  const float g16 = __builtin_amdgcn_exp2f(16.f * lg);
+  const float gC = pow_k(lg, neg, CH);
+  const float g16 = pow_k(lg, neg, 16);
   float vf3[8];
-  v_decay3(L, lg, vf3);
+  v_decay3(L, lg, neg, vf3);
   float gq[2];  // scale γ^a of this lane's query column in each query tile
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) gq[qb] = scale * __builtin_amdgcn_exp2f((float)(32 * qb + L.l32) * lg);
+  for (int qb = 0; qb < 2; ++qb) gq[qb] = scale * pow_k(lg, neg, 32 * qb + L.l32);
   float dec[16];  // scale γ^(a - c) of the score tile's entries (0 above the diagonal)
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int c = 32 * KB + acc_row(r, L.g), a = 32 * QB + L.l32;
-    dec[r] = (SCORE && c <= a) ? scale * __builtin_amdgcn_exp2f((float)(a - c) * lg) : 0.f;
+    dec[r] = (SCORE && c <= a) ? scale * pow_k(lg, neg, a - c) : 0.f;
   }
   uint32_t koff[4], voff[4];
   tile_offsets(tid, dk, koff);
@@ -521,7 +523,9 @@ __global__ __launch_bounds__(NT, 1) void retention_out(
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const Lanes L(tid);
-  const float lg = __log2f(gamma[bh % H]);
+  const float gam = gamma[bh % H];
+  const float lg = __log2f(fabsf(gam));
+  const bool neg = gam < 0.f;
   const int c0 = plan.seg[s], c1 = plan.seg[s + 1];
   if (c0 >= c1) return;
 
@@ -536,7 +540,7 @@ __global__ __launch_bounds__(NT, 1) void retention_out(
     const float* ph = pieces + (int64_t)bh * 2 * plan.nseg * WFLOATS;
     for (int p = 0; p < 2 * plan.nseg; ++p) {
       if (plan.r0[p] >= plan.r1[p] || plan.r1[p] > c0) continue;
-      const float fct = __builtin_amdgcn_exp2f((float)(c0 - plan.r1[p]) * (float)CH * lg);
+      const float fct = pow_k(lg, neg, (c0 - plan.r1[p]) * CH);
       const f32x4* src = reinterpret_cast<const f32x4*>(ph + (int64_t)p * WFLOATS);
 #pragma unroll
       for (int t = 0; t < 4; ++t)
@@ -555,13 +559,13 @@ __global__ __launch_bounds__(NT, 1) void retention_out(
   uint16_t* oh = o + hb * dv;
   // wave roles: waves 0-2 each take one score tile of the causal block
   if (w == 0)
-    out_segment<0>(lds, qh, kh, vh, oh, T, dk, dv, scale, lg, c0, c1, S, L, w, tid);
+    out_segment<0>(lds, qh, kh, vh, oh, T, dk, dv, scale, lg, neg, c0, c1, S, L, w, tid);
   else if (w == 1)
-    out_segment<1>(lds, qh, kh, vh, oh, T, dk, dv, scale, lg, c0, c1, S, L, w, tid);
+    out_segment<1>(lds, qh, kh, vh, oh, T, dk, dv, scale, lg, neg, c0, c1, S, L, w, tid);
   else if (w == 2)
-    out_segment<2>(lds, qh, kh, vh, oh, T, dk, dv, scale, lg, c0, c1, S, L, w, tid);
+    out_segment<2>(lds, qh, kh, vh, oh, T, dk, dv, scale, lg, neg, c0, c1, S, L, w, tid);
   else
-    out_segment<3>(lds, qh, kh, vh, oh, T, dk, dv, scale, lg, c0, c1, S, L, w, tid);
+    out_segment<3>(lds, qh, kh, vh, oh, T, dk, dv, scale, lg, neg, c0, c1, S, L, w, tid);
 }
 
 // Segments per head: about one workgroup per CU in all, at least two chunks

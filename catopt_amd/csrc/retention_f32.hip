@@ -115,19 +115,21 @@ __global__ __launch_bounds__(kNT) void retention_f32(const float* __restrict__ q
   float* oh = o + base;
 
   // decay factors of this lane, fixed over the chunks (exp2 domain)
-  const float lg = log2f(gamma[h]);
+  const float gam = gamma[h];
+  const float lg = log2f(fabsf(gam));
+  const bool neg = gam < 0.f;
   float rowf[2][16], diagf[16], offf[16], wv[2][16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int ar = acc_row(r, g);
-    rowf[0][r] = __builtin_amdgcn_exp2f((float)ar * lg);                       // γ^a, a = row in chunk
-    rowf[1][r] = __builtin_amdgcn_exp2f((float)(32 + ar) * lg);
-    diagf[r] = ar <= l32 ? __builtin_amdgcn_exp2f((float)(l32 - ar) * lg) : 0.f;  // D on diagonal tiles
-    offf[r] = __builtin_amdgcn_exp2f((float)(32 + l32 - ar) * lg);               // D on the lower tile
-    wv[0][r] = __builtin_amdgcn_exp2f((float)(kC - ar) * lg);                   // γ^(C − b)
-    wv[1][r] = __builtin_amdgcn_exp2f((float)(kC - 32 - ar) * lg);
+    rowf[0][r] = pow_k(lg, neg, ar);                             // γ^a, a = row in chunk
+    rowf[1][r] = pow_k(lg, neg, 32 + ar);
+    diagf[r] = ar <= l32 ? pow_k(lg, neg, l32 - ar) : 0.f;        // D on diagonal tiles
+    offf[r] = pow_k(lg, neg, 32 + l32 - ar);                      // D on the lower tile
+    wv[0][r] = pow_k(lg, neg, kC - ar);                           // γ^(C − b)
+    wv[1][r] = pow_k(lg, neg, kC - 32 - ar);
   }
-  const float gC = __builtin_amdgcn_exp2f((float)kC * lg);
+  const float gC = pow_k(lg, neg, kC);
 
   // per-lane parts of the load offsets (bytes); row bases go to soffset
   uint32_t vrow[4];

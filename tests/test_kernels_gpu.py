@@ -272,6 +272,24 @@ def test_retention_vs_kway_form(dev, B, H, T):
     _gate(ref, o, TOL_BF16)
 
 
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, TOL_BF16), (torch.float32, TOL_F32)])
+def test_retention_decay_rates_zero_one_and_negative(dev, dtype, tol):
+    # γ^k as pow gives it for integer k: 0^0 = 1 (a γ = 0 head is the
+    # diagonal term alone), γ = 1 (no decay), a negative γ alternating in
+    # sign; T = 1024 over 4 heads splits each head into segments, so the
+    # start-state pieces are scaled by these powers too
+    B, H, T, d = 1, 4, 1024, 128
+    q = _rand((B, H, T, d), dtype, 140, 1 / math.sqrt(d))
+    k = _rand((B, H, T, d), dtype, 141, 1 / math.sqrt(d))
+    v = _rand((B, H, T, d), dtype, 142, 1 / math.sqrt(d))
+    gam = np.array([0.0, 1.0, -0.9, 0.5], dtype=np.float32)
+    o = K.retention(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(gam).to(dev), 0.25)
+    ref = oracle.retention_quadratic(_np(q), _np(k), _np(v), gam.astype(np.float64), 0.25)
+    assert np.isfinite(ref).all() and np.isfinite(_np(o)).all()
+    for h in range(H):  # per head: the heads' scales differ by orders of magnitude
+        _gate(ref[:, h], o[:, h], tol)
+
+
 @pytest.mark.parametrize("dk,dv", [(64, 64), (96, 64), (128, 80)])
 def test_retention_narrow_heads(dev, dk, dv):
     # head dims below 128 run zero-padded to the kernel's width
