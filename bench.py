@@ -466,8 +466,8 @@ class C3Attention(Form):
     workload = "C3 causal MHA (om_apply(om_elem) online softmax): q,k,v[4,32,4096,128] bf16, scale 1/sqrt(128)"
     peak = PEAK["bf16_tflops"]
     work = dom_work = 4.0 * B * H * T * T * Dh / 2  # causal half of the square
-    dom_name = "attn_fwd_kernel<128,CAUSAL>"
-    dom_key = "attn_fwd_kernel<128, 1>"
+    dom_name = "attn_q64_kernel<CAUSAL>"
+    dom_key = "attn_q64_kernel<1>"
 
     def setup(self, dev):
         import torch

@@ -51,6 +51,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "attn_q64_loop.inc"
 
 namespace catopt {
 namespace {
@@ -109,6 +110,30 @@ __device__ __forceinline__ s16x4 ds_read_tr(const char* lds_base, int byte_off) 
       (__attribute__((address_space(3))) s16x4*)(lds_base + byte_off));
 }
 
+// (head, query tile) of this workgroup in a 1-D grid of nqt x H x B tiles.
+// Workgroups are dealt round robin over the 8 XCDs (linear id L runs on XCD
+// L % 8).  Each XCD owns a contiguous range of heads, so that K and V of a
+// head stay in one XCD's L2, and takes them in pairs of heads, each pair in
+// query-tile order (qi = 0, the longest causal tile, of both heads first).
+// Head by head left a tail of long tiles started late (about 10% of a
+// causal launch at C3's shape); all of an XCD's heads in query-tile order
+// kept 16 heads' K and V in flight and read 3.5x the algorithmic bytes from
+// HBM.  Pairs keep both the tail and the traffic down.
+__device__ __forceinline__ void tile_of_block(int nqt, int& bh, int& qi) {
+  const int nblk = gridDim.x, nbh = nblk / nqt;
+  if ((nblk & 7) == 0 && (nbh & 15) == 0) {
+    const int hx = nbh >> 3, kk = blockIdx.x >> 3;
+    const int pair = kk / (2 * nqt), w = kk - pair * 2 * nqt;
+    qi = w >> 1;
+    bh = (blockIdx.x & 7) * hx + 2 * pair + (w & 1);
+  } else {
+    int w = blockIdx.x;
+    if ((nblk & 7) == 0) w = (w & 7) * (nblk >> 3) + (w >> 3);
+    bh = w / nqt;
+    qi = w - bh * nqt;
+  }
+}
+
 template <int D, int MASK>
 __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
     const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh, int64_t qst,
@@ -119,16 +144,9 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
     const void* __restrict__ mask, int64_t mask_ld, int normalize) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   using L = AttnLds<D>;
-  // 1-D grid of nqt x H x B tiles.  Workgroups are dealt round robin over
-  // the 8 XCDs, so linear id L runs on XCD L % 8; work item w is chosen so
-  // that each XCD owns a contiguous range of (b, h) with all of their query
-  // tiles, and K / V of one head stay in one XCD's L2.  Within a head the
-  // causal order is longest tile first.
   const int nqt = (Tq + QT - 1) / QT;
-  const int nblk = gridDim.x;
-  int w = blockIdx.x;
-  if ((nblk & 7) == 0) w = (w & 7) * (nblk >> 3) + (w >> 3);
-  const int bh = w / nqt, qi = w - bh * nqt;
+  int bh, qi;
+  tile_of_block(nqt, bh, qi);
   const int qt = (MASK == CATOPT_MASK_CAUSAL) ? (nqt - 1 - qi) : qi;
   const int64_t b = bh / H, h = bh - (int64_t)(bh / H) * H;
   q += b * qsb + h * qsh;
@@ -446,6 +464,191 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
   }
 }
 
+// ------------------------------------------------ 64 queries per wave (D = 128)
+// One workgroup = 4 waves = 256 queries of one (b, h), 64 per wave, one wave
+// per SIMD (512 registers: the O accumulators, Q and K fragments in AGPRs).
+// Every K / Vᵀ fragment a wave reads from LDS feeds two MFMAs, half the LDS
+// bytes per MFMA of the 32-query kernel above.  The tile loop is the inline
+// asm of attn_q64_loop.inc (generated by gen_attn_q64.py, which documents
+// its registers, the software pipeline of the softmax across tiles, the LDS
+// ring and the waits); this C++ computes its addresses and bounds and does
+// the epilogue.  Keys come in whole 64-key tiles (Tk a multiple of 64, no
+// key mask): causal and unmasked leaves only.
+constexpr int QT64 = 256;                // queries per workgroup
+constexpr int LDS64 = 128 * 1024;        // three 32 KB tile stages; O staged through it after the loop
+
+template <int MASK>
+__global__ __launch_bounds__(NT, 1) void attn_q64_kernel(
+    const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh, int64_t qst,
+    const uint16_t* __restrict__ k, int64_t ksb, int64_t ksh, int64_t kst,
+    const uint16_t* __restrict__ v, int64_t vsb, int64_t vsh, int64_t vst,
+    uint16_t* __restrict__ o, int64_t osb, int64_t osh, int64_t ost, float* __restrict__ m_out,
+    float* __restrict__ l_out, int H, int Tq, int Tk, float scale, int64_t causal_off, int normalize) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  const int nqt = (Tq + QT64 - 1) / QT64;
+  int bh, qi;
+  tile_of_block(nqt, bh, qi);
+  const int qt = (MASK == CATOPT_MASK_CAUSAL) ? (nqt - 1 - qi) : qi;
+  const int64_t b = bh / H, h = bh - (int64_t)(bh / H) * H;
+  q += b * qsb + h * qsh;
+  k += b * ksb + h * ksh;
+  v += b * vsb + h * vsh;
+  o += b * osb + h * osh;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, g = lane >> 5, G = lane >> 4, jj = lane & 15;
+  const int q0 = qt * QT64;
+  const int qw0 = q0 + wave * 64;  // first query of this wave
+  const float c = scale * 1.4426950408889634f;
+
+  // tiles of the workgroup (nkv), of this wave (wnt: a wave past Tq computes
+  // none) and the first one reaching past the wave's first query (mfrom:
+  // from there on the causal mask applies)
+  int64_t kv_end = Tk, wave_end = Tk, mfrom64 = 0x7fffffff;
+  if (MASK == CATOPT_MASK_CAUSAL) {
+    const int64_t lim = (int64_t)q0 + QT64 + causal_off;
+    kv_end = lim < 0 ? 0 : (lim < Tk ? lim : Tk);
+    const int64_t wl = (int64_t)qw0 + 64 + causal_off;
+    wave_end = wl < 0 ? 0 : (wl < Tk ? wl : Tk);
+    const int64_t x = (int64_t)qw0 + causal_off - 63;  // first tile t with 64 t > x
+    const int64_t fl = x >= 0 ? x / 64 : -((-x + 63) / 64);
+    mfrom64 = fl + 1 < 0 ? 0 : fl + 1;
+  }
+  const int nkv = (int)((kv_end + 63) / 64);
+  const int wnt = qw0 < Tq ? (int)((wave_end + 63) / 64) : 0;
+  const int mfrom = (int)(mfrom64 < nkv ? mfrom64 : nkv);
+  int64_t l0 = (int64_t)qw0 + causal_off;  // (keys and queries stay below 2^31)
+  l0 = l0 < -(1LL << 30) ? -(1LL << 30) : (l0 > (1LL << 30) ? (1LL << 30) : l0);
+  const int lim0 = (int)l0 + l32 - 4 * g;
+
+  // LDS fragment addresses of stage 0 (stage 1 adds 32 KB in the immediate,
+  // stage 2 reads through the second set, 64 KB further): K rows swizzled as
+  // tile_off<128>, Vᵀ by the transposing-read swizzle vtile_off<128>
+  const uint32_t lb = lds_u32(lds);
+  uint32_t ka[8], kah[8], va[4], vah[4], ko[4], vo[4];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    ka[j] = lb + tile_off<128>(l32, 2 * j + g);
+    kah[j] = ka[j] + 65536;
+  }
+#pragma unroll
+  for (int db = 0; db < 4; ++db) {
+    const int key0 = 4 * (G >> 1) + (jj >> 2);
+    const int d = 32 * db + 16 * (G & 1) + 4 * (jj & 3);
+    va[db] = lb + AttnLds<128>::TILE_BYTES + vtile_off<128>(key0, d >> 3) + (d & 7) * 2;
+    vah[db] = va[db] + 65536;
+  }
+  // this thread's four 16-byte slots of a K and of a V tile (byte offsets
+  // from the tile's first row; the tile's offset goes in soffset)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int s = i * NT + wave * 64 + lane;
+    const int row = s / AttnLds<128>::CH, cp = s % AttnLds<128>::CH;
+    ko[i] = (uint32_t)(row * (int)kst + (cp ^ (row & 15)) * 8) * 2u;
+    vo[i] = (uint32_t)(row * (int)vst + (cp ^ vswz<128>(row)) * 8) * 2u;
+  }
+  uint64_t qa[2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    int row = qw0 + 32 * qb + l32;
+    row = row < Tq ? row : Tq - 1;  // rows past Tq load a valid row; their outputs are dropped
+    qa[qb] = reinterpret_cast<uint64_t>(q + (int64_t)row * qst) + 16 * g;
+  }
+  const u32x4 krs = make_rsrc(k, (uint32_t)(((int64_t)(Tk - 1) * kst + 128) * 2));
+  const u32x4 vrs = make_rsrc(v, (uint32_t)(((int64_t)(Tk - 1) * vst + 128) * 2));
+  const uint32_t kstep = __builtin_amdgcn_readfirstlane((uint32_t)(64 * kst * 2));
+  const uint32_t vstep = __builtin_amdgcn_readfirstlane((uint32_t)(64 * vst * 2));
+  const uint32_t dmab = __builtin_amdgcn_readfirstlane(lb + wave * 1024);
+  const uint32_t ob = lb + wave * 32768 + lane * 16;
+  const int s_nkv = __builtin_amdgcn_readfirstlane(nkv);
+  const int s_wnt = __builtin_amdgcn_readfirstlane(wnt);
+  const int s_mfrom = __builtin_amdgcn_readfirstlane(mfrom);
+  const float s_c = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, c)));
+
+  float m_run[2], m_true[2], l_run[2];
+  int st_t, st_kv0, st_kso, st_vso, st_tmp, st_fl0, st_fl1;
+  asm volatile(ATTN_Q64_ASM
+               : [mr0] "=&v"(m_run[0]), [mr1] "=&v"(m_run[1]), [mt0] "=&v"(m_true[0]),
+                 [mt1] "=&v"(m_true[1]), [lr0] "=&v"(l_run[0]), [lr1] "=&v"(l_run[1]),
+                 [t] "=&s"(st_t), [kv0] "=&s"(st_kv0), [kso] "=&s"(st_kso), [vso] "=&s"(st_vso),
+                 [tmp] "=&s"(st_tmp), [fl0] "=&s"(st_fl0), [fl1] "=&s"(st_fl1)
+               : [nkv] "s"(s_nkv), [wnt] "s"(s_wnt), [mfrom] "s"(s_mfrom), [krs] "s"(krs), [vrs] "s"(vrs),
+                 [kstep] "s"(kstep), [vstep] "s"(vstep), [dmab] "s"(dmab), [c] "s"(s_c), [lim0] "v"(lim0),
+                 [ka0] "v"(ka[0]), [ka1] "v"(ka[1]), [ka2] "v"(ka[2]), [ka3] "v"(ka[3]), [ka4] "v"(ka[4]),
+                 [ka5] "v"(ka[5]), [ka6] "v"(ka[6]), [ka7] "v"(ka[7]), [kah0] "v"(kah[0]), [kah1] "v"(kah[1]),
+                 [kah2] "v"(kah[2]), [kah3] "v"(kah[3]), [kah4] "v"(kah[4]), [kah5] "v"(kah[5]),
+                 [kah6] "v"(kah[6]), [kah7] "v"(kah[7]), [va0] "v"(va[0]), [va1] "v"(va[1]), [va2] "v"(va[2]),
+                 [va3] "v"(va[3]), [vah0] "v"(vah[0]), [vah1] "v"(vah[1]), [vah2] "v"(vah[2]),
+                 [vah3] "v"(vah[3]), [ko0] "v"(ko[0]), [ko1] "v"(ko[1]), [ko2] "v"(ko[2]), [ko3] "v"(ko[3]),
+                 [vo0] "v"(vo[0]), [vo1] "v"(vo[1]), [vo2] "v"(vo[2]), [vo3] "v"(vo[3]), [qa0] "v"(qa[0]),
+                 [qa1] "v"(qa[1]), [ob] "v"(ob)
+               : "memory", "m0", "vcc", "scc", ATTN_Q64_CLOBBERS);
+
+  // ---- epilogue (as attn_fwd_kernel's): O from LDS, back to the true max,
+  // normalise, store
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int qrow = qw0 + 32 * qb + l32;
+    float fix = 1.f;
+    if (m_true[qb] != -__builtin_inff() && m_run[qb] != -__builtin_inff())
+      fix = __builtin_amdgcn_exp2f((m_run[qb] - m_true[qb]) * c);
+    const float l_sum = l_run[qb] + __shfl_xor(l_run[qb], 32, 64);
+    const float l_tot = l_sum * fix;
+    if (qrow >= Tq) continue;
+    const float inv = normalize ? 1.0f / l_sum : fix;
+    const bool empty_row = normalize && l_sum == 0.f;
+    const float fill = normalize == 2 ? 0.f : __builtin_nanf("");
+    uint16_t* orow = o + (int64_t)qrow * ost;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(lds + wave * 32768 + lane * 16 +
+                                                        ((qb * 4 + db) * 4 + rg) * 1024);
+        const int d = 32 * db + 8 * rg + 4 * g;
+        float x0 = x[0] * inv, x1 = x[1] * inv, x2 = x[2] * inv, x3 = x[3] * inv;
+        if (empty_row) x0 = x1 = x2 = x3 = fill;
+        *reinterpret_cast<u32x2*>(orow + d) = u32x2{pack_bf16x2(x0, x1), pack_bf16x2(x2, x3)};
+      }
+    }
+    if (g == 0) {
+      const int64_t mi = (b * H + h) * (int64_t)Tq + qrow;
+      if (m_out) m_out[mi] = m_true[qb] * scale;  // natural-log units of the scaled score
+      if (l_out) l_out[mi] = l_tot;
+    }
+  }
+}
+
+template <int MASK>
+int32_t attn_q64_launch(const uint16_t* q, const int64_t* qs, const uint16_t* k, const int64_t* ks,
+                        const uint16_t* v, const int64_t* vs, uint16_t* o, const int64_t* os, float* m_out,
+                        float* l_out, int64_t B, int64_t H, int64_t Tq, int64_t Tk, float scale,
+                        int64_t causal_off, int normalize, hipStream_t s) {
+  static bool attr_done = false;
+  if (!attr_done) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_q64_kernel<MASK>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, LDS64);
+    if (e != hipSuccess) return set_hip_error(e);
+    attr_done = true;
+  }
+  const int64_t nblk = (Tq + QT64 - 1) / QT64 * H * B;
+  if (nblk > 0x7fffffffLL) return CATOPT_E_UNSUPPORTED;
+  attn_q64_kernel<MASK><<<dim3((uint32_t)nblk), dim3(NT), LDS64, s>>>(
+      q, qs[0], qs[1], qs[2], k, ks[0], ks[1], ks[2], v, vs[0], vs[1], vs[2], o, os[0], os[1], os[2], m_out,
+      l_out, (int)H, (int)Tq, (int)Tk, scale, causal_off, normalize);
+  CATOPT_LAUNCH_CHECK();
+  return CATOPT_OK;
+}
+
+// The 64-query kernel takes bf16, D = 128, no mask or causal, whole 64-key
+// tiles, and K / V heads whose buffer ranges fit 31 bits.
+bool q64_fits(int64_t d, int32_t mode, int64_t Tk, const int64_t* ks, const int64_t* vs) {
+  if (d != 128 || (mode != CATOPT_MASK_NONE && mode != CATOPT_MASK_CAUSAL)) return false;
+  if (Tk <= 0 || Tk % 64 != 0) return false;
+  return ((Tk - 1) * ks[2] + 128) * 2 < 0x7fffffffLL && ((Tk - 1) * vs[2] + 128) * 2 < 0x7fffffffLL;
+}
+
 template <int D, int MASK>
 int32_t attn_launch(const uint16_t* q, const int64_t* qs, const uint16_t* k, const int64_t* ks,
                     const uint16_t* v, const int64_t* vs, uint16_t* o, const int64_t* os,
@@ -531,6 +734,13 @@ extern "C" int32_t catopt_hip_attn_fwd(int32_t dtype, int64_t B, int64_t H, int6
   auto kp = static_cast<const uint16_t*>(k);
   auto vp = static_cast<const uint16_t*>(v);
   auto op = static_cast<uint16_t*>(o);
+  if (q64_fits(d, mask_mode, Tk, k_strides, v_strides)) {
+    if (mask_mode == CATOPT_MASK_CAUSAL)
+      return attn_q64_launch<CATOPT_MASK_CAUSAL>(qp, q_strides, kp, k_strides, vp, v_strides, op, o_strides,
+                                                 m_out, l_out, B, H, Tq, Tk, scale, causal_off, normalize, s);
+    return attn_q64_launch<CATOPT_MASK_NONE>(qp, q_strides, kp, k_strides, vp, v_strides, op, o_strides, m_out,
+                                             l_out, B, H, Tq, Tk, scale, causal_off, normalize, s);
+  }
   if (d == 128)
     return attn_dispatch_mask<128>(mask_mode, qp, q_strides, kp, k_strides, vp, v_strides, op,
                                    o_strides, m_out, l_out, B, H, Tq, Tk, scale, causal_off, mask,

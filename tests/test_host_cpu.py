@@ -674,3 +674,26 @@ def test_omd_block_restart_form_is_attention_over_restarted_states(dense, bracke
     w = np.exp(sc - sc.max(-1, keepdims=True))
     ref = (w / w.sum(-1, keepdims=True)) @ np.concatenate(blocks)
     assert oracle.verify_equiv(ref, _np(out), rtol=1e-12)["passed"]
+
+
+def test_attention_q64_asm_is_the_generator_output():
+    # attn_q64_loop.inc is committed generated code: it must be exactly what
+    # gen_attn_q64.py emits, and its clobbers must cover every register the
+    # loop names
+    import importlib.util
+    import re
+    from pathlib import Path
+
+    csrc = Path(__file__).resolve().parents[1] / "catopt_amd" / "csrc"
+    spec = importlib.util.spec_from_file_location("gen_attn_q64", csrc / "gen_attn_q64.py")
+    gen = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(gen)
+    text = gen.render()
+    assert (csrc / "attn_q64_loop.inc").read_text() == text
+    body = text.split("#define ATTN_Q64_CLOBBERS")[0]
+    vregs = {int(x) for x in re.findall(r"\bv(\d+)\b", body)}
+    vregs |= {int(b) for a, b in re.findall(r"\bv\[(\d+):(\d+)\]", body)}
+    aregs = {int(x) for x in re.findall(r"\ba(\d+)\b", body)} | {int(b) for a, b in re.findall(r"\ba\[(\d+):(\d+)\]", body)}
+    assert max(vregs) < gen.NVGPR and max(aregs) < 256
+    assert body.count("v_mfma_f32_32x32x16_bf16") == 3 * 64 + 16  # three unrolled tiles and the drain
+    assert body.count("s_barrier") == 1 + 3

@@ -227,6 +227,61 @@ def test_attention_causal_offset_and_cross_lengths(dev):
     _gate(ref, o, TOL_BF16)
 
 
+# The 64-query kernel (attn_q64_kernel) takes d = 128, no mask or causal, and
+# whole 64-key tiles; these cases reach its edges: query counts off a
+# multiple of the 256-query workgroup and of a wave's 64, keys of one and of
+# many tiles, causal offsets that start, end or empty rows, several heads per
+# XCD and a head count off a multiple of 8 (the two grid mappings).
+@pytest.mark.parametrize("B,H,Tq,Tk,causal,off", [
+    (1, 2, 256, 256, True, 0), (2, 3, 100, 320, True, 220), (1, 16, 300, 512, True, 0),
+    (1, 2, 200, 64, False, 0), (1, 4, 512, 512, True, -130), (1, 2, 64, 1024, True, 960),
+    (2, 8, 320, 384, False, 0), (1, 1, 1000, 1024, True, 24),
+])
+def test_attention_q64_tiles(dev, B, H, Tq, Tk, causal, off):
+    q, k, v = _qkv(B, H, Tq, 128, 300 + Tq + Tk, Tk=Tk)
+    scale = 1 / math.sqrt(128)
+    o, m, lsum = K.attention(q.to(dev), k.to(dev), v.to(dev), scale, causal=causal, causal_off=off,
+                             return_ml=True)
+    ref, mr, lr = oracle.attention_om(_np(q), _np(k), _np(v), scale, causal=causal, causal_off=off,
+                                      return_ml=True)
+    on = _np(o)
+    assert np.array_equal(np.isnan(on), np.isnan(ref))  # rows with no key (negative offsets) are NaN
+    fin = ~np.isnan(ref)
+    _gate(np.where(fin, ref, 0), np.where(fin, on, 0), TOL_BF16)
+    mf = np.isfinite(mr)
+    assert np.array_equal(np.isfinite(_np(m)), mf)
+    _gate(np.where(mf, mr, 0), np.where(mf, _np(m), 0), 1e-5)
+    # a row with no key: the single-leaf oracle's l is exp(-inf - -inf) = NaN;
+    # the kernel's carrier is the empty one, (m, l) = (-inf, 0)
+    ln = _np(lsum)
+    _gate(np.where(mf, lr, 0), np.where(mf, ln, 0), TOL_BF16)
+    assert bool((ln[~mf] == 0).all())
+
+
+def test_attention_q64_strided_and_zero_rows(dev):
+    # (B, T, H, d) operands viewed as (B, H, T, d): row stride H·d, the head
+    # ranges of the buffer resources far from the tensor start; a causal
+    # offset that leaves the first rows without keys returns 0 there in the
+    # sdpa convention
+    B, T, H = 2, 448, 3
+    base = [_rand((B, T, H, 128), torch.bfloat16, 400 + i).to(dev) for i in range(3)]
+    q, k, v = (t.transpose(1, 2) for t in base)
+    o = K.attention(q, k, v, 0.09, causal=True, causal_off=-40, empty_rows="zero")
+    ref = oracle.attention_om(_np(q), _np(k), _np(v), 0.09, causal=True, causal_off=-40)
+    ref = np.where(np.isnan(ref), 0.0, ref)
+    _gate(ref, o, TOL_BF16)
+    assert bool((o[:, :, :40] == 0).all())
+
+
+def test_attention_q64_unnormalised_numerator(dev):
+    q, k, v = _qkv(1, 2, 192, 128, 450, Tk=256)
+    a, m, lsum = K.attention(q.to(dev), k.to(dev), v.to(dev), 0.1, causal=False, normalize=False, return_ml=True)
+    out, mr, lr = oracle.attention_om(_np(q), _np(k), _np(v), 0.1, causal=False, return_ml=True)
+    _gate(mr, m, 1e-5)
+    _gate(lr, lsum, TOL_BF16)
+    _gate(out * lr, a, TOL_BF16)
+
+
 def test_om_compose_kernel(dev):
     rng = np.random.default_rng(1)
     m1 = rng.standard_normal((40, 1))
