@@ -200,11 +200,11 @@ def host_provenance() -> dict:
             "python": sys.version.split()[0]}
 
 
-def time_cpu(fn, budget_s: float, min_reps: int = 4) -> tuple[float, float, int, object]:
-    """Median and IQR of seconds per call of ``fn`` (≥ ``min_reps`` calls,
-    about ``budget_s`` in all, at most 50), the reference's timing contract
-    (``timing.py:54-80``: median, and the IQR from quartiles at n = 4, 0.0
-    below 4 samples)."""
+def time_cpu(fn, budget_s: float, min_reps: int = 4) -> tuple[float, tuple[float, float], int, object]:
+    """Median and (first, third) quartiles of seconds per call of ``fn``
+    (≥ ``min_reps`` calls, about ``budget_s`` in all, at most 50), the
+    reference's timing contract (``timing.py:54-80``: median, and the IQR
+    from quartiles at n = 4; no spread below 4 samples)."""
     times, out = [], None
     t_start = time.perf_counter()
     while len(times) < min_reps or time.perf_counter() - t_start < budget_s:
@@ -214,11 +214,17 @@ def time_cpu(fn, budget_s: float, min_reps: int = 4) -> tuple[float, float, int,
         if len(times) >= 50:
             break
     med = statistics.median(times)
-    iqr = 0.0
+    quart = (med, med)
     if len(times) >= 4:
         q1, _, q3 = statistics.quantiles(times, n=4)
-        iqr = q3 - q1
-    return med, iqr, len(times), out
+        quart = (q1, q3)
+    return med, quart, len(times), out
+
+
+def rate_iqr(work: float, quart: tuple[float, float]) -> float:
+    """IQR of the rate work / t from the quartiles of t (the rate falls as t
+    grows, so its quartiles are work / q3 and work / q1)."""
+    return work / quart[0] - work / quart[1]
 
 
 class host_threads:
@@ -389,7 +395,7 @@ class C1WeightChain(Form):
             sec, iqr, reps, out = time_cpu(lambda: oracle.torch_cpu.weight_chain(x, W, c), budget)
         self.step()
         rel = oracle.verify_equiv(out.double().numpy(), self.y.cpu().double().numpy())["max_rel"]
-        return cpu_record(self.work / sec / 1e12, self.work * iqr / sec ** 2 / 1e12, "TFLOP/s", ht.n,
+        return cpu_record(self.work / sec / 1e12, rate_iqr(self.work, iqr) / 1e12, "TFLOP/s", ht.n,
                           "full C1 forward (the folded linear, fp32)", reps, rel)
 
 class C2SwiGLU(Form):
@@ -456,7 +462,7 @@ class C2SwiGLU(Form):
         self.step()
         rel = oracle.verify_equiv(out.double().numpy(), self.y.reshape(-1, self.D)[:rows].cpu().double().numpy())["max_rel"]
         flops = self.work * rows / self.M
-        return cpu_record(flops / sec / 1e12, flops * iqr / sec ** 2 / 1e12, "TFLOP/s", ht.n,
+        return cpu_record(flops / sec / 1e12, rate_iqr(flops, iqr) / 1e12, "TFLOP/s", ht.n,
                           f"first {rows} of {self.M} rows: rms_norm, fused gate/up linear, silu*mul, down linear (bf16)",
                           reps, rel)
 
@@ -509,7 +515,7 @@ class C3Attention(Form):
         self.step()
         rel = oracle.verify_equiv(out.double().numpy(), self.o[0, :nh].cpu().double().numpy())["max_rel"]
         flops = self.work * nh / (self.B * self.H)
-        return cpu_record(flops / sec / 1e12, flops * iqr / sec ** 2 / 1e12, "TFLOP/s", ht.n,
+        return cpu_record(flops / sec / 1e12, rate_iqr(flops, iqr) / 1e12, "TFLOP/s", ht.n,
                           f"{nh} of {self.B * self.H} heads, T={self.T}: matmul, masked_fill, softmax, matmul (bf16; "
                           "work counted as the causal half)", reps, rel)
 
@@ -568,7 +574,7 @@ class C4Retention(Form):
         self.step()
         rel = oracle.verify_equiv(out.double().numpy(), self.o[:1, :, :Ts].cpu().double().numpy())["max_rel"]
         nbytes = 4.0 * self.H * Ts * self.Dh * 2
-        return cpu_record(nbytes / sec / 1e9, nbytes * iqr / sec ** 2 / 1e9, "GB/s", ht.n,
+        return cpu_record(nbytes / sec / 1e9, rate_iqr(nbytes, iqr) / 1e9, "GB/s", ht.n,
                           f"b=0, all {self.H} heads, first {Ts} of {self.T} steps: the chunked decayed form, C={self.C} "
                           "(bf16 operands, fp32 arithmetic)", reps, rel)
 
@@ -623,7 +629,7 @@ class C5SSM(Form):
         self.step()
         rel = oracle.verify_equiv(out.double().numpy(), self.y[:, :Ts].cpu().double().numpy())["max_rel"]
         nbytes = self.work * Ts / self.T
-        return cpu_record(nbytes / sec / 1e9, nbytes * iqr / sec ** 2 / 1e9, "GB/s", ht.n,
+        return cpu_record(nbytes / sec / 1e9, rate_iqr(nbytes, iqr) / 1e9, "GB/s", ht.n,
                           f"all {self.B}x{self.D}x{self.N} lanes, first {Ts} of {self.T} steps: the serial recurrence "
                           "and read-out, each step over every lane (fp32)", reps, rel)
 
@@ -675,7 +681,7 @@ class DenseScan(Form):
         self.step()
         rel = oracle.verify_equiv(out.double().numpy(), self.out[:Bs, :, 0].cpu().double().numpy())["max_rel"]
         flops = 2.0 * self.T * Bs * self.d * self.d
-        return cpu_record(flops / sec / 1e12, flops * iqr / sec ** 2 / 1e12, "TFLOP/s", ht.n,
+        return cpu_record(flops / sec / 1e12, rate_iqr(flops, iqr) / 1e12, "TFLOP/s", ht.n,
                           f"{Bs} of {self.B} sequences, all {self.T} steps: one batched matmul + add per step (fp32)",
                           reps, rel)
 
@@ -733,7 +739,7 @@ class OmdScanAttention(Form):
         self.step()
         rel = oracle.verify_equiv(out.double().numpy(), self.out.double().cpu().numpy())["max_rel"]
         flops = 2.0 * self.Tq * self.T * (self.dk + self.d)
-        return cpu_record(flops / sec / 1e12, flops * iqr / sec ** 2 / 1e12, "TFLOP/s", ht.n,
+        return cpu_record(flops / sec / 1e12, rate_iqr(flops, iqr) / 1e12, "TFLOP/s", ht.n,
                           f"the full form: {self.Tq} queries over all {self.T} scan states (serial scan, dense "
                           "softmax, fp32)", reps, rel)
 

@@ -477,18 +477,49 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
 constexpr int QT64 = 256;                // queries per workgroup
 constexpr int LDS64 = 128 * 1024;        // three 32 KB tile stages; O staged through it after the loop
 
+// Workgroups that take two query tiles of one (b, h), tiles p and nqt - 1 - p
+// (nqt even): every causal pair then holds the same number of key tiles, so
+// the grid stays balanced without a longest-first order, and a CU starts half
+// as many workgroups (each start costs a dispatch gap, and the first tile's
+// prologue waits out the memory latency alone).  Each XCD owns a contiguous
+// range of heads and takes them in order, pairs of a head together.
+__device__ __forceinline__ void pair_of_block(int npair, int& bh, int& p) {
+  const int nblk = gridDim.x, nbh = nblk / npair;
+  int w = blockIdx.x;
+  if ((nblk & 7) == 0 && (nbh & 7) == 0) {
+    const int hx = nbh >> 3, kk = w >> 3;
+    bh = (w & 7) * hx + kk / npair;
+    p = kk - (kk / npair) * npair;
+    return;
+  }
+  if ((nblk & 7) == 0) w = (w & 7) * (nblk >> 3) + (w >> 3);
+  bh = w / npair;
+  p = w - bh * npair;
+}
+
 template <int MASK>
 __global__ __launch_bounds__(NT, 1) void attn_q64_kernel(
     const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh, int64_t qst,
     const uint16_t* __restrict__ k, int64_t ksb, int64_t ksh, int64_t kst,
     const uint16_t* __restrict__ v, int64_t vsb, int64_t vsh, int64_t vst,
     uint16_t* __restrict__ o, int64_t osb, int64_t osh, int64_t ost, float* __restrict__ m_out,
-    float* __restrict__ l_out, int H, int Tq, int Tk, float scale, int64_t causal_off, int normalize) {
+    float* __restrict__ l_out, int H, int Tq, int Tk, float scale, int64_t causal_off, int normalize,
+    int paired) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   const int nqt = (Tq + QT64 - 1) / QT64;
-  int bh, qi;
-  tile_of_block(nqt, bh, qi);
-  const int qt = (MASK == CATOPT_MASK_CAUSAL) ? (nqt - 1 - qi) : qi;
+  // the workgroup's query tiles: the short one of a causal pair first
+  int bh, qt_first, ntile;
+  if (paired) {
+    int p;
+    pair_of_block(nqt >> 1, bh, p);
+    qt_first = p;
+    ntile = 2;
+  } else {
+    int qi;
+    tile_of_block(nqt, bh, qi);
+    qt_first = (MASK == CATOPT_MASK_CAUSAL) ? (nqt - 1 - qi) : qi;
+    ntile = 1;
+  }
   const int64_t b = bh / H, h = bh - (int64_t)(bh / H) * H;
   q += b * qsb + h * qsh;
   k += b * ksb + h * ksh;
@@ -498,125 +529,175 @@ __global__ __launch_bounds__(NT, 1) void attn_q64_kernel(
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g = lane >> 5, G = lane >> 4, jj = lane & 15;
-  const int q0 = qt * QT64;
-  const int qw0 = q0 + wave * 64;  // first query of this wave
   const float c = scale * 1.4426950408889634f;
 
-  // tiles of the workgroup (nkv), of this wave (wnt: a wave past Tq computes
-  // none) and the first one reaching past the wave's first query (mfrom:
-  // from there on the causal mask applies)
-  int64_t kv_end = Tk, wave_end = Tk, mfrom64 = 0x7fffffff;
-  if (MASK == CATOPT_MASK_CAUSAL) {
-    const int64_t lim = (int64_t)q0 + QT64 + causal_off;
-    kv_end = lim < 0 ? 0 : (lim < Tk ? lim : Tk);
-    const int64_t wl = (int64_t)qw0 + 64 + causal_off;
-    wave_end = wl < 0 ? 0 : (wl < Tk ? wl : Tk);
-    const int64_t x = (int64_t)qw0 + causal_off - 63;  // first tile t with 64 t > x
-    const int64_t fl = x >= 0 ? x / 64 : -((-x + 63) / 64);
-    mfrom64 = fl + 1 < 0 ? 0 : fl + 1;
-  }
-  const int nkv = (int)((kv_end + 63) / 64);
-  const int wnt = qw0 < Tq ? (int)((wave_end + 63) / 64) : 0;
-  const int mfrom = (int)(mfrom64 < nkv ? mfrom64 : nkv);
-  int64_t l0 = (int64_t)qw0 + causal_off;  // (keys and queries stay below 2^31)
-  l0 = l0 < -(1LL << 30) ? -(1LL << 30) : (l0 > (1LL << 30) ? (1LL << 30) : l0);
-  const int lim0 = (int)l0 + l32 - 4 * g;
-
-  // LDS fragment addresses of stage 0 (stage 1 adds 32 KB in the immediate,
-  // stage 2 reads through the second set, 64 KB further): K rows swizzled as
-  // tile_off<128>, Vᵀ by the transposing-read swizzle vtile_off<128>
   const uint32_t lb = lds_u32(lds);
-  uint32_t ka[8], kah[8], va[4], vah[4], ko[4], vo[4];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    ka[j] = lb + tile_off<128>(l32, 2 * j + g);
-    kah[j] = ka[j] + 65536;
-  }
-#pragma unroll
-  for (int db = 0; db < 4; ++db) {
-    const int key0 = 4 * (G >> 1) + (jj >> 2);
-    const int d = 32 * db + 16 * (G & 1) + 4 * (jj & 3);
-    va[db] = lb + AttnLds<128>::TILE_BYTES + vtile_off<128>(key0, d >> 3) + (d & 7) * 2;
-    vah[db] = va[db] + 65536;
-  }
-  // this thread's four 16-byte slots of a K and of a V tile (byte offsets
-  // from the tile's first row; the tile's offset goes in soffset)
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int s = i * NT + wave * 64 + lane;
-    const int row = s / AttnLds<128>::CH, cp = s % AttnLds<128>::CH;
-    ko[i] = (uint32_t)(row * (int)kst + (cp ^ (row & 15)) * 8) * 2u;
-    vo[i] = (uint32_t)(row * (int)vst + (cp ^ vswz<128>(row)) * 8) * 2u;
-  }
-  uint64_t qa[2];
-#pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    int row = qw0 + 32 * qb + l32;
-    row = row < Tq ? row : Tq - 1;  // rows past Tq load a valid row; their outputs are dropped
-    qa[qb] = reinterpret_cast<uint64_t>(q + (int64_t)row * qst) + 16 * g;
-  }
   const u32x4 krs = make_rsrc(k, (uint32_t)(((int64_t)(Tk - 1) * kst + 128) * 2));
   const u32x4 vrs = make_rsrc(v, (uint32_t)(((int64_t)(Tk - 1) * vst + 128) * 2));
   const uint32_t kstep = __builtin_amdgcn_readfirstlane((uint32_t)(64 * kst * 2));
   const uint32_t vstep = __builtin_amdgcn_readfirstlane((uint32_t)(64 * vst * 2));
   const uint32_t dmab = __builtin_amdgcn_readfirstlane(lb + wave * 1024);
-  const uint32_t ob = lb + wave * 32768 + lane * 16;
-  const int s_nkv = __builtin_amdgcn_readfirstlane(nkv);
-  const int s_wnt = __builtin_amdgcn_readfirstlane(wnt);
-  const int s_mfrom = __builtin_amdgcn_readfirstlane(mfrom);
   const float s_c = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, c)));
 
-  float m_run[2], m_true[2], l_run[2];
-  int st_t, st_kv0, st_kso, st_vso, st_tmp, st_fl0, st_fl1;
-  asm volatile(ATTN_Q64_ASM
-               : [mr0] "=&v"(m_run[0]), [mr1] "=&v"(m_run[1]), [mt0] "=&v"(m_true[0]),
-                 [mt1] "=&v"(m_true[1]), [lr0] "=&v"(l_run[0]), [lr1] "=&v"(l_run[1]),
-                 [t] "=&s"(st_t), [kv0] "=&s"(st_kv0), [kso] "=&s"(st_kso), [vso] "=&s"(st_vso),
-                 [tmp] "=&s"(st_tmp), [fl0] "=&s"(st_fl0), [fl1] "=&s"(st_fl1)
-               : [nkv] "s"(s_nkv), [wnt] "s"(s_wnt), [mfrom] "s"(s_mfrom), [krs] "s"(krs), [vrs] "s"(vrs),
-                 [kstep] "s"(kstep), [vstep] "s"(vstep), [dmab] "s"(dmab), [c] "s"(s_c), [lim0] "v"(lim0),
-                 [ka0] "v"(ka[0]), [ka1] "v"(ka[1]), [ka2] "v"(ka[2]), [ka3] "v"(ka[3]), [ka4] "v"(ka[4]),
-                 [ka5] "v"(ka[5]), [ka6] "v"(ka[6]), [ka7] "v"(ka[7]), [kah0] "v"(kah[0]), [kah1] "v"(kah[1]),
-                 [kah2] "v"(kah[2]), [kah3] "v"(kah[3]), [kah4] "v"(kah[4]), [kah5] "v"(kah[5]),
-                 [kah6] "v"(kah[6]), [kah7] "v"(kah[7]), [va0] "v"(va[0]), [va1] "v"(va[1]), [va2] "v"(va[2]),
-                 [va3] "v"(va[3]), [vah0] "v"(vah[0]), [vah1] "v"(vah[1]), [vah2] "v"(vah[2]),
-                 [vah3] "v"(vah[3]), [ko0] "v"(ko[0]), [ko1] "v"(ko[1]), [ko2] "v"(ko[2]), [ko3] "v"(ko[3]),
-                 [vo0] "v"(vo[0]), [vo1] "v"(vo[1]), [vo2] "v"(vo[2]), [vo3] "v"(vo[3]), [qa0] "v"(qa[0]),
-                 [qa1] "v"(qa[1]), [ob] "v"(ob)
-               : "memory", "m0", "vcc", "scc", ATTN_Q64_CLOBBERS);
+#pragma unroll 1
+  for (int pt = 0; pt < ntile; ++pt) {
+    const int qt = pt == 0 ? qt_first : nqt - 1 - qt_first;
+    const int q0 = qt * QT64;
+    const int qw0 = q0 + wave * 64;  // first query of this wave
 
-  // ---- epilogue (as attn_fwd_kernel's): O from LDS, back to the true max,
-  // normalise, store
+    // tiles of the workgroup (nkv), of this wave (wnt: a wave past Tq
+    // computes none) and the first one reaching past the wave's first query
+    // (mfrom: from there on the causal mask applies)
+    int64_t kv_end = Tk, wave_end = Tk, mfrom64 = 0x7fffffff;
+    if (MASK == CATOPT_MASK_CAUSAL) {
+      const int64_t lim = (int64_t)q0 + QT64 + causal_off;
+      kv_end = lim < 0 ? 0 : (lim < Tk ? lim : Tk);
+      const int64_t wl_end = (int64_t)qw0 + 64 + causal_off;
+      wave_end = wl_end < 0 ? 0 : (wl_end < Tk ? wl_end : Tk);
+      const int64_t x = (int64_t)qw0 + causal_off - 63;  // first tile t with 64 t > x
+      const int64_t fl = x >= 0 ? x / 64 : -((-x + 63) / 64);
+      mfrom64 = fl + 1 < 0 ? 0 : fl + 1;
+    }
+    const int nkv = (int)((kv_end + 63) / 64);
+    const int wnt = qw0 < Tq ? (int)((wave_end + 63) / 64) : 0;
+    const int mfrom = (int)(mfrom64 < nkv ? mfrom64 : nkv);
+    int64_t l0 = (int64_t)qw0 + causal_off;  // (keys and queries stay below 2^31)
+    l0 = l0 < -(1LL << 30) ? -(1LL << 30) : (l0 > (1LL << 30) ? (1LL << 30) : l0);
+    const int lim0 = (int)l0 + l32 - 4 * g;
+    uint64_t qa[2];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const int qrow = qw0 + 32 * qb + l32;
-    float fix = 1.f;
-    if (m_true[qb] != -__builtin_inff() && m_run[qb] != -__builtin_inff())
-      fix = __builtin_amdgcn_exp2f((m_run[qb] - m_true[qb]) * c);
-    const float l_sum = l_run[qb] + __shfl_xor(l_run[qb], 32, 64);
-    const float l_tot = l_sum * fix;
-    if (qrow >= Tq) continue;
-    const float inv = normalize ? 1.0f / l_sum : fix;
-    const bool empty_row = normalize && l_sum == 0.f;
-    const float fill = normalize == 2 ? 0.f : __builtin_nanf("");
-    uint16_t* orow = o + (int64_t)qrow * ost;
+    for (int qb = 0; qb < 2; ++qb) {
+      int row = qw0 + 32 * qb + l32;
+      row = row < Tq ? row : Tq - 1;  // rows past Tq load a valid row; their outputs are dropped
+      qa[qb] = reinterpret_cast<uint64_t>(q + (int64_t)row * qst) + 16 * g;
+    }
+    // LDS fragment addresses of stage 0 (stage 1 adds 32 KB in the immediate,
+    // stage 2 reads through the second set, 64 KB further): K rows swizzled as
+    // tile_off<128>, Vᵀ by the transposing-read swizzle vtile_off<128>.  They
+    // are recomputed per tile from a lane index the compiler cannot hoist, so
+    // that only scalars stay live across the asm block (hoisted, they spilled).
+    int lt = lane;
+    asm volatile("" : "+v"(lt));
+    const int l32t = lt & 31, gt = lt >> 5, Gt = lt >> 4, jjt = lt & 15;
+    uint32_t ka[8], kah[8], va[4], vah[4], ko[4], vo[4];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      ka[j] = lb + tile_off<128>(l32t, 2 * j + gt);
+      kah[j] = ka[j] + 65536;
+    }
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
+      const int key0 = 4 * (Gt >> 1) + (jjt >> 2);
+      const int d = 32 * db + 16 * (Gt & 1) + 4 * (jjt & 3);
+      va[db] = lb + AttnLds<128>::TILE_BYTES + vtile_off<128>(key0, d >> 3) + (d & 7) * 2;
+      vah[db] = va[db] + 65536;
+    }
+    // this thread's four 16-byte slots of a K and of a V tile (byte offsets
+    // from the tile's first row; the tile's offset goes in soffset)
 #pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        const f32x4 x = *reinterpret_cast<const f32x4*>(lds + wave * 32768 + lane * 16 +
-                                                        ((qb * 4 + db) * 4 + rg) * 1024);
-        const int d = 32 * db + 8 * rg + 4 * g;
-        float x0 = x[0] * inv, x1 = x[1] * inv, x2 = x[2] * inv, x3 = x[3] * inv;
-        if (empty_row) x0 = x1 = x2 = x3 = fill;
-        *reinterpret_cast<u32x2*>(orow + d) = u32x2{pack_bf16x2(x0, x1), pack_bf16x2(x2, x3)};
+    for (int i = 0; i < 4; ++i) {
+      const int s = i * NT + wave * 64 + lt;
+      const int row = s / AttnLds<128>::CH, cp = s % AttnLds<128>::CH;
+      ko[i] = (uint32_t)(row * (int)kst + (cp ^ (row & 15)) * 8) * 2u;
+      vo[i] = (uint32_t)(row * (int)vst + (cp ^ vswz<128>(row)) * 8) * 2u;
+    }
+    const uint32_t ob = lb + wave * 32768 + lt * 16;
+    const int s_nkv = __builtin_amdgcn_readfirstlane(nkv);
+    const int s_wnt = __builtin_amdgcn_readfirstlane(wnt);
+    const int s_mfrom = __builtin_amdgcn_readfirstlane(mfrom);
+
+    float m_run[2], m_true[2], l_run[2];
+    int st_t, st_kv0, st_kso, st_vso, st_tmp, st_fl0, st_fl1;
+    asm volatile(ATTN_Q64_ASM
+                 : [mr0] "=&v"(m_run[0]), [mr1] "=&v"(m_run[1]), [mt0] "=&v"(m_true[0]),
+                   [mt1] "=&v"(m_true[1]), [lr0] "=&v"(l_run[0]), [lr1] "=&v"(l_run[1]),
+                   [t] "=&s"(st_t), [kv0] "=&s"(st_kv0), [kso] "=&s"(st_kso), [vso] "=&s"(st_vso),
+                   [tmp] "=&s"(st_tmp), [fl0] "=&s"(st_fl0), [fl1] "=&s"(st_fl1)
+                 : [nkv] "s"(s_nkv), [wnt] "s"(s_wnt), [mfrom] "s"(s_mfrom), [krs] "s"(krs), [vrs] "s"(vrs),
+                   [kstep] "s"(kstep), [vstep] "s"(vstep), [dmab] "s"(dmab), [c] "s"(s_c), [lim0] "v"(lim0),
+                   [ka0] "v"(ka[0]), [ka1] "v"(ka[1]), [ka2] "v"(ka[2]), [ka3] "v"(ka[3]), [ka4] "v"(ka[4]),
+                   [ka5] "v"(ka[5]), [ka6] "v"(ka[6]), [ka7] "v"(ka[7]), [kah0] "v"(kah[0]), [kah1] "v"(kah[1]),
+                   [kah2] "v"(kah[2]), [kah3] "v"(kah[3]), [kah4] "v"(kah[4]), [kah5] "v"(kah[5]),
+                   [kah6] "v"(kah[6]), [kah7] "v"(kah[7]), [va0] "v"(va[0]), [va1] "v"(va[1]), [va2] "v"(va[2]),
+                   [va3] "v"(va[3]), [vah0] "v"(vah[0]), [vah1] "v"(vah[1]), [vah2] "v"(vah[2]),
+                   [vah3] "v"(vah[3]), [ko0] "v"(ko[0]), [ko1] "v"(ko[1]), [ko2] "v"(ko[2]), [ko3] "v"(ko[3]),
+                   [vo0] "v"(vo[0]), [vo1] "v"(vo[1]), [vo2] "v"(vo[2]), [vo3] "v"(vo[3]), [qa0] "v"(qa[0]),
+                   [qa1] "v"(qa[1]), [ob] "v"(ob)
+                 : "memory", "m0", "vcc", "scc", ATTN_Q64_CLOBBERS);
+
+    // ---- epilogue (as attn_fwd_kernel's): O from LDS (all 32 reads in
+    // flight at once), back to the true max, normalise; the bf16 rows go back
+    // into the wave's own LDS region (row r at 256 r, its 16-byte chunk c in
+    // slot c ^ (r % 16), so that neither the scattered writes nor the row
+    // reads collide in a bank) and leave as whole 256-byte rows, four rows
+    // per store instruction.  A lane holds query row 32 qb + l32, dims
+    // 32 db + 8 rg + 4 g .. +3 of (qb, db, rg).
+    char* wl = lds + wave * 32768;
+    int le = lane;  // opaque again: the epilogue's addresses stay in the loop too
+    asm volatile("" : "+v"(le));
+    const int l32e = le & 31, ge = le >> 5;
+    f32x4 ox[2][4][4];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg)
+          ox[qb][db][rg] = *reinterpret_cast<const f32x4*>(wl + le * 16 + ((qb * 4 + db) * 4 + rg) * 1024);
+    u32x2 ov[2][4][4];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const int qrow = qw0 + 32 * qb + l32e;
+      float fix = 1.f;
+      if (m_true[qb] != -__builtin_inff() && m_run[qb] != -__builtin_inff())
+        fix = __builtin_amdgcn_exp2f((m_run[qb] - m_true[qb]) * c);
+      const float l_sum = l_run[qb] + __shfl_xor(l_run[qb], 32, 64);
+      const float l_tot = l_sum * fix;
+      const float inv = normalize ? 1.0f / l_sum : fix;
+      const bool empty_row = normalize && l_sum == 0.f;
+      const float fill = normalize == 2 ? 0.f : __builtin_nanf("");
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          const f32x4 x = ox[qb][db][rg];
+          float x0 = x[0] * inv, x1 = x[1] * inv, x2 = x[2] * inv, x3 = x[3] * inv;
+          if (empty_row) x0 = x1 = x2 = x3 = fill;
+          ov[qb][db][rg] = u32x2{pack_bf16x2(x0, x1), pack_bf16x2(x2, x3)};
+        }
+      }
+      if (ge == 0 && qrow < Tq) {
+        const int64_t mi = (b * H + h) * (int64_t)Tq + qrow;
+        if (m_out) m_out[mi] = m_true[qb] * scale;  // natural-log units of the scaled score
+        if (l_out) l_out[mi] = l_tot;
       }
     }
-    if (g == 0) {
-      const int64_t mi = (b * H + h) * (int64_t)Tq + qrow;
-      if (m_out) m_out[mi] = m_true[qb] * scale;  // natural-log units of the scaled score
-      if (l_out) l_out[mi] = l_tot;
+    // every lane's fp32 reads have returned before any bf16 row overwrites them
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          const int r = 32 * qb + l32e, ch = 4 * db + rg;
+          *reinterpret_cast<u32x2*>(wl + r * 256 + ((ch ^ (r & 15)) << 4) + 8 * ge) = ov[qb][db][rg];
+        }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const int ch = le & 15;
+    u32x4 rows[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int r = 4 * j + (le >> 4);
+      rows[j] = *reinterpret_cast<const u32x4*>(wl + r * 256 + ((ch ^ (r & 15)) << 4));
     }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int r = 4 * j + (le >> 4);
+      if (qw0 + r < Tq) *reinterpret_cast<u32x4*>(o + (int64_t)(qw0 + r) * ost + 8 * ch) = rows[j];
+    }
+    // the next tile's loads go into LDS that every wave has read out
+    if (pt + 1 < ntile) __syncthreads();
   }
 }
 
@@ -632,11 +713,14 @@ int32_t attn_q64_launch(const uint16_t* q, const int64_t* qs, const uint16_t* k,
     if (e != hipSuccess) return set_hip_error(e);
     attr_done = true;
   }
-  const int64_t nblk = (Tq + QT64 - 1) / QT64 * H * B;
+  const int64_t nqt = (Tq + QT64 - 1) / QT64;
+  // an even number of query tiles goes two to a workgroup
+  const int paired = nqt % 2 == 0 ? 1 : 0;
+  const int64_t nblk = (paired ? nqt / 2 : nqt) * H * B;
   if (nblk > 0x7fffffffLL) return CATOPT_E_UNSUPPORTED;
   attn_q64_kernel<MASK><<<dim3((uint32_t)nblk), dim3(NT), LDS64, s>>>(
       q, qs[0], qs[1], qs[2], k, ks[0], ks[1], ks[2], v, vs[0], vs[1], vs[2], o, os[0], os[1], os[2], m_out,
-      l_out, (int)H, (int)Tq, (int)Tk, scale, causal_off, normalize);
+      l_out, (int)H, (int)Tq, (int)Tk, scale, causal_off, normalize, paired);
   CATOPT_LAUNCH_CHECK();
   return CATOPT_OK;
 }

@@ -231,11 +231,12 @@ def test_attention_causal_offset_and_cross_lengths(dev):
 # whole 64-key tiles; these cases reach its edges: query counts off a
 # multiple of the 256-query workgroup and of a wave's 64, keys of one and of
 # many tiles, causal offsets that start, end or empty rows, several heads per
-# XCD and a head count off a multiple of 8 (the two grid mappings).
+# XCD and a head count off a multiple of 8 (the grid mappings), and odd and
+# even query-tile counts (even counts run two tiles per workgroup).
 @pytest.mark.parametrize("B,H,Tq,Tk,causal,off", [
     (1, 2, 256, 256, True, 0), (2, 3, 100, 320, True, 220), (1, 16, 300, 512, True, 0),
     (1, 2, 200, 64, False, 0), (1, 4, 512, 512, True, -130), (1, 2, 64, 1024, True, 960),
-    (2, 8, 320, 384, False, 0), (1, 1, 1000, 1024, True, 24),
+    (2, 8, 320, 384, False, 0), (1, 1, 1000, 1024, True, 24), (1, 4, 1024, 1024, True, 0),
 ])
 def test_attention_q64_tiles(dev, B, H, Tq, Tk, causal, off):
     q, k, v = _qkv(B, H, Tq, 128, 300 + Tq + Tk, Tk=Tk)
