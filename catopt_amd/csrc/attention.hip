@@ -465,8 +465,9 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
 }
 
 // ------------------------------------------------ 64 queries per wave (D = 128)
-// One workgroup = 4 waves = 256 queries of one (b, h), 64 per wave, one wave
-// per SIMD (512 registers: the O accumulators, Q and K fragments in AGPRs).
+// One workgroup = 4 waves over a query tile of 256 queries of one (b, h) (or
+// two such tiles in turn), 64 per wave, one wave per SIMD (512 registers: the
+// O accumulators, Q and K fragments in AGPRs).
 // Every K / Vᵀ fragment a wave reads from LDS feeds two MFMAs, half the LDS
 // bytes per MFMA of the 32-query kernel above.  The tile loop is the inline
 // asm of attn_q64_loop.inc (generated by gen_attn_q64.py, which documents
@@ -474,15 +475,16 @@ __global__ __launch_bounds__(NT, QB == 1 ? 2 : 1) void attn_fwd_kernel(
 // ring and the waits); this C++ computes its addresses and bounds and does
 // the epilogue.  Keys come in whole 64-key tiles (Tk a multiple of 64, no
 // key mask): causal and unmasked leaves only.
-constexpr int QT64 = 256;                // queries per workgroup
+constexpr int QT64 = 256;                // queries per query tile (a workgroup takes one or two)
 constexpr int LDS64 = 128 * 1024;        // three 32 KB tile stages; O staged through it after the loop
 
 // Workgroups that take two query tiles of one (b, h), tiles p and nqt - 1 - p
 // (nqt even): every causal pair then holds the same number of key tiles, so
 // the grid stays balanced without a longest-first order, and a CU starts half
-// as many workgroups (each start costs a dispatch gap, and the first tile's
-// prologue waits out the memory latency alone).  Each XCD owns a contiguous
-// range of heads and takes them in order, pairs of a head together.
+// as many workgroups (each start costs a dispatch gap of its own, and the
+// second tile's loads start while the first tile's stores drain).  Each XCD
+// owns a contiguous range of heads and takes them in order, pairs of a head
+// together.
 __device__ __forceinline__ void pair_of_block(int npair, int& bh, int& p) {
   const int nblk = gridDim.x, nbh = nblk / npair;
   int w = blockIdx.x;
