@@ -274,10 +274,12 @@ def test_attention_q64_strided_and_zero_rows(dev):
     assert bool((o[:, :, :40] == 0).all())
 
 
-def test_attention_q64_unnormalised_numerator(dev):
-    q, k, v = _qkv(1, 2, 192, 128, 450, Tk=256)
-    a, m, lsum = K.attention(q.to(dev), k.to(dev), v.to(dev), 0.1, causal=False, normalize=False, return_ml=True)
-    out, mr, lr = oracle.attention_om(_np(q), _np(k), _np(v), 0.1, causal=False, return_ml=True)
+# one query tile per workgroup (192 queries) and two (448: the paired path)
+@pytest.mark.parametrize("Tq,Tk,causal", [(192, 256, False), (448, 512, True)])
+def test_attention_q64_unnormalised_numerator(dev, Tq, Tk, causal):
+    q, k, v = _qkv(1, 2, Tq, 128, 450, Tk=Tk)
+    a, m, lsum = K.attention(q.to(dev), k.to(dev), v.to(dev), 0.1, causal=causal, normalize=False, return_ml=True)
+    out, mr, lr = oracle.attention_om(_np(q), _np(k), _np(v), 0.1, causal=causal, return_ml=True)
     _gate(mr, m, 1e-5)
     _gate(lr, lsum, TOL_BF16)
     _gate(out * lr, a, TOL_BF16)
