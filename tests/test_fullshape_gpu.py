@@ -141,11 +141,15 @@ def test_linear_persistent_rounds_ragged(dev, epi):
 # ------------------------------------------------------- attention grid
 
 
+# Grids that are multiples of 8 workgroups, so the XCD remaps and (causal)
+# the tile orders run: d = 128, T = 256 is the 64-query kernel with one
+# query tile per workgroup (8 workgroups), T = 512 the same kernel with the
+# two tiles of a head's pair per workgroup (8 workgroups, 8 heads: one per
+# XCD), and d = 64 the 32-query kernel (B·H·⌈T/128⌉ = 16 workgroups).
+@pytest.mark.parametrize("T,d", [(256, 128), (512, 128), (256, 64)])
 @pytest.mark.parametrize("causal", [True, False])
-def test_attention_remapped_grid(dev, causal):
-    # B·H·⌈T/128⌉ = 1·8·2 = 16 workgroups: a multiple of 8, so the XCD remap
-    # and (causal) the longest-tile-first order both run
-    B, H, T, d = 1, 8, 256, 128
+def test_attention_remapped_grid(dev, causal, T, d):
+    B, H = 1, 8
     q = _rand((B, H, T, d), torch.bfloat16, 60)
     k = _rand((B, H, T, d), torch.bfloat16, 61)
     v = _rand((B, H, T, d), torch.bfloat16, 62)
